@@ -1,0 +1,246 @@
+"""Decode throughput of the MI355X token loop (BASELINE.json's metric).
+
+Workload ("config 2"): Llama-3.2-1B architecture,
+seeded random-init bf16 weights (synthetic: there is no checkpoint and no
+network), batch 1, contiguous KV cache of 2048 positions, a seeded 128-token
+prompt prefilled, then greedy decoding. One step = one decoded token: the
+whole hipGraph-captured decode step (16 layers x 5 fused kernels, lm_head with
+fp32 logits, argmax) feeding its argmax to the next step on the device. W
+warmup steps run first (they also capture the graphs), then exactly K steps
+are timed between device synchronizations with hipEvents on the model's
+stream. value = K / seconds.
+
+Bytes per token follow the reference's accounting (src/model.cu:86-102,
+src/main.cu:195-220): 2,471,628,800 weight bytes + 32,768 bytes of KV per
+position at the mean context length prompt + (K+1)/2.
+
+The JSON line also carries:
+  roofline      the dominant kernel (gate_up, 43% of the weight bytes): its
+                algorithmic bytes per launch / its mean launch time, timed live
+                here with a hipEvent pair around each launch on the model's
+                stream, against the 8 TB/s HBM peak; traffic from rocprofv3
+                counters when profiles/ holds them, else null;
+  cpu_baseline  the CPU oracle (oracle/, the restatement of the reference's
+                decode step) decoding a bounded sample of the same workload on
+                this box's host cores.
+
+Usage: python bench.py [--gpus 1] [--steps 255] [--warmup 16]
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0        # MI355X published HBM3E bandwidth
+BF16_DENSE_PEAK_TFLOPS = 2500.0
+REFERENCE_TOK_S = 322.3      # RTX 4090, docs/benchmarks.md:16
+REFERENCE_PEAK_FRAC = 0.791
+
+
+def load_package():
+    spec = importlib.util.spec_from_file_location("lcr_amd", REPO / "llama-cuda-runtime_amd" / "__init__.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["lcr_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def checkpoint_dir(lcr, config, seed) -> Path:
+    base = Path(os.environ.get("LCR_SYNTH_DIR", tempfile.gettempdir()))
+    d = base / f"lcr_synth_llama32_1b_bf16_{seed}"
+    st = d / "model.safetensors"
+    stamp = d / "STAMP"
+    want = json.dumps({"config": config, "seed": seed})
+    if not (st.exists() and stamp.exists() and stamp.read_text() == want):
+        lcr.write_synthetic_checkpoint(d, config, seed=seed)
+        stamp.write_text(want)
+    return d
+
+
+def traffic_from_profiles():
+    """HBM bytes per gate_up launch from the committed rocprofv3 counter
+    summary, when present."""
+    f = REPO / "profiles" / "gate_up_decode_counters.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get("traffic_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def cpu_baseline(model_dir: Path, steps: int):
+    sys.path.insert(0, str(REPO))
+    import oracle  # the checker, timed as the CPU baseline only
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    ref = oracle.OracleModel(model_dir, max_seq=64)
+    ref.decode(1)  # page the memory-mapped weights in
+    t0 = time.perf_counter()
+    for s in range(steps):
+        ref.decode(2 + s)
+    dt = time.perf_counter() - t0
+    ref.close()
+    return {
+        "value": steps / dt,
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} decode steps of the same 2.47 GB-per-token model at context 2..{steps + 1} "
+                  f"(CPU oracle, OpenMP over GEMV rows, {threads} threads), after one untimed step",
+        "ms_per_token": 1000.0 * dt / steps,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=255)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--max-seq", type=int, default=2048)
+    ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--kernel-launches", type=int, default=64)
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build measures the single-MI355X token loop "
+              f"(--gpus {args.gpus} is not supported; the multi-GPU design is described in DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    lcr = load_package()
+    if lcr.device_count() < 1:
+        print("no HIP device visible", file=sys.stderr)
+        return 1
+    config = lcr.llama_config()
+    seed = args.seed if args.seed is not None else lcr.WEIGHT_SEED
+    t0 = time.perf_counter()
+    model_dir = checkpoint_dir(lcr, config, seed)
+    gen_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    model = lcr.Model(model_dir, max_seq=args.max_seq)
+    load_s = time.perf_counter() - t0
+    st = model.stats()
+    assert st.fused == 1, "the benchmark measures the fused decode step"
+    prompt = lcr.synthetic_tokens(args.prompt, config["vocab_size"], seed=lcr.PROMPT_SEED)
+
+    # Warmup: prefill, W greedy steps (captures the decode graphs), reset.
+    first = model.sample(model.prefill(prompt), 0.0)
+    if args.warmup > 0:
+        model.generate_greedy(first, min(args.warmup, args.max_seq - args.prompt))
+    model.reset()
+
+    # Timed: prefill (reported separately), then exactly K decode steps.
+    logits = model.prefill(prompt)
+    prefill_ms = model.stats().last_prefill_ms
+    first = model.sample(logits, 0.0)
+    ids, decode_ms = model.generate_greedy(first, args.steps)
+    K = args.steps
+    ms_per_step = decode_ms / K
+    tok_s = K / (decode_ms / 1000.0)
+    mean_len = args.prompt + (K + 1) / 2.0
+    bytes_per_token = st.weight_bytes_per_token + mean_len * st.kv_bytes_per_position
+    achieved_gbs = bytes_per_token / (ms_per_step / 1000.0) / 1e9
+
+    # Reference-style loop: synchronous decode() calls from the host, one per
+    # token (src/main.cu:456-466 times decode() only).
+    model.reset()
+    model.prefill(prompt)
+    tok = first
+    host_steps = min(32, K)
+    t_host = 0.0
+    for _ in range(host_steps):
+        logits_ptr = model.decode(tok)
+        t_host += model.stats().last_decode_ms
+        tok = model.sample(logits_ptr, 0.0)
+    host_ms_per_token = t_host / host_steps
+
+    # Per-kernel timing (dominant kernel first), live, on the model's stream.
+    kernels = {}
+    for name in ("gate_up", "down", "lm_head", "qkv", "o_proj", "attention"):
+        ms, nbytes = model.time_decode_kernel(name, args.kernel_launches)
+        kernels[name] = {"avg_us": ms * 1000.0, "bytes_per_launch": nbytes,
+                         "gbs": nbytes / (ms / 1000.0) / 1e9}
+    dom = kernels["gate_up"]
+
+    # Prefill MFMA figures for the 128-token prompt.
+    H, F, V = config["hidden_size"], config["intermediate_size"], config["vocab_size"]
+    L = config["num_hidden_layers"]
+    qkv_n = (config["num_attention_heads"] + 2 * config["num_key_value_heads"]) * config["head_dim"]
+    T = args.prompt
+    lin_flops = 2.0 * T * (qkv_n * H + H * H + 2 * F * H + H * F) * L + 2.0 * V * H
+    attn_flops = 2.0 * 2.0 * config["num_attention_heads"] * config["head_dim"] * T * (T + 1) / 2.0 * L
+    prefill_tflops = (lin_flops + attn_flops) / (prefill_ms / 1000.0) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(model_dir, args.cpu_steps)
+    model.close()
+
+    result = {
+        "metric": "decode tok/s + HBM GB/s (% of peak), Llama-3.2-1B-arch bf16 batch 1",
+        "value": tok_s,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": tok_s / REFERENCE_TOK_S,
+        "vs_baseline_basis": "reference's published 322.3 tok/s (RTX 4090, real Llama-3.2-1B weights, "
+                             "docs/benchmarks.md:16); same metric and model architecture, other hardware",
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init N(0,0.02) bf16 weights, norms 1.0; seeded uniform prompt ids)",
+        "config": {
+            "workload": "config 2: 128-token prompt prefill + 255 greedy decode steps (256 generated tokens), "
+                        "batch 1, contiguous KV bf16 [16x2x8x2048x64], hipGraph-captured decode step",
+            "prompt_tokens": args.prompt,
+            "decode_steps": K,
+            "max_seq": args.max_seq,
+            "kv_layout": "contiguous",
+            "parallelism": "single GPU",
+        },
+        "decode_gbs": achieved_gbs,
+        "decode_frac_of_peak": achieved_gbs / HBM_PEAK_GBS,
+        "bytes_per_token": bytes_per_token,
+        "roofline_tok_s": HBM_PEAK_GBS * 1e9 / bytes_per_token,
+        "host_loop_ms_per_token": host_ms_per_token,
+        "prefill_ms": prefill_ms,
+        "prefill_tok_s": T / (prefill_ms / 1000.0),
+        "prefill_tflops": prefill_tflops,
+        "prefill_mfma_frac": prefill_tflops / BF16_DENSE_PEAK_TFLOPS,
+        "roofline": {
+            "kernel": "gate_up (fused RMSNorm + gate/up GEMV [16384x2048] + SwiGLU)",
+            "bound": "hbm",
+            "achieved": dom["gbs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": dom["gbs"] / HBM_PEAK_GBS,
+            "traffic": traffic_from_profiles(),
+            "avg_us": dom["avg_us"],
+            "bytes_per_launch": dom["bytes_per_launch"],
+        },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "generated_first_ids": [int(x) for x in ids[:8]],
+        "setup_s": {"checkpoint": gen_s, "load": load_s},
+        "reference_frac_of_peak": REFERENCE_PEAK_FRAC,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,83 @@
+// The 16-bit element type, chosen at build time, and its exact conversions.
+//
+// Like the reference's src/dtype.cuh:24-54, the whole pipeline stores one
+// 16-bit type: bf16 by default, fp16 when built with LCR_ELEM_FP16
+// (-DLCR_DTYPE=fp16 in the reference). Arithmetic is always fp32. The type is
+// a plain 16-bit word here, with conversions written out so host code, device
+// code and the CPU oracle agree bit for bit:
+//   bf16 -> f32   exact (the bits are the top half of the float)
+//   f32  -> bf16  round to nearest even; NaN stays a quiet NaN of the same sign
+//   fp16 <-> f32  IEEE conversions with round to nearest even
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.h"
+
+namespace lcr {
+
+struct alignas(2) elem_t {
+  uint16_t bits;
+};
+static_assert(sizeof(elem_t) == 2, "elem_t must be 16 bits");
+
+#if defined(LCR_ELEM_FP16)
+constexpr DType kElemDType = DType::kF16;
+constexpr const char* kElemName = "fp16";
+#else
+constexpr DType kElemDType = DType::kBF16;
+constexpr const char* kElemName = "bf16";
+#endif
+
+__host__ __device__ __forceinline__ float u32_as_f32(uint32_t u) {
+  return __builtin_bit_cast(float, u);
+}
+__host__ __device__ __forceinline__ uint32_t f32_as_u32(float f) {
+  return __builtin_bit_cast(uint32_t, f);
+}
+
+__host__ __device__ __forceinline__ float bf16_bits_to_float(uint32_t b) {
+  return u32_as_f32(b << 16);
+}
+
+__host__ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+  uint32_t u = f32_as_u32(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__host__ __device__ __forceinline__ float half_bits_to_float(uint32_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+
+__host__ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+#if defined(LCR_ELEM_FP16)
+__host__ __device__ __forceinline__ float elem_bits_to_float(uint32_t b) {
+  return half_bits_to_float(b & 0xffffu);
+}
+__host__ __device__ __forceinline__ uint16_t float_to_elem_bits(float f) {
+  return float_to_half_bits(f);
+}
+#else
+__host__ __device__ __forceinline__ float elem_bits_to_float(uint32_t b) {
+  return bf16_bits_to_float(b & 0xffffu);
+}
+__host__ __device__ __forceinline__ uint16_t float_to_elem_bits(float f) {
+  return float_to_bf16_bits(f);
+}
+#endif
+
+__host__ __device__ __forceinline__ float elem_to_float(elem_t x) {
+  return elem_bits_to_float(x.bits);
+}
+__host__ __device__ __forceinline__ elem_t float_to_elem(float v) {
+  return elem_t{float_to_elem_bits(v)};
+}
+
+}  // namespace lcr

@@ -1,0 +1,93 @@
+// The fused decode step: five kernels per layer plus the output head, every
+// one reading the position and token id from device memory so the whole step
+// can be captured once in a hipGraph and replayed.
+//
+// The arithmetic is exactly that of the reference's unfused sequence
+// (src/model.cu:370-484): every bf16 rounding point of the reference is kept
+// (qkv, q/k after RoPE, attention output, o_proj output, x after each residual
+// join, gate and up, the SwiGLU activation, down output), and every sum uses
+// the fixed orders of gemv_core.h, row_norm.h and attention_decode.h. What
+// fusion changes is only where intermediate values live:
+//  - the residual stream is kept as the unrounded fp32 sum v of each join
+//    (x = rne(v) is what the reference stores; the next RMSNorm needs the
+//    sum of v^2 over the unrounded v, src/kernels/rmsnorm.cu:86-101), so a
+//    GEMV epilogue can finish the join for its own rows and the next kernel's
+//    prologue can redo the norm from v;
+//  - RMSNorm runs as a prologue of the GEMV that consumes it, once per block,
+//    while the block's weight loads are already in flight;
+//  - RoPE and the KV append run in the QKV epilogue (a block owns rows i and
+//    i + head_dim/2 of a head), SwiGLU in the gate/up epilogue (a wave owns
+//    gate row i and up row i), the residual join in the o_proj and down
+//    epilogues;
+//  - the split-K merge runs in the last attention block of each kv head;
+//  - lm_head writes fp32 logits and per-block argmax partials.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../kv_cache.h"
+
+namespace lcr {
+
+struct LayerDevicePtrs {
+  const elem_t* input_norm;
+  const elem_t* qkv;       // [q_dim + 2 kv_dim][hidden]
+  const elem_t* o;         // [hidden][q_dim]
+  const elem_t* post_norm;
+  const elem_t* gate_up;   // [2 ffn][hidden]
+  const elem_t* down;      // [hidden][ffn]
+};
+
+struct DecodeStepArgs {
+  // model
+  int hidden, ffn, num_heads, num_kv_heads, head_dim, vocab;
+  float eps;
+  const elem_t* embedding;
+  const elem_t* final_norm;
+  const elem_t* lm_head;
+  const float* inv_freq;
+  // device state
+  const int32_t* token;      // [1] token id of this step
+  int32_t* position;         // [1] position of this step; incremented at the end
+  int32_t* sampled;          // [1] argmax of this step's logits
+  int32_t* next_token;       // [1] also receives the argmax (may alias token)
+  int32_t* history;          // [history_len] history[position + 1] = argmax
+  int history_len;
+  float* resid;              // [hidden] fp32 residual sum v
+  elem_t* q;                 // [num_heads * head_dim]
+  elem_t* attn;              // [num_heads * head_dim]
+  elem_t* act;               // [ffn]
+  float* logits;             // [vocab]
+  float* partials;           // attention split partials
+  unsigned* counters;        // [num_kv_heads] split arrival counters, zero between uses
+  unsigned long long* argmax_partials;  // [lm_head blocks]
+  bool paged;
+  int splits;
+};
+
+// True when the fused kernels are compiled for this geometry.
+bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads, int head_dim);
+
+// The five kernels of a layer, as bits of a selection mask.
+enum DecodeKernel : unsigned {
+  kDecodeQkv = 1u,
+  kDecodeAttention = 2u,
+  kDecodeOProj = 4u,
+  kDecodeGateUp = 8u,
+  kDecodeDown = 16u,
+  kDecodeAll = 31u,
+};
+
+// Enqueues one layer's kernels (qkv+rope+kv, attention, o_proj+residual,
+// gate_up+swiglu, down+residual); `mask` selects a subset (for timing one
+// kernel in isolation).
+void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
+                          const KvCacheView& view, int layer, hipStream_t stream,
+                          unsigned mask = kDecodeAll);
+// Enqueues the output head and the argmax (which also advances the position;
+// leave it out only to time the head alone).
+void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t stream, bool with_argmax = true);
+
+int lm_head_blocks(int vocab);
+
+}  // namespace lcr

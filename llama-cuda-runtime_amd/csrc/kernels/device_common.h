@@ -1,0 +1,155 @@
+// Device-side building blocks shared by every kernel: 16-byte vector access,
+// element unpacking, wavefront reductions, and the two transcendental
+// functions the token loop needs (exp and sincos).
+//
+// exp and sincos are written out as fixed sequences of IEEE operations rather
+// than taken from a math library, so the CPU oracle can evaluate the very same
+// sequence and agree with the GPU bit for bit. Every multiply-add that is meant
+// to be fused is an explicit fma; the sources are compiled with
+// -ffp-contract=off so nothing else is fused behind the code's back.
+//
+//   lcr_expf: Cody-Waite reduction x = k*ln2 + r with ln2 split in two parts
+//     (the high part has 15 significant bits, so k*ln2_hi is exact), then the
+//     degree-7 Taylor polynomial of exp(r) in Horner form, then ldexp by k.
+//     |r| <= ~0.35 keeps the truncation error near 5e-9 relative. Inputs below
+//     -87 return 0 (the result would be under FLT_MIN), above 88.72283 return
+//     +inf. NaN propagates.
+//   lcr_sincosf: the float angle is widened to double, reduced by k*pi/2 with
+//     fdlibm's two-part pi/2 (the 33-bit leading part makes k*pio2_1 exact for
+//     |k| < 2^20), sin and cos of the remainder come from their Maclaurin
+//     series to degree 17/18, the quadrant picks signs, and the results are
+//     rounded to float once.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "../dtype.h"
+
+namespace lcr {
+
+struct alignas(16) vec16 {
+  uint32_t w[4];
+};
+
+// Identity of the online-softmax accumulator (the reference's
+// src/kernels/reduce.cuh:15): finite, so two empty partials combine to zero
+// weight instead of NaN.
+constexpr float kSoftmaxIdentity = -FLT_MAX;
+
+__device__ __forceinline__ vec16 load16(const void* p) {
+  return *reinterpret_cast<const vec16*>(p);
+}
+__device__ __forceinline__ void store16(void* p, const vec16& v) {
+  *reinterpret_cast<vec16*>(p) = v;
+}
+
+// The two elements packed in one 32-bit word (element 2i in the low half).
+__device__ __forceinline__ float elem_lo(uint32_t p) {
+#if defined(LCR_ELEM_FP16)
+  return half_bits_to_float(p & 0xffffu);
+#else
+  return u32_as_f32(p << 16);
+#endif
+}
+__device__ __forceinline__ float elem_hi(uint32_t p) {
+#if defined(LCR_ELEM_FP16)
+  return half_bits_to_float(p >> 16);
+#else
+  return u32_as_f32(p & 0xffff0000u);
+#endif
+}
+__device__ __forceinline__ uint32_t pack_elems(float lo, float hi) {
+  return static_cast<uint32_t>(float_to_elem_bits(lo)) |
+         (static_cast<uint32_t>(float_to_elem_bits(hi)) << 16);
+}
+
+// Eight elements of a 16-byte chunk, widened to float, in memory order.
+__device__ __forceinline__ void unpack8(const vec16& v, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = elem_lo(v.w[i]);
+    out[2 * i + 1] = elem_hi(v.w[i]);
+  }
+}
+
+__host__ __device__ __forceinline__ float lcr_expf(float x) {
+  if (x != x) return x;
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.72283f) return __builtin_huge_valf();
+  const float k = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(k, -0.693145751953125f, x);
+  r = __builtin_fmaf(k, -1.428606765330187045e-06f, r);
+  float p = 1.98412698412698413e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, static_cast<int>(k));
+}
+
+__host__ __device__ __forceinline__ void lcr_sincosf(float angle, float* s_out, float* c_out) {
+  const double x = static_cast<double>(angle);
+  const double k = __builtin_rint(x * 6.36619772367581382433e-01);
+  double r = __builtin_fma(-k, 1.57079632673412561417e+00, x);
+  r = __builtin_fma(-k, 6.07710050650619224932e-11, r);
+  const double r2 = r * r;
+  double sp = 2.81145725434552076320e-15;
+  sp = __builtin_fma(sp, r2, -7.64716373181981647590e-13);
+  sp = __builtin_fma(sp, r2, 1.60590438368216145994e-10);
+  sp = __builtin_fma(sp, r2, -2.50521083854417187751e-08);
+  sp = __builtin_fma(sp, r2, 2.75573192239858906526e-06);
+  sp = __builtin_fma(sp, r2, -1.98412698412698412698e-04);
+  sp = __builtin_fma(sp, r2, 8.33333333333333333333e-03);
+  sp = __builtin_fma(sp, r2, -1.66666666666666666667e-01);
+  const double sin_r = __builtin_fma(r * r2, sp, r);
+  double cp = -1.56192069685862264622e-16;
+  cp = __builtin_fma(cp, r2, 4.77947733238738529744e-14);
+  cp = __builtin_fma(cp, r2, -1.14707455977297247139e-11);
+  cp = __builtin_fma(cp, r2, 2.08767569878680989792e-09);
+  cp = __builtin_fma(cp, r2, -2.75573192239858906526e-07);
+  cp = __builtin_fma(cp, r2, 2.48015873015873015873e-05);
+  cp = __builtin_fma(cp, r2, -1.38888888888888888889e-03);
+  cp = __builtin_fma(cp, r2, 4.16666666666666666667e-02);
+  cp = __builtin_fma(cp, r2, -0.5);
+  const double cos_r = __builtin_fma(r2, cp, 1.0);
+  const int quadrant = static_cast<int>(static_cast<long long>(k) & 3);
+  double s, c;
+  switch (quadrant) {
+    case 0: s = sin_r; c = cos_r; break;
+    case 1: s = cos_r; c = -sin_r; break;
+    case 2: s = -sin_r; c = -cos_r; break;
+    default: s = -cos_r; c = sin_r; break;
+  }
+  *s_out = static_cast<float>(s);
+  *c_out = static_cast<float>(c);
+}
+
+// Butterfly over the 64 lanes of a wavefront, offsets 32, 16, 8, 4, 2, 1.
+// Lane i adds lane i^o at each step; addition commutes, so every lane ends
+// with the same bits.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// The same butterfly restricted to aligned groups of 32 lanes (offsets 16..1).
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63u); }
+
+}  // namespace lcr

@@ -1,0 +1,405 @@
+// The fused decode step (see decode_step.h for what is fused and why the
+// results equal the unfused sequence bit for bit).
+#include <algorithm>
+#include <cmath>
+
+#include "../hip_utils.h"
+#include "attention_decode.h"
+#include "decode_step.h"
+#include "gemv_core.h"
+#include "row_norm.h"
+#include "sampling.h"
+
+namespace lcr {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kLmHeadMaxBlocks = 1024;
+constexpr int kLmHeadRows = 2;  // rows per wave per group
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + lcr_expf(-v)); }
+
+// RMSNorm of the residual sum v into LDS as elements:
+//   normed = rne((f(rne(v)) * scale) * f(w)),  scale from sum(v^2).
+// `load_chunk(c, out8)` yields the 8 floats of chunk c of v. Thread t handles
+// chunks t, t+256, ... as the fixed norm order requires.
+template <int NCH, typename LoadChunk>
+__device__ __forceinline__ void norm_into_lds(elem_t* xs, LoadChunk load_chunk,
+                                              const elem_t* __restrict__ w, float eps,
+                                              float* scratch) {
+  constexpr int H = NCH * 512;
+  constexpr int PER = NCH / 4;  // chunks per thread (H / 8 / 256)
+  const int t = threadIdx.x;
+  float v[PER][8];
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < PER; ++c) {
+    load_chunk(t + c * kThreads, v[c]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = __builtin_fmaf(v[c][j], v[c][j], s);
+  }
+  const float scale = norm_scale(block_norm_total(s, scratch), H, eps);
+#pragma unroll
+  for (int c = 0; c < PER; ++c) {
+    const int chunk = t + c * kThreads;
+    const vec16 wv = load16(w + 8 * chunk);
+    vec16 out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x0 = elem_to_float(float_to_elem(v[c][2 * i]));
+      const float x1 = elem_to_float(float_to_elem(v[c][2 * i + 1]));
+      out.w[i] = pack_elems((x0 * scale) * elem_lo(wv.w[i]), (x1 * scale) * elem_hi(wv.w[i]));
+    }
+    store16(xs + 8 * chunk, out);
+  }
+  __syncthreads();
+}
+
+template <int NCH>
+__device__ __forceinline__ void load_x_lds(vec16 (&xv)[NCH], const elem_t* xs, int lane) {
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) xv[c] = load16(xs + c * 512 + lane * kGemvChunk);
+}
+
+template <int NCH>
+__device__ __forceinline__ void load_x_global(vec16 (&xv)[NCH], const elem_t* x, int lane) {
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) xv[c] = load16(x + c * 512 + lane * kGemvChunk);
+}
+
+__device__ __forceinline__ void load_resid_chunk(const float* resid, int chunk, float* out) {
+  const float4 a = *reinterpret_cast<const float4*>(resid + 8 * chunk);
+  const float4 b = *reinterpret_cast<const float4*>(resid + 8 * chunk + 4);
+  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+
+// ---------------------------------------------------------------------------
+// 1. QKV projection + RoPE + KV append
+// ---------------------------------------------------------------------------
+
+template <int NCH, int HD, bool kPaged>
+__global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, LayerDevicePtrs w,
+                                                            KvCacheView view, int layer) {
+  constexpr int H = NCH * 512;
+  constexpr int HALF = HD / 2;
+  constexpr int BLOCKS_PER_HEAD = HALF / 4;
+  __shared__ __attribute__((aligned(16))) elem_t xs[H];
+  __shared__ float scratch[9];
+  __shared__ float rowv[8];
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int head = blockIdx.x / BLOCKS_PER_HEAD;
+  const int i0 = (blockIdx.x % BLOCKS_PER_HEAD) * 4;
+  const int r0 = i0 + (wave & 1) * 2 + ((wave >> 1) ? HALF : 0);  // row within the head
+
+  GemvTile<2, NCH> tile;
+  {
+    const elem_t* rows[2] = {w.qkv + static_cast<size_t>(head * HD + r0) * H,
+                             w.qkv + static_cast<size_t>(head * HD + r0 + 1) * H};
+    tile.load(rows, lane);
+  }
+
+  if (layer == 0) {
+    const elem_t* erow = a.embedding + static_cast<size_t>(*a.token) * H;
+    const bool keep = blockIdx.x == 0;
+    norm_into_lds<NCH>(xs, [&](int chunk, float* out) {
+      const vec16 e = load16(erow + 8 * chunk);
+      unpack8(e, out);
+      if (keep) {
+        *reinterpret_cast<float4*>(a.resid + 8 * chunk) = make_float4(out[0], out[1], out[2], out[3]);
+        *reinterpret_cast<float4*>(a.resid + 8 * chunk + 4) = make_float4(out[4], out[5], out[6], out[7]);
+      }
+    }, w.input_norm, a.eps, scratch);
+  } else {
+    norm_into_lds<NCH>(xs, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
+                       w.input_norm, a.eps, scratch);
+  }
+
+  vec16 xv[NCH];
+  load_x_lds<NCH>(xv, xs, lane);
+  float out[2];
+  tile.dot(out, xv);
+  if (lane == 0) {
+    rowv[wave * 2 + 0] = elem_to_float(float_to_elem(out[0]));
+    rowv[wave * 2 + 1] = elem_to_float(float_to_elem(out[1]));
+  }
+  __syncthreads();
+
+  if (threadIdx.x < 4) {
+    const int k = threadIdx.x;
+    const int i = i0 + k;
+    const float lo = rowv[k];
+    const float hi = rowv[4 + k];
+    const int pos = *a.position;
+    if (head < a.num_heads + a.num_kv_heads) {
+      float s, c;
+      lcr_sincosf(static_cast<float>(pos) * a.inv_freq[i], &s, &c);
+      const float ra = lo * c - hi * s;
+      const float rb = hi * c + lo * s;
+      if (head < a.num_heads) {
+        a.q[head * HD + i] = float_to_elem(ra);
+        a.q[head * HD + i + HALF] = float_to_elem(rb);
+      } else {
+        const size_t off = view.offset<kPaged>(head - a.num_heads, pos);
+        view.keys[off + i] = float_to_elem(ra);
+        view.keys[off + i + HALF] = float_to_elem(rb);
+      }
+    } else {
+      const size_t off = view.offset<kPaged>(head - a.num_heads - a.num_kv_heads, pos);
+      view.values[off + i] = float_to_elem(lo);
+      view.values[off + i + HALF] = float_to_elem(hi);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Attention (split-K; the last block of a kv head merges the splits)
+// ---------------------------------------------------------------------------
+
+template <bool kPaged, int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStepArgs a,
+                                                                      KvCacheView view,
+                                                                      float scale) {
+  __shared__ AttnShared<HD, G> sh;
+  __shared__ int is_last;
+  const int seq_len = *a.position + 1;
+  const int splits = min(a.splits, seq_len);
+  // A graph captured for more splits than this position can use: the extra
+  // blocks have no range and must not touch the partials of other heads.
+  if (blockIdx.y >= static_cast<unsigned>(splits)) return;
+  decode_attention_block<kPaged, HD, G>(sh, a.attn, a.partials, a.q, view, blockIdx.x, blockIdx.y,
+                                        splits, seq_len, scale);
+  if (splits <= 1) return;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = atomicAdd(&a.counters[blockIdx.x], 1u);
+    is_last = prev == static_cast<unsigned>(splits - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    merge_split_partials(a.attn, a.partials, blockIdx.x * G + g, splits, HD);
+  }
+  if (threadIdx.x == 0) a.counters[blockIdx.x] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// 3 / 5. Projection + residual join (o_proj, down)
+// ---------------------------------------------------------------------------
+
+template <int NCH>
+__global__ __launch_bounds__(kThreads) void proj_residual_kernel(DecodeStepArgs a,
+                                                                 const elem_t* __restrict__ W,
+                                                                 const elem_t* __restrict__ x) {
+  constexpr int K = NCH * 512;
+  const int lane = lane_id();
+  const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * 2;
+  GemvTile<2, NCH> tile;
+  const elem_t* rows[2] = {W + static_cast<size_t>(row0) * K, W + static_cast<size_t>(row0 + 1) * K};
+  tile.load(rows, lane);
+  vec16 xv[NCH];
+  load_x_global<NCH>(xv, x, lane);
+  float out[2];
+  tile.dot(out, xv);
+  if (lane < 2) {
+    const int row = row0 + lane;
+    const float proj = elem_to_float(float_to_elem(lane == 0 ? out[0] : out[1]));
+    const float xold = elem_to_float(float_to_elem(a.resid[row]));
+    a.resid[row] = xold + proj;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. gate/up projection + SwiGLU
+// ---------------------------------------------------------------------------
+
+template <int NCH>
+__global__ __launch_bounds__(kThreads) void gate_up_kernel(DecodeStepArgs a, LayerDevicePtrs w) {
+  constexpr int H = NCH * 512;
+  __shared__ __attribute__((aligned(16))) elem_t xs[H];
+  __shared__ float scratch[9];
+  const int lane = lane_id();
+  const int i = blockIdx.x * kWaves + (threadIdx.x >> 6);  // activation index of this wave
+  GemvTile<2, NCH> tile;
+  const elem_t* rows[2] = {w.gate_up + static_cast<size_t>(i) * H,
+                           w.gate_up + static_cast<size_t>(a.ffn + i) * H};
+  tile.load(rows, lane);
+  norm_into_lds<NCH>(xs, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
+                     w.post_norm, a.eps, scratch);
+  vec16 xv[NCH];
+  load_x_lds<NCH>(xv, xs, lane);
+  float out[2];
+  tile.dot(out, xv);
+  if (lane == 0) {
+    const float g = elem_to_float(float_to_elem(out[0]));
+    const float u = elem_to_float(float_to_elem(out[1]));
+    a.act[i] = float_to_elem(silu(g) * u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 6. Output head: final norm, fp32 logits, argmax partials
+// ---------------------------------------------------------------------------
+
+template <int NCH>
+__global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
+  constexpr int H = NCH * 512;
+  constexpr int GROUP_ROWS = kWaves * kLmHeadRows;
+  __shared__ __attribute__((aligned(16))) elem_t xs[H];
+  __shared__ float scratch[9];
+  __shared__ unsigned long long lds_best[16];
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int groups = (a.vocab + GROUP_ROWS - 1) / GROUP_ROWS;
+  const int stride = gridDim.x;
+
+  auto row_ptrs = [&](int g, const elem_t* (&rows)[kLmHeadRows]) {
+#pragma unroll
+    for (int r = 0; r < kLmHeadRows; ++r) {
+      const int row = min(g * GROUP_ROWS + wave * kLmHeadRows + r, a.vocab - 1);
+      rows[r] = a.lm_head + static_cast<size_t>(row) * H;
+    }
+  };
+
+  GemvTile<kLmHeadRows, NCH> t0, t1;
+  int g = blockIdx.x;
+  if (g < groups) {
+    const elem_t* rows[kLmHeadRows];
+    row_ptrs(g, rows);
+    t0.load(rows, lane);
+  }
+  norm_into_lds<NCH>(xs, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
+                     a.final_norm, a.eps, scratch);
+  vec16 xv[NCH];
+  load_x_lds<NCH>(xv, xs, lane);
+
+  unsigned long long best = 0;
+  auto finish = [&](const GemvTile<kLmHeadRows, NCH>& t, int grp) {
+    float out[kLmHeadRows];
+    t.dot(out, xv);
+#pragma unroll
+    for (int r = 0; r < kLmHeadRows; ++r) {
+      const int row = grp * GROUP_ROWS + wave * kLmHeadRows + r;
+      if (lane == r && row < a.vocab) {
+        a.logits[row] = out[r];
+        best = umax64(best, argmax_key(out[r], static_cast<uint32_t>(row)));
+      }
+    }
+  };
+
+  for (; g < groups; g += 2 * stride) {
+    const int g1 = g + stride;
+    if (g1 < groups) {
+      const elem_t* rows[kLmHeadRows];
+      row_ptrs(g1, rows);
+      t1.load(rows, lane);
+    }
+    finish(t0, g);
+    const int g2 = g + 2 * stride;
+    if (g2 < groups) {
+      const elem_t* rows[kLmHeadRows];
+      row_ptrs(g2, rows);
+      t0.load(rows, lane);
+    }
+    if (g1 < groups) finish(t1, g1);
+  }
+  best = block_max_u64(best, lds_best);
+  if (threadIdx.x == 0) a.argmax_partials[blockIdx.x] = best;
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_step_kernel(DecodeStepArgs a, int blocks) {
+  __shared__ unsigned long long lds_best[16];
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < blocks; i += kThreads) best = umax64(best, a.argmax_partials[i]);
+  best = block_max_u64(best, lds_best);
+  if (threadIdx.x == 0) {
+    const int32_t id = argmax_id(best);
+    const int pos = *a.position;
+    *a.sampled = id;
+    *a.next_token = id;
+    if (pos + 1 < a.history_len) a.history[pos + 1] = id;
+    *a.position = pos + 1;
+  }
+}
+
+template <int NCH, int NCH_F, int HD, bool kPaged, int G>
+void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, const KvCacheView& view,
+                         int layer, hipStream_t s, unsigned mask) {
+  if (mask & kDecodeQkv) {
+    const int qkv_rows = (a.num_heads + 2 * a.num_kv_heads) * HD;
+    qkv_rope_kernel<NCH, HD, kPaged><<<qkv_rows / 8, kThreads, 0, s>>>(a, w, view, layer);
+    HIP_CHECK_LAUNCH();
+  }
+  if (mask & kDecodeAttention) {
+    const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
+    attention_step_kernel<kPaged, HD, G>
+        <<<dim3(a.num_kv_heads, a.splits), kAttnThreads, 0, s>>>(a, view, scale);
+    HIP_CHECK_LAUNCH();
+  }
+  if (mask & kDecodeOProj) {
+    proj_residual_kernel<NCH><<<a.hidden / (2 * kWaves), kThreads, 0, s>>>(a, w.o, a.attn);
+    HIP_CHECK_LAUNCH();
+  }
+  if (mask & kDecodeGateUp) {
+    gate_up_kernel<NCH><<<a.ffn / kWaves, kThreads, 0, s>>>(a, w);
+    HIP_CHECK_LAUNCH();
+  }
+  if (mask & kDecodeDown) {
+    proj_residual_kernel<NCH_F><<<a.hidden / (2 * kWaves), kThreads, 0, s>>>(a, w.down, a.act);
+    HIP_CHECK_LAUNCH();
+  }
+}
+
+}  // namespace
+
+bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads, int head_dim) {
+  if (hidden != 2048 || ffn != 8192 || head_dim != 64) return false;
+  if (num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return false;
+  if (num_heads * head_dim != hidden) return false;  // o_proj input width == hidden
+  const int g = num_heads / num_kv_heads;
+  return g == 1 || g == 2 || g == 4 || g == 8;
+}
+
+int lm_head_blocks(int vocab) {
+  const int groups = (vocab + kWaves * kLmHeadRows - 1) / (kWaves * kLmHeadRows);
+  return std::max(1, std::min(groups, kLmHeadMaxBlocks));
+}
+
+void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
+                          const KvCacheView& view, int layer, hipStream_t s, unsigned mask) {
+  const int g = a.num_heads / a.num_kv_heads;
+#define LCR_LAYER_CASE(G_)                                                          \
+  case G_:                                                                          \
+    if (a.paged) {                                                                  \
+      enqueue_layer_typed<4, 16, 64, true, G_>(a, w, view, layer, s, mask);         \
+    } else {                                                                        \
+      enqueue_layer_typed<4, 16, 64, false, G_>(a, w, view, layer, s, mask);        \
+    }                                                                               \
+    return;
+  switch (g) {
+    LCR_LAYER_CASE(1)
+    LCR_LAYER_CASE(2)
+    LCR_LAYER_CASE(4)
+    LCR_LAYER_CASE(8)
+    default:
+      LCR_FAIL("fused decode step has no kernels for " << g << " query heads per kv head");
+  }
+#undef LCR_LAYER_CASE
+}
+
+void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t s, bool with_argmax) {
+  const int blocks = lm_head_blocks(a.vocab);
+  lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a);
+  HIP_CHECK_LAUNCH();
+  if (!with_argmax) return;
+  argmax_step_kernel<<<1, kThreads, 0, s>>>(a, blocks);
+  HIP_CHECK_LAUNCH();
+}
+
+}  // namespace lcr

@@ -1,0 +1,228 @@
+// lcr_sample: greedy argmax and temperature / top-k / top-p sampling. The
+// algorithm and its fixed orders are described in sampling.h.
+#include <algorithm>
+#include <climits>
+
+#include "../capi_util.h"
+#include "sampling.h"
+
+namespace lcr {
+namespace {
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
+    unsigned long long* __restrict__ block_best, const float* __restrict__ logits, int vocab) {
+  __shared__ unsigned long long lds[16];
+  const int stride = gridDim.x * kArgmaxThreads;
+  unsigned long long local = 0;
+  for (int i = blockIdx.x * kArgmaxThreads + threadIdx.x; i < vocab; i += stride) {
+    local = umax64(local, argmax_key(logits[i], static_cast<uint32_t>(i)));
+  }
+  local = block_max_u64(local, lds);
+  if (threadIdx.x == 0) block_best[blockIdx.x] = local;
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(
+    int32_t* __restrict__ out_id, const unsigned long long* __restrict__ block_best, int blocks) {
+  __shared__ unsigned long long lds[16];
+  unsigned long long local = 0;
+  for (int i = threadIdx.x; i < blocks; i += kArgmaxThreads) local = umax64(local, block_best[i]);
+  local = block_max_u64(local, lds);
+  if (threadIdx.x == 0) *out_id = argmax_id(local);
+}
+
+// Sum over the 1024 threads in the reference's block_reduce_sum order.
+__device__ __forceinline__ float block_sum_1024(float v, float* lds32) {
+  const int t = threadIdx.x;
+  v = half_wave_sum(v);
+  if ((t & 31) == 0) lds32[t >> 5] = v;
+  __syncthreads();
+  float total = 0.0f;
+  if (t < 32) total = half_wave_sum(lds32[t]);
+  __syncthreads();
+  if (t == 0) lds32[0] = total;
+  __syncthreads();
+  total = lds32[0];
+  __syncthreads();
+  return total;
+}
+
+__device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restrict__ out_id,
+                                                                const float* __restrict__ logits,
+                                                                int vocab, float inv_temperature,
+                                                                int top_k, float top_p,
+                                                                float uniform) {
+  __shared__ float lds32[32];
+  __shared__ unsigned long long lds_u64[16];
+  __shared__ int histogram[kHistogramBins];
+  __shared__ int counts[kSampleThreads];
+  __shared__ int shared_cutoff;
+  __shared__ float values[kMaxCandidates];
+  __shared__ int indices[kMaxCandidates];
+  const int t = threadIdx.x;
+
+  // 1. Maximum logit (exact in any order).
+  float local_max = -FLT_MAX;
+  for (int i = t; i < vocab; i += kSampleThreads) local_max = fmaxf(local_max, logits[i]);
+  {
+    // Reuse the u64 block max on the order key of the float (ties irrelevant).
+    unsigned long long key = static_cast<unsigned long long>(order_key(local_max)) << 32;
+    key = block_max_u64(key, lds_u64);
+    const uint32_t k = static_cast<uint32_t>(key >> 32);
+    local_max = u32_as_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+  }
+  const float max_logit = local_max;
+
+  // 2. Exponential sum over the whole vocabulary, and the histogram.
+  for (int b = t; b < kHistogramBins; b += kSampleThreads) histogram[b] = 0;
+  __syncthreads();
+  float local_sum = 0.0f;
+  for (int i = t; i < vocab; i += kSampleThreads) {
+    const float scaled = (logits[i] - max_logit) * inv_temperature;
+    local_sum += lcr_expf(scaled);
+    const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
+    if (bin >= 0) atomicAdd(&histogram[bin], 1);
+  }
+  const float total_sum = block_sum_1024(local_sum, lds32);
+
+  // 3. Cutoff bin.
+  if (t == 0) {
+    int running = 0;
+    int cutoff = 0;
+    for (int b = 0; b < kHistogramBins; ++b) {
+      if (running + histogram[b] > kMaxCandidates) break;
+      running += histogram[b];
+      cutoff = b + 1;
+    }
+    shared_cutoff = max(cutoff, 1);
+  }
+  __syncthreads();
+  const int cutoff_bin = shared_cutoff;
+
+  // 4. Ordered compaction: thread t scans the contiguous index range
+  // [t*per, (t+1)*per), counts, takes an exclusive prefix over threads, writes.
+  const int per = (vocab + kSampleThreads - 1) / kSampleThreads;
+  const int lo = min(vocab, t * per);
+  const int hi = min(vocab, lo + per);
+  auto is_candidate = [&](int i, float* scaled_out) {
+    const float scaled = (logits[i] - max_logit) * inv_temperature;
+    const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
+    *scaled_out = scaled;
+    return bin < cutoff_bin;
+  };
+  int mine = 0;
+  for (int i = lo; i < hi; ++i) {
+    float scaled;
+    if (is_candidate(i, &scaled)) ++mine;
+  }
+  counts[t] = mine;
+  __syncthreads();
+  // Inclusive scan (Hillis-Steele) over the 1024 counts.
+  for (int o = 1; o < kSampleThreads; o <<= 1) {
+    const int add = t >= o ? counts[t - o] : 0;
+    __syncthreads();
+    counts[t] += add;
+    __syncthreads();
+  }
+  const int total_found = counts[kSampleThreads - 1];
+  int slot = counts[t] - mine;
+  for (int i = lo; i < hi && slot < kMaxCandidates; ++i) {
+    float scaled;
+    if (is_candidate(i, &scaled)) {
+      values[slot] = scaled;
+      indices[slot] = i;
+      ++slot;
+    }
+  }
+  const int found = min(total_found, kMaxCandidates);
+  __syncthreads();
+  for (int i = t; i < kMaxCandidates; i += kSampleThreads) {
+    if (i >= found) {
+      values[i] = -FLT_MAX;
+      indices[i] = INT_MAX;
+    }
+  }
+  __syncthreads();
+
+  // 5. Bitonic sort into (value desc, index asc).
+  for (int span = 2; span <= kMaxCandidates; span <<= 1) {
+    for (int step = span >> 1; step > 0; step >>= 1) {
+      const int partner = t ^ step;
+      if (partner > t) {
+        const bool first_half = (t & span) == 0;
+        const bool partner_first = ranks_before(values[partner], indices[partner], values[t], indices[t]);
+        const bool swap = first_half ? partner_first : !partner_first;
+        if (swap) {
+          const float tv = values[t];
+          values[t] = values[partner];
+          values[partner] = tv;
+          const int ti = indices[t];
+          indices[t] = indices[partner];
+          indices[partner] = ti;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // 6. Walk.
+  if (t == 0) {
+    const int limit = top_k > 0 ? min(found, top_k) : found;
+    const float inv_total = 1.0f / total_sum;
+    int keep = 0;
+    float kept_mass = 0.0f;
+    for (int i = 0; i < limit; ++i) {
+      kept_mass = __builtin_fmaf(lcr_expf(values[i]), inv_total, kept_mass);
+      ++keep;
+      if (top_p < 1.0f && kept_mass >= top_p) break;
+    }
+    if (keep == 0) keep = 1;
+    const float target = uniform * kept_mass;
+    int picked = indices[0];
+    float running = 0.0f;
+    for (int i = 0; i < keep; ++i) {
+      running = __builtin_fmaf(lcr_expf(values[i]), inv_total, running);
+      picked = indices[i];
+      if (running >= target) break;
+    }
+    *out_id = picked;
+  }
+}
+
+}  // namespace
+}  // namespace lcr
+
+using namespace lcr;
+
+extern "C" size_t lcr_sample_scratch_floats(int vocab, int top_k) {
+  (void)vocab;
+  (void)top_k;
+  // One 64-bit partial maximum per argmax block.
+  return 2 * static_cast<size_t>(kArgmaxBlocks);
+}
+
+extern "C" int lcr_sample(int32_t* out_id, const float* logits, int vocab, float temperature,
+                          int top_k, float top_p, float uniform, float* scratch, void* stream) {
+  CAPI_CHECK(vocab > 0, "cannot sample from an empty vocabulary");
+  auto s = static_cast<hipStream_t>(stream);
+  if (temperature <= 0.0f) {
+    CAPI_CHECK(scratch != nullptr, "argmax needs scratch space for its partial maxima");
+    CAPI_CHECK((reinterpret_cast<uintptr_t>(scratch) & 7u) == 0,
+               "argmax scratch must be 8-byte aligned");
+    auto* best = reinterpret_cast<unsigned long long*>(scratch);
+    const int blocks = std::min(kArgmaxBlocks, (vocab + kArgmaxThreads - 1) / kArgmaxThreads);
+    argmax_partial_kernel<<<blocks, kArgmaxThreads, 0, s>>>(best, logits, vocab);
+    CAPI_LAUNCHED();
+    argmax_final_kernel<<<1, kArgmaxThreads, 0, s>>>(out_id, best, blocks);
+    CAPI_LAUNCHED();
+    return LCR_OK;
+  }
+  CAPI_CHECK(top_p > 0.0f && top_p <= 1.0f, "top_p must be in (0, 1], got " << top_p);
+  sample_kernel<<<1, kSampleThreads, 0, s>>>(out_id, logits, vocab, 1.0f / temperature, top_k,
+                                             top_p, uniform);
+  CAPI_LAUNCHED();
+  return LCR_OK;
+}

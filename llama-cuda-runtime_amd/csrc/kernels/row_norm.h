@@ -1,0 +1,66 @@
+// The row sum of squares behind every RMSNorm, in one fixed order.
+//
+// A 256-thread block reduces one row. Thread t squares-and-accumulates the
+// 8-element chunks t, t+256, t+512, ... (elements in order, s = fma(v, v, s)),
+// then the elements past the last whole chunk at positions t, t+256, ...; the
+// 256 partials are added by a butterfly inside each aligned group of 32 threads
+// (offsets 16..1), and the 8 group totals by the same 32-wide butterfly with
+// zeros in lanes 8..31. That is the shape of the reference's rmsnorm kernels
+// (src/kernels/rmsnorm.cu:32-47 with block_reduce_sum, reduce.cuh:23-37), so the
+// order is well defined and the CPU oracle reproduces it exactly.
+//
+// The scale is 1 / sqrt(total / dim + eps) with a correctly rounded divide and
+// square root, and each output is rne((x * scale) * w).
+#pragma once
+
+#include "device_common.h"
+
+namespace lcr {
+
+constexpr int kNormThreads = 256;
+
+// Adds the per-thread partial sums of a 256-thread block in the fixed tree.
+// Every thread must call it; every thread gets the total. `scratch` holds at
+// least 9 floats of LDS.
+__device__ __forceinline__ float block_norm_total(float s, float* scratch) {
+  const int t = static_cast<int>(threadIdx.x);
+  s = half_wave_sum(s);
+  if ((t & 31) == 0) scratch[t >> 5] = s;
+  __syncthreads();
+  if (t < 32) {
+    float v = (t < 8) ? scratch[t] : 0.0f;
+    v = half_wave_sum(v);
+    if (t == 0) scratch[8] = v;
+  }
+  __syncthreads();
+  const float total = scratch[8];
+  __syncthreads();
+  return total;
+}
+
+// `get(i)` returns element i of the row as float; every thread of a
+// 256-thread block must call this.
+template <typename Get>
+__device__ __forceinline__ float block_sum_squares(Get get, int dim, float* scratch) {
+  const int t = static_cast<int>(threadIdx.x);
+  float s = 0.0f;
+  const int chunks = dim / 8;
+  for (int c = t; c < chunks; c += kNormThreads) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = get(8 * c + j);
+      s = __builtin_fmaf(v, v, s);
+    }
+  }
+  for (int i = chunks * 8 + t; i < dim; i += kNormThreads) {
+    const float v = get(i);
+    s = __builtin_fmaf(v, v, s);
+  }
+  return block_norm_total(s, scratch);
+}
+
+__device__ __forceinline__ float norm_scale(float total, int dim, float eps) {
+  return 1.0f / __builtin_sqrtf(total / static_cast<float>(dim) + eps);
+}
+
+}  // namespace lcr

@@ -1,0 +1,640 @@
+#include "model.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <sstream>
+
+#include "hip_utils.h"
+#include "kernels.h"
+#include "kernels/fill.h"
+
+namespace lcr {
+namespace {
+
+// Largest split count attention ever uses, so its scratch is sized once
+// (the reference's src/model.cu:23).
+constexpr int kMaxAttentionSplits = 64;
+constexpr int kMaxLmHeadBlocks = 1024;
+
+}  // namespace
+
+Model::Model(const std::string& model_dir, const Options& options) : options_(options) {
+  HIP_CHECK(hipSetDevice(options.device));
+  const DeviceInfo device = query_device(options.device);
+  multiprocessors_ = device.multiprocessors;
+
+  config_ = ModelConfig::load(model_dir);
+  LCR_CHECK(options_.max_seq > 0, "max_seq must be positive");
+  LCR_CHECK(options_.prefill_chunk > 0, "prefill chunk must be positive");
+  max_tokens_ = std::min(options_.prefill_chunk, options_.max_seq);
+
+  HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+
+  {
+    const SafetensorsArchive archive(model_dir);
+    load_weights(archive);
+  }
+  kv_cache_ = std::make_unique<KvCache>(config_, options_.max_seq, options_.kv_layout,
+                                        options_.page_size);
+
+  const std::vector<float> inv_freq = compute_rope_inv_freq(config_);
+  HIP_CHECK(hipMalloc(&inv_freq_, inv_freq.size() * sizeof(float)));
+  HIP_CHECK(hipMemcpy(inv_freq_, inv_freq.data(), inv_freq.size() * sizeof(float),
+                      hipMemcpyHostToDevice));
+
+  allocate_arena();
+  HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&pinned_state_), 2 * sizeof(int32_t),
+                          hipHostMallocDefault));
+  pinned_state_[0] = 0;
+  pinned_state_[1] = 0;
+
+  fused_ = options_.fused_decode &&
+           decode_step_supported(config_.hidden_size, config_.intermediate_size,
+                                 config_.num_heads, config_.num_kv_heads, config_.head_dim) &&
+           config_.vocab_size > 0;
+
+  stats_.kv_bytes_per_position = config_.kv_bytes_per_token(sizeof(elem_t));
+  // Weight bytes streamed per decoded token, counted as the reference does
+  // (src/model.cu:86-102): every projection, both norms per layer, the final
+  // norm and the output head; one embedding row is not counted.
+  size_t per_token = 0;
+  for (int layer = 0; layer < config_.num_layers; ++layer) {
+    per_token += static_cast<size_t>(config_.hidden_size) * 2;
+    per_token += static_cast<size_t>(config_.q_dim()) * config_.hidden_size;
+    per_token += static_cast<size_t>(config_.kv_dim()) * config_.hidden_size * 2;
+    per_token += static_cast<size_t>(config_.hidden_size) * config_.q_dim();
+    per_token += static_cast<size_t>(config_.intermediate_size) * config_.hidden_size * 3;
+  }
+  per_token += config_.hidden_size;
+  per_token += static_cast<size_t>(config_.vocab_size) * config_.hidden_size;
+  stats_.weight_bytes_per_token = per_token * sizeof(elem_t);
+}
+
+Model::~Model() {
+  for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
+  graphs_.clear();
+  if (stream_ != nullptr) (void)hipStreamSynchronize(stream_);
+  if (pinned_state_ != nullptr) (void)hipHostFree(pinned_state_);
+  if (stream_ != nullptr) (void)hipStreamDestroy(stream_);
+  (void)hipFree(weight_block_);
+  (void)hipFree(inv_freq_);
+}
+
+// Layout and checks follow the reference's src/model.cu:112-213: one device
+// block in reading order, 256-byte aligned pieces, q/k/v and gate/up
+// concatenated by rows, tied output head = embedding.
+void Model::load_weights(const SafetensorsArchive& archive) {
+  layers_.assign(static_cast<size_t>(config_.num_layers), LayerWeights{});
+  struct Block {
+    const elem_t** destination;
+    std::vector<const TensorView*> pieces;
+    size_t bytes = 0;
+  };
+  std::vector<Block> blocks;
+  auto check = [&](const std::string& name, const std::vector<int64_t>& shape) {
+    const TensorView& t = archive.get(name);
+    LCR_CHECK(t.dtype == kElemDType,
+              "tensor \"" << name << "\" is " << dtype_name(t.dtype) << " but this build computes in "
+                          << kElemName << "; rebuild with -DLCR_DTYPE="
+                          << (kElemDType == DType::kBF16 ? "fp16" : "bf16"));
+    t.expect_shape(shape);
+    return &t;
+  };
+  auto add = [&](const elem_t** dest, std::vector<const TensorView*> pieces) {
+    Block b;
+    b.destination = dest;
+    for (const TensorView* t : pieces) b.bytes += t->nbytes;
+    b.pieces = std::move(pieces);
+    blocks.push_back(std::move(b));
+  };
+  const int64_t hidden = config_.hidden_size;
+  const int64_t ffn = config_.intermediate_size;
+  const int64_t q_dim = config_.q_dim();
+  const int64_t kv_dim = config_.kv_dim();
+
+  add(&embedding_, {check("model.embed_tokens.weight", {config_.vocab_size, hidden})});
+  for (int i = 0; i < config_.num_layers; ++i) {
+    LayerWeights& w = layers_[static_cast<size_t>(i)];
+    const std::string p = "model.layers." + std::to_string(i) + ".";
+    add(&w.input_norm, {check(p + "input_layernorm.weight", {hidden})});
+    add(&w.qkv_proj, {check(p + "self_attn.q_proj.weight", {q_dim, hidden}),
+                      check(p + "self_attn.k_proj.weight", {kv_dim, hidden}),
+                      check(p + "self_attn.v_proj.weight", {kv_dim, hidden})});
+    add(&w.o_proj, {check(p + "self_attn.o_proj.weight", {hidden, q_dim})});
+    add(&w.post_attention_norm, {check(p + "post_attention_layernorm.weight", {hidden})});
+    add(&w.gate_up_proj, {check(p + "mlp.gate_proj.weight", {ffn, hidden}),
+                          check(p + "mlp.up_proj.weight", {ffn, hidden})});
+    add(&w.down_proj, {check(p + "mlp.down_proj.weight", {hidden, ffn})});
+  }
+  add(&final_norm_, {check("model.norm.weight", {hidden})});
+  const bool has_lm_head = archive.has("lm_head.weight");
+  if (has_lm_head) {
+    add(&lm_head_, {check("lm_head.weight", {config_.vocab_size, hidden})});
+  } else {
+    LCR_CHECK(config_.tie_word_embeddings,
+              "the checkpoint has no lm_head.weight and config.json does not say the "
+              "embeddings are tied");
+  }
+
+  size_t total = 0;
+  for (const Block& b : blocks) total = align_up(total, 256) + b.bytes;
+  HIP_CHECK(hipMalloc(&weight_block_, total));
+  weight_bytes_ = total;
+  size_t offset = 0;
+  for (const Block& b : blocks) {
+    offset = align_up(offset, 256);
+    char* base = reinterpret_cast<char*>(weight_block_) + offset;
+    size_t piece_offset = 0;
+    for (const TensorView* t : b.pieces) {
+      HIP_CHECK(hipMemcpy(base + piece_offset, t->data, t->nbytes, hipMemcpyHostToDevice));
+      piece_offset += t->nbytes;
+    }
+    *b.destination = reinterpret_cast<const elem_t*>(base);
+    offset += b.bytes;
+  }
+  if (!has_lm_head) lm_head_ = embedding_;
+}
+
+void Model::allocate_arena() {
+  const size_t H = static_cast<size_t>(config_.hidden_size);
+  const size_t F = static_cast<size_t>(config_.intermediate_size);
+  const size_t T = static_cast<size_t>(max_tokens_);
+  const size_t e = sizeof(elem_t);
+  const size_t qkv_w = static_cast<size_t>(config_.q_dim() + 2 * config_.kv_dim());
+  const size_t qd = static_cast<size_t>(config_.q_dim());
+  const size_t attn_floats = std::max<size_t>(
+      decode_attention_scratch_floats(config_.num_heads, config_.head_dim, kMaxAttentionSplits),
+      sample_scratch_floats(config_.vocab_size, 0));
+  const size_t sizes[] = {
+      T * H * e,                                 // x_
+      T * H * e,                                 // normed_
+      T * qkv_w * e,                             // qkv_
+      T * qd * e,                                // q_heads_
+      T * qd * e,                                // attn_out_
+      T * H * e,                                 // proj_out_
+      T * 2 * F * e,                             // gate_up_
+      T * F * e,                                 // act_
+      static_cast<size_t>(config_.vocab_size) * sizeof(float),  // logits_
+      attn_floats * sizeof(float),               // attention_scratch_
+      T * sizeof(int32_t),                       // token_ids_
+      sizeof(int32_t),                           // sampled_id_
+      H * sizeof(float),                         // resid_
+      sizeof(int32_t),                           // position_dev_
+      static_cast<size_t>(config_.num_kv_heads) * sizeof(unsigned),  // split_counters_
+      kMaxLmHeadBlocks * sizeof(unsigned long long),                  // argmax_partials_
+      (static_cast<size_t>(options_.max_seq) + 1) * sizeof(int32_t),  // history_
+  };
+  size_t total = 0;
+  for (size_t s : sizes) total = align_up(total, 256) + s;
+  arena_.reserve(total + 4096);
+  x_ = arena_.alloc<elem_t>(T * H);
+  normed_ = arena_.alloc<elem_t>(T * H);
+  qkv_ = arena_.alloc<elem_t>(T * qkv_w);
+  q_heads_ = arena_.alloc<elem_t>(T * qd);
+  attn_out_ = arena_.alloc<elem_t>(T * qd);
+  proj_out_ = arena_.alloc<elem_t>(T * H);
+  gate_up_ = arena_.alloc<elem_t>(T * 2 * F);
+  act_ = arena_.alloc<elem_t>(T * F);
+  logits_ = arena_.alloc<float>(static_cast<size_t>(config_.vocab_size));
+  attention_scratch_ = arena_.alloc<float>(attn_floats);
+  token_ids_ = arena_.alloc<int32_t>(T);
+  sampled_id_ = arena_.alloc<int32_t>(1);
+  resid_ = arena_.alloc<float>(H);
+  position_dev_ = arena_.alloc<int32_t>(1);
+  split_counters_ = arena_.alloc<unsigned>(static_cast<size_t>(config_.num_kv_heads));
+  argmax_partials_ = arena_.alloc<unsigned long long>(kMaxLmHeadBlocks);
+  history_ = arena_.alloc<int32_t>(static_cast<size_t>(options_.max_seq) + 1);
+  // The split counters must start at zero; the kernels return them to zero.
+  HIP_CHECK(hipMemset(split_counters_, 0, static_cast<size_t>(config_.num_kv_heads) * sizeof(unsigned)));
+  HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
+  HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
+}
+
+void Model::reset() {
+  position_ = 0;
+  taps_.clear();
+}
+
+int Model::decode_splits(int seq_len) const {
+  const int s = options_.attention_splits > 0
+                    ? std::min(options_.attention_splits, kMaxAttentionSplits)
+                    : choose_attention_splits(config_.num_kv_heads, seq_len, multiprocessors_);
+  return std::max(1, std::min(s, seq_len));
+}
+
+const float* Model::prefill(const std::vector<int>& tokens) {
+  LCR_CHECK(!tokens.empty(), "prefill needs at least one token");
+  LCR_CHECK(position_ + static_cast<int>(tokens.size()) <= options_.max_seq,
+            "prompt of " << tokens.size() << " tokens at position " << position_
+                         << " exceeds the cache built for " << options_.max_seq);
+  for (int t : tokens) {
+    LCR_CHECK(t >= 0 && t < config_.vocab_size,
+              "token id " << t << " is outside the vocabulary of " << config_.vocab_size);
+  }
+  if (options_.prefill_via_decode) {
+    GpuTimer timer;
+    timer.start(stream_);
+    const float* out = nullptr;
+    for (int t : tokens) out = decode(t);
+    timer.stop(stream_);
+    stats_.last_prefill_ms = timer.elapsed_ms();
+    return out;
+  }
+  GpuTimer timer;
+  timer.start(stream_);
+  size_t consumed = 0;
+  while (consumed < tokens.size()) {
+    const int chunk = static_cast<int>(std::min<size_t>(static_cast<size_t>(max_tokens_),
+                                                        tokens.size() - consumed));
+    std::vector<int32_t> ids(tokens.begin() + static_cast<long>(consumed),
+                             tokens.begin() + static_cast<long>(consumed) + chunk);
+    HIP_CHECK(hipMemcpyAsync(token_ids_, ids.data(), ids.size() * sizeof(int32_t),
+                             hipMemcpyHostToDevice, stream_));
+    kv_cache_->reserve_length(position_ + chunk);
+    launch_embedding_lookup(x_, embedding_, token_ids_, chunk, config_.hidden_size, stream_);
+    run_layers(chunk, position_);
+    position_ += chunk;
+    consumed += static_cast<size_t>(chunk);
+    // The ids buffer above is pageable host memory read by the async copy.
+    HIP_CHECK(hipStreamSynchronize(stream_));
+  }
+  timer.stop(stream_);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  stats_.last_prefill_ms = timer.elapsed_ms();
+  if (profiler_.enabled()) profiler_.collect();
+  return logits_;
+}
+
+void Model::write_step_state(int token) {
+  pinned_state_[0] = token;
+  pinned_state_[1] = position_;
+  HIP_CHECK(hipMemcpyAsync(token_ids_, &pinned_state_[0], sizeof(int32_t),
+                           hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(position_dev_, &pinned_state_[1], sizeof(int32_t),
+                           hipMemcpyHostToDevice, stream_));
+}
+
+DecodeStepArgs Model::step_args(int splits) const {
+  DecodeStepArgs a{};
+  a.hidden = config_.hidden_size;
+  a.ffn = config_.intermediate_size;
+  a.num_heads = config_.num_heads;
+  a.num_kv_heads = config_.num_kv_heads;
+  a.head_dim = config_.head_dim;
+  a.vocab = config_.vocab_size;
+  a.eps = config_.rms_norm_eps;
+  a.embedding = embedding_;
+  a.final_norm = final_norm_;
+  a.lm_head = lm_head_;
+  a.inv_freq = inv_freq_;
+  a.token = token_ids_;
+  a.position = position_dev_;
+  a.sampled = sampled_id_;
+  a.next_token = token_ids_;
+  a.history = history_;
+  a.history_len = options_.max_seq + 1;
+  a.resid = resid_;
+  a.q = q_heads_;
+  a.attn = attn_out_;
+  a.act = act_;
+  a.logits = logits_;
+  a.partials = attention_scratch_;
+  a.counters = split_counters_;
+  a.argmax_partials = argmax_partials_;
+  a.paged = options_.kv_layout == KvLayout::kPaged;
+  a.splits = splits;
+  return a;
+}
+
+void Model::launch_fused_step(int seq_len) {
+  const int splits = decode_splits(seq_len);
+  const DecodeStepArgs args = step_args(splits);
+  auto enqueue = [&]() {
+    for (int layer = 0; layer < config_.num_layers; ++layer) {
+      const LayerWeights& lw = layers_[static_cast<size_t>(layer)];
+      LayerDevicePtrs w{lw.input_norm, lw.qkv_proj, lw.o_proj, lw.post_attention_norm,
+                        lw.gate_up_proj, lw.down_proj};
+      enqueue_decode_layer(args, w, kv_cache_->view(layer), layer, stream_);
+    }
+    enqueue_decode_head(args, stream_);
+  };
+  if (!options_.use_graph || synchronous_launches()) {
+    enqueue();
+    return;
+  }
+  auto it = graphs_.find(splits);
+  if (it == graphs_.end()) {
+    hipGraph_t graph = nullptr;
+    HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    try {
+      enqueue();
+    } catch (...) {
+      hipGraph_t discard = nullptr;
+      (void)hipStreamEndCapture(stream_, &discard);
+      if (discard != nullptr) (void)hipGraphDestroy(discard);
+      throw;
+    }
+    HIP_CHECK(hipStreamEndCapture(stream_, &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIP_CHECK(status);
+    it = graphs_.emplace(splits, exec).first;
+  }
+  HIP_CHECK(hipGraphLaunch(it->second, stream_));
+}
+
+const float* Model::decode(int token) {
+  LCR_CHECK(position_ < options_.max_seq,
+            "sequence reached " << position_ << " positions, the cache limit");
+  LCR_CHECK(token >= 0 && token < config_.vocab_size,
+            "token id " << token << " is outside the vocabulary of " << config_.vocab_size);
+  GpuTimer timer;
+  timer.start(stream_);
+  kv_cache_->reserve_length(position_ + 1);
+  if (fused_ && !capture_activations_) {
+    write_step_state(token);
+    launch_fused_step(position_ + 1);
+  } else {
+    pinned_state_[0] = token;
+    HIP_CHECK(hipMemcpyAsync(token_ids_, &pinned_state_[0], sizeof(int32_t),
+                             hipMemcpyHostToDevice, stream_));
+    launch_embedding_lookup(x_, embedding_, token_ids_, 1, config_.hidden_size, stream_);
+    run_layers(1, position_);
+  }
+  position_ += 1;
+  timer.stop(stream_);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  stats_.last_decode_ms = timer.elapsed_ms();
+  if (profiler_.enabled()) profiler_.collect();
+  return logits_;
+}
+
+std::vector<int> Model::generate_greedy(int first_token, int steps, double* elapsed_ms) {
+  LCR_CHECK(fused_, "device-side greedy generation needs the fused decode path");
+  LCR_CHECK(steps >= 0, "steps must be non-negative");
+  LCR_CHECK(first_token >= 0 && first_token < config_.vocab_size,
+            "token id " << first_token << " is outside the vocabulary of " << config_.vocab_size);
+  LCR_CHECK(position_ + steps <= options_.max_seq,
+            "generating " << steps << " tokens at position " << position_
+                          << " exceeds the cache built for " << options_.max_seq);
+  std::vector<int> out(static_cast<size_t>(steps));
+  if (steps == 0) {
+    if (elapsed_ms) *elapsed_ms = 0.0;
+    return out;
+  }
+  const int start = position_;
+  kv_cache_->reserve_length(position_ + steps);
+  // Capture every graph this run needs before timing it.
+  for (int s = 0; s < steps; ++s) {
+    const int splits = decode_splits(start + s + 1);
+    if (options_.use_graph && graphs_.find(splits) == graphs_.end()) {
+      write_step_state(first_token);
+      launch_fused_step(start + s + 1);  // captures, then runs once at `start`
+      HIP_CHECK(hipStreamSynchronize(stream_));
+    }
+  }
+  write_step_state(first_token);
+  GpuTimer timer;
+  timer.start(stream_);
+  for (int s = 0; s < steps; ++s) launch_fused_step(start + s + 1);
+  timer.stop(stream_);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  const double ms = timer.elapsed_ms();
+  if (elapsed_ms) *elapsed_ms = ms;
+  stats_.last_decode_ms = ms / steps;
+  position_ = start + steps;
+  std::vector<int32_t> ids(static_cast<size_t>(steps));
+  HIP_CHECK(hipMemcpy(ids.data(), history_ + start + 1, static_cast<size_t>(steps) * sizeof(int32_t),
+                      hipMemcpyDeviceToHost));
+  for (int s = 0; s < steps; ++s) out[static_cast<size_t>(s)] = ids[static_cast<size_t>(s)];
+  return out;
+}
+
+double Model::time_decode_kernel(const std::string& kernel, int launches,
+                                 double* bytes_per_launch) {
+  LCR_CHECK(fused_, "kernel timing needs the fused decode path");
+  LCR_CHECK(launches > 0, "launches must be positive");
+  LCR_CHECK(position_ > 0, "time kernels after a prefill, so the step state is valid");
+  const double H = config_.hidden_size, F = config_.intermediate_size, V = config_.vocab_size;
+  const double qd = config_.q_dim(), kvd = config_.kv_dim();
+  const double e = sizeof(elem_t);
+  const int seq_len = position_;  // attention reads the positions present
+  unsigned mask = 0;
+  double bytes = 0.0;
+  if (kernel == "qkv") {
+    mask = kDecodeQkv;
+    bytes = (qd + 2 * kvd) * H * e + H * e + H * 4 + (qd + 2 * kvd) * e;
+  } else if (kernel == "attention") {
+    mask = kDecodeAttention;
+    bytes = 2.0 * kvd * seq_len * e + qd * e + qd * e;
+  } else if (kernel == "o_proj") {
+    mask = kDecodeOProj;
+    bytes = H * qd * e + qd * e + 2 * H * 4;
+  } else if (kernel == "gate_up") {
+    mask = kDecodeGateUp;
+    bytes = 2 * F * H * e + H * e + H * 4 + F * e;
+  } else if (kernel == "down") {
+    mask = kDecodeDown;
+    bytes = H * F * e + F * e + 2 * H * 4;
+  } else if (kernel == "lm_head") {
+    bytes = V * H * e + H * e + H * 4 + V * 4;
+  } else {
+    LCR_FAIL("unknown decode kernel \"" << kernel << "\"");
+  }
+  if (bytes_per_launch) *bytes_per_launch = bytes;
+  pinned_state_[1] = position_ - 1;  // the step that produced the current cache length
+  HIP_CHECK(hipMemcpyAsync(position_dev_, &pinned_state_[1], sizeof(int32_t), hipMemcpyHostToDevice,
+                           stream_));
+  const DecodeStepArgs args = step_args(decode_splits(seq_len));
+  std::vector<hipEvent_t> events(2 * static_cast<size_t>(launches));
+  for (hipEvent_t& ev : events) HIP_CHECK(hipEventCreate(&ev));
+  for (int i = 0; i < launches; ++i) {
+    const int layer = i % config_.num_layers;
+    HIP_CHECK(hipEventRecord(events[2 * static_cast<size_t>(i)], stream_));
+    if (mask == 0) {
+      enqueue_decode_head(args, stream_, false);
+    } else {
+      const LayerWeights& lw = layers_[static_cast<size_t>(layer)];
+      LayerDevicePtrs w{lw.input_norm, lw.qkv_proj, lw.o_proj, lw.post_attention_norm,
+                        lw.gate_up_proj, lw.down_proj};
+      enqueue_decode_layer(args, w, kv_cache_->view(layer), layer, stream_, mask);
+    }
+    HIP_CHECK(hipEventRecord(events[2 * static_cast<size_t>(i) + 1], stream_));
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  double total = 0.0;
+  for (int i = 0; i < launches; ++i) {
+    float ms = 0.0f;
+    HIP_CHECK(hipEventElapsedTime(&ms, events[2 * static_cast<size_t>(i)], events[2 * static_cast<size_t>(i) + 1]));
+    total += ms;
+  }
+  for (hipEvent_t ev : events) (void)hipEventDestroy(ev);
+  return total / launches;
+}
+
+void Model::set_position(int position) {
+  LCR_CHECK(position >= 0 && position <= options_.max_seq,
+            "position " << position << " outside [0, " << options_.max_seq << "]");
+  kv_cache_->reserve_length(position);
+  position_ = position;
+}
+
+void Model::fill_kv_normal(uint64_t seed, float stddev) {
+  fill_normal(kv_cache_->key_pool(), kv_cache_->pool_elements(), seed, stddev, stream_);
+  fill_normal(kv_cache_->value_pool(), kv_cache_->pool_elements(), seed ^ 0x5bf03635f0a5c3a9ull,
+              stddev, stream_);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+// The reference's run_layers (src/model.cu:370-484) on the kernel ABI: the
+// unfused path, used for prefill chunks and whenever the fused kernels do not
+// cover the model's geometry or activations are being captured.
+void Model::run_layers(int tokens, int start_position) {
+  const int hidden = config_.hidden_size;
+  const int ffn = config_.intermediate_size;
+  input_norm_done_ = false;
+  if (capture_activations_) {
+    taps_.clear();
+    capture("embed", x_, tokens, hidden);
+  }
+  const int qkv_stride = config_.q_dim() + 2 * config_.kv_dim();
+  const bool paged = options_.kv_layout == KvLayout::kPaged;
+  for (int layer = 0; layer < config_.num_layers; ++layer) {
+    const LayerWeights& w = layers_[static_cast<size_t>(layer)];
+    if (!input_norm_done_) {
+      ProfileScope scope(&profiler_, "rmsnorm", stream_);
+      launch_rmsnorm(normed_, x_, w.input_norm, tokens, hidden, config_.rms_norm_eps, stream_);
+    }
+    input_norm_done_ = false;
+    {
+      ProfileScope scope(&profiler_, "qkv_proj", stream_);
+      if (tokens == 1) {
+        launch_gemv(qkv_, false, w.qkv_proj, normed_, qkv_stride, hidden, stream_);
+      } else {
+        launch_gemm(qkv_, false, normed_, w.qkv_proj, tokens, qkv_stride, hidden, stream_);
+      }
+    }
+    const KvCacheView view = kv_cache_->view(layer);
+    {
+      ProfileScope scope(&profiler_, "rope + kv write", stream_);
+      launch_rope_q(q_heads_, qkv_, inv_freq_, tokens, start_position, config_.num_heads,
+                    config_.head_dim, qkv_stride, stream_);
+      launch_rope_write_kv(view, qkv_ + config_.q_dim(), qkv_ + config_.q_dim() + config_.kv_dim(),
+                           inv_freq_, tokens, start_position, paged, qkv_stride, stream_);
+    }
+    {
+      ProfileScope scope(&profiler_, "attention", stream_);
+      if (tokens == 1) {
+        attention_decode(layer, start_position);
+      } else {
+        attention_prefill(layer, tokens, start_position);
+      }
+    }
+    {
+      ProfileScope scope(&profiler_, "o_proj", stream_);
+      if (tokens == 1) {
+        launch_gemv(proj_out_, false, w.o_proj, attn_out_, hidden, config_.q_dim(), stream_);
+      } else {
+        launch_gemm(proj_out_, false, attn_out_, w.o_proj, tokens, hidden, config_.q_dim(), stream_);
+      }
+    }
+    {
+      ProfileScope scope(&profiler_, "residual+rmsnorm", stream_);
+      launch_add_residual_rmsnorm(normed_, x_, proj_out_, w.post_attention_norm, tokens, hidden,
+                                  config_.rms_norm_eps, stream_);
+    }
+    {
+      ProfileScope scope(&profiler_, "gate/up", stream_);
+      if (tokens == 1) {
+        launch_gemv(gate_up_, false, w.gate_up_proj, normed_, 2 * ffn, hidden, stream_);
+      } else {
+        launch_gemm(gate_up_, false, normed_, w.gate_up_proj, tokens, 2 * ffn, hidden, stream_);
+      }
+    }
+    {
+      ProfileScope scope(&profiler_, "swiglu", stream_);
+      launch_swiglu_strided(act_, gate_up_, gate_up_ + ffn, tokens, ffn, 2 * ffn, stream_);
+    }
+    {
+      ProfileScope scope(&profiler_, "down", stream_);
+      if (tokens == 1) {
+        launch_gemv(proj_out_, false, w.down_proj, act_, hidden, ffn, stream_);
+      } else {
+        launch_gemm(proj_out_, false, act_, w.down_proj, tokens, hidden, ffn, stream_);
+      }
+    }
+    {
+      const elem_t* next = (layer + 1 < config_.num_layers)
+                               ? layers_[static_cast<size_t>(layer + 1)].input_norm
+                               : final_norm_;
+      ProfileScope scope(&profiler_, "residual+rmsnorm", stream_);
+      launch_add_residual_rmsnorm(normed_, x_, proj_out_, next, tokens, hidden,
+                                  config_.rms_norm_eps, stream_);
+      input_norm_done_ = true;
+    }
+    if (capture_activations_) capture("layer_" + std::to_string(layer), x_, tokens, hidden);
+  }
+  if (!input_norm_done_) {
+    ProfileScope scope(&profiler_, "final norm", stream_);
+    launch_rmsnorm(normed_, x_, final_norm_, tokens, hidden, config_.rms_norm_eps, stream_);
+  }
+  input_norm_done_ = false;
+  if (capture_activations_) capture("final_norm", normed_, tokens, hidden);
+  const elem_t* last = normed_ + static_cast<int64_t>(tokens - 1) * hidden;
+  {
+    ProfileScope scope(&profiler_, "lm_head", stream_);
+    launch_gemv(logits_, true, lm_head_, last, config_.vocab_size, hidden, stream_);
+  }
+}
+
+void Model::attention_prefill(int layer, int tokens, int start_position) {
+  const float scale = 1.0f / std::sqrt(static_cast<float>(config_.head_dim));
+  launch_prefill_attention(attn_out_, q_heads_, kv_cache_->view(layer), config_.num_heads,
+                           config_.heads_per_kv(), tokens, start_position, scale,
+                           options_.kv_layout == KvLayout::kPaged, stream_);
+}
+
+void Model::attention_decode(int layer, int position) {
+  const int seq_len = position + 1;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(config_.head_dim));
+  launch_decode_attention(attn_out_, q_heads_, kv_cache_->view(layer), config_.num_heads,
+                          config_.heads_per_kv(), seq_len, scale,
+                          options_.kv_layout == KvLayout::kPaged, decode_splits(seq_len),
+                          attention_scratch_, stream_);
+}
+
+void Model::capture(const std::string& name, const elem_t* source, int tokens, int width) {
+  const size_t count = static_cast<size_t>(tokens) * width;
+  std::vector<elem_t> host(count);
+  HIP_CHECK(hipMemcpyAsync(host.data(), source, count * sizeof(elem_t), hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  Tap tap;
+  tap.name = name;
+  tap.tokens = tokens;
+  tap.width = width;
+  tap.values.resize(count);
+  for (size_t i = 0; i < count; ++i) tap.values[i] = elem_to_float(host[i]);
+  taps_.push_back(std::move(tap));
+}
+
+int Model::sample(const float* device_logits, float temperature, int top_k, float top_p,
+                  float uniform) {
+  launch_sample(sampled_id_, device_logits, config_.vocab_size, temperature, top_k, top_p, uniform,
+                attention_scratch_, stream_);
+  int32_t id = 0;
+  HIP_CHECK(hipMemcpyAsync(&id, sampled_id_, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  LCR_CHECK(id >= 0 && id < config_.vocab_size,
+            "sampling produced token id " << id << ", outside the vocabulary");
+  return static_cast<int>(id);
+}
+
+std::vector<float> Model::logits_to_host(const float* device_logits) const {
+  std::vector<float> host(static_cast<size_t>(config_.vocab_size));
+  HIP_CHECK(hipMemcpy(host.data(), device_logits, host.size() * sizeof(float), hipMemcpyDeviceToHost));
+  return host;
+}
+
+}  // namespace lcr

@@ -1,0 +1,184 @@
+// The model: weights resident in HBM, chunked prefill, single-token decode,
+// sampling. Drop-in for the reference's src/model.h:27-193 (same Options
+// fields, same public methods and semantics), running on HIP kernels only.
+//
+// Decode is a weight stream: 2.47 GB of bf16 weights per token for
+// Llama-3.2-1B, each used for one multiply-add. The decode step therefore runs
+// as fused kernels (five per layer, see kernels/decode_step.h) captured once in
+// a hipGraph per attention split count and replayed, with the token id and
+// position living in device memory so nothing has to be re-captured per token.
+// Prefill (more than one token) is compute bound and runs the projections as
+// MFMA GEMMs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "arena.h"
+#include "config.h"
+#include "kv_cache.h"
+#include "kernels/decode_step.h"
+#include "profiler.h"
+#include "safetensors.h"
+
+namespace lcr {
+
+struct LayerWeights {
+  const elem_t* input_norm = nullptr;
+  const elem_t* qkv_proj = nullptr;      // [q_dim + 2 kv_dim][hidden]: q, k, v rows
+  const elem_t* o_proj = nullptr;
+  const elem_t* post_attention_norm = nullptr;
+  const elem_t* gate_up_proj = nullptr;  // [2 ffn][hidden]: gate rows, then up rows
+  const elem_t* down_proj = nullptr;
+};
+
+struct ForwardStats {
+  size_t weight_bytes_per_token = 0;
+  size_t kv_bytes_per_position = 0;
+  size_t kv_bytes_at(int seq_len) const {
+    return static_cast<size_t>(seq_len) * kv_bytes_per_position;
+  }
+  double last_prefill_ms = 0.0;
+  double last_decode_ms = 0.0;
+};
+
+class Model {
+ public:
+  struct Options {
+    int device = 0;
+    int max_seq = 4096;
+    KvLayout kv_layout = KvLayout::kContiguous;
+    int page_size = 16;
+    int prefill_chunk = 256;
+    int attention_splits = 0;
+    // Not in the reference:
+    bool fused_decode = true;        // fused kernels when the geometry has them
+    bool use_graph = true;           // replay the fused step from a hipGraph
+    bool prefill_via_decode = false; // run prompts token by token through decode
+  };
+
+  Model(const std::string& model_dir, const Options& options);
+  ~Model();
+  Model(const Model&) = delete;
+  Model& operator=(const Model&) = delete;
+
+  const float* prefill(const std::vector<int>& tokens);
+  const float* decode(int token);
+  std::vector<float> logits_to_host(const float* device_logits) const;
+
+  void reset();
+  int position() const { return position_; }
+
+  const ModelConfig& config() const { return config_; }
+  const KvCache& kv_cache() const { return *kv_cache_; }
+  KvCache& mutable_kv_cache() { return *kv_cache_; }
+  const DeviceArena& arena() const { return arena_; }
+  const ForwardStats& stats() const { return stats_; }
+  size_t weight_bytes() const { return weight_bytes_; }
+  int multiprocessors() const { return multiprocessors_; }
+  hipStream_t stream() const { return stream_; }
+  const Options& options() const { return options_; }
+  bool fused() const { return fused_; }
+
+  int sample(const float* device_logits, float temperature, int top_k, float top_p,
+             float uniform);
+
+  struct Tap {
+    std::string name;
+    int tokens = 0;
+    int width = 0;
+    std::vector<float> values;
+  };
+  void set_capture_activations(bool enabled) { capture_activations_ = enabled; }
+  Profiler& profiler() { return profiler_; }
+  const Profiler& profiler() const { return profiler_; }
+  const std::vector<Tap>& activation_taps() const { return taps_; }
+
+  // Not in the reference. Greedy generation kept on the device: decodes
+  // `first_token`, then feeds each step's argmax straight into the next step
+  // with no host round trip, `steps` decodes in all. Returns the generated ids
+  // (the argmax after each step). Needs the fused decode path.
+  std::vector<int> generate_greedy(int first_token, int steps, double* elapsed_ms);
+  // Moves the position without running the model (the long-context stress
+  // case fills the cache directly). The cache must already hold `position`.
+  void set_position(int position);
+  // Fills every K and V element of the pool with N(0, stddev^2) bf16 values
+  // from a counter-based generator keyed by `seed` (long-context stress case).
+  void fill_kv_normal(uint64_t seed, float stddev);
+  // The attention split count decode uses at a given sequence length.
+  int decode_splits(int seq_len) const;
+  // Times one fused decode kernel in isolation: `launches` launches on this
+  // model's stream, cycling through the layers so each launch streams
+  // different weights, each bracketed by its own pair of hipEvents. Returns
+  // the mean launch duration in ms and the algorithmic bytes one launch moves.
+  // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head".
+  double time_decode_kernel(const std::string& kernel, int launches, double* bytes_per_launch);
+
+ private:
+  void load_weights(const SafetensorsArchive& archive);
+  void allocate_arena();
+  void run_layers(int tokens, int start_position);
+  void attention_prefill(int layer, int tokens, int start_position);
+  void attention_decode(int layer, int position);
+  void capture(const std::string& name, const elem_t* source, int tokens, int width);
+  void capture_f32_residual(const std::string& name);
+  void write_step_state(int token);
+  void enqueue_fused_step();
+  void launch_fused_step(int seq_len);
+  DecodeStepArgs step_args(int splits) const;
+
+  ModelConfig config_;
+  Options options_;
+  int multiprocessors_ = 0;
+  bool fused_ = false;
+  hipStream_t stream_ = nullptr;
+
+  elem_t* weight_block_ = nullptr;
+  size_t weight_bytes_ = 0;
+  const elem_t* embedding_ = nullptr;
+  const elem_t* final_norm_ = nullptr;
+  const elem_t* lm_head_ = nullptr;
+  std::vector<LayerWeights> layers_;
+  float* inv_freq_ = nullptr;
+
+  DeviceArena arena_;
+  std::unique_ptr<KvCache> kv_cache_;
+
+  elem_t* x_ = nullptr;           // [max_tokens][hidden]
+  elem_t* normed_ = nullptr;      // [max_tokens][hidden]
+  elem_t* qkv_ = nullptr;         // [max_tokens][q_dim + 2 kv_dim]
+  elem_t* q_heads_ = nullptr;     // [num_heads][max_tokens][head_dim]
+  elem_t* attn_out_ = nullptr;    // [max_tokens][q_dim]
+  elem_t* proj_out_ = nullptr;    // [max_tokens][hidden]
+  elem_t* gate_up_ = nullptr;     // [max_tokens][2 ffn]
+  elem_t* act_ = nullptr;         // [max_tokens][ffn]
+  float* logits_ = nullptr;       // [vocab]
+  float* attention_scratch_ = nullptr;
+  int32_t* token_ids_ = nullptr;  // [max_tokens]
+  int32_t* sampled_id_ = nullptr;
+  // Fused decode state.
+  float* resid_ = nullptr;        // [hidden] fp32 residual sum
+  int32_t* position_dev_ = nullptr;
+  unsigned* split_counters_ = nullptr;
+  unsigned long long* argmax_partials_ = nullptr;
+  int32_t* history_ = nullptr;    // [max_seq + 1]
+  int32_t* pinned_state_ = nullptr;  // host {token, position}
+
+  std::map<int, hipGraphExec_t> graphs_;  // by split count
+  hipGraph_t graph_template_ = nullptr;
+
+  int position_ = 0;
+  int max_tokens_ = 0;
+  ForwardStats stats_;
+  bool input_norm_done_ = false;
+  bool capture_activations_ = false;
+  std::vector<Tap> taps_;
+  Profiler profiler_;
+};
+
+}  // namespace lcr

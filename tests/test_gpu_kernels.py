@@ -1,0 +1,466 @@
+"""GPU parity of every kernel of the C-ABI against the CPU oracle.
+
+Shapes follow the reference's tests/test_kernels.cu:126-508 (rmsnorm 5x2048,
+swiglu/residual of length 24581, embedding with ids {7, 0, 127, 63}, rope 3
+tokens x 4 heads at start 11, causal softmax 3x6x20 at start 8, the 11 decode
+attention cases, the sampling known answers). Each kernel is called through
+the C-ABI on seeded inputs rounded through the element type and compared with
+the oracle on the same inputs: bit for bit for everything on the decode path
+(the kernels and the oracle share fixed operation orders), within the
+reference's 3e-2 relative-to-max tolerance for the MFMA GEMM and prefill
+attention, whose summation order belongs to the matrix cores.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import (BF16, dev, elems, expect_bits_equal, expect_close, host, kv_view_structs,
+                     oracle_view, p, random_elems, rng, sync, to_f32, zeros_dev)
+
+pytestmark = pytest.mark.gpu
+
+NULL = None
+
+
+def ok(lib, status, what):
+    if status != 0:
+        raise AssertionError(f"{what}: {lib.lcr_last_error_message().decode()}")
+
+
+def test_embedding_lookup(gpu, orc):
+    lib = gpu
+    r = rng()
+    vocab, dim, tokens = 128, 2048, 4
+    table = random_elems(r, (vocab, dim))
+    ids = np.array([7, 0, 127, 63], dtype=np.int32)
+    out = zeros_dev(tokens * dim)
+    ok(lib, lib.lcr_embedding_lookup(p(out), p(dev(table)), p(dev(ids)), tokens, dim, NULL), "embedding")
+    expect_bits_equal(host(out), table[ids].ravel(), "embedding")
+    # odd dim exercises the scalar tail
+    dim2 = 37
+    table2 = random_elems(r, (vocab, dim2))
+    out2 = zeros_dev(tokens * dim2)
+    ok(lib, lib.lcr_embedding_lookup(p(out2), p(dev(table2)), p(dev(ids)), tokens, dim2, NULL), "embedding odd")
+    expect_bits_equal(host(out2), table2[ids].ravel(), "embedding odd")
+
+
+@pytest.mark.parametrize("tokens,dim", [(5, 2048), (3, 1000), (1, 8), (2, 20000)])
+def test_rmsnorm(gpu, orc, tokens, dim):
+    lib = gpu
+    r = rng(tokens * 7919 + dim)
+    x = random_elems(r, (tokens, dim))
+    w = random_elems(r, (dim,), 0.5)
+    out = zeros_dev(tokens * dim)
+    ok(lib, lib.lcr_rmsnorm(p(out), p(dev(x)), p(dev(w)), tokens, dim, 1e-5, NULL), "rmsnorm")
+    expected = np.zeros(tokens * dim, dtype=np.uint16)
+    orc.load().orc_rmsnorm(BF16, expected.ctypes.data, x.ctypes.data, w.ctypes.data, tokens, dim, 1e-5)
+    expect_bits_equal(host(out), expected, f"rmsnorm {tokens}x{dim}")
+
+
+@pytest.mark.parametrize("tokens,dim", [(5, 2048), (4, 999), (2, 20000)])
+def test_add_residual_rmsnorm(gpu, orc, tokens, dim):
+    lib = gpu
+    r = rng(dim)
+    x = random_elems(r, (tokens, dim))
+    d = random_elems(r, (tokens, dim))
+    w = random_elems(r, (dim,), 0.5)
+    xt = dev(x)
+    out = zeros_dev(tokens * dim)
+    ok(lib, lib.lcr_add_residual_rmsnorm(p(out), p(xt), p(dev(d)), p(dev(w)), tokens, dim, 1e-5, NULL), "arr")
+    x_exp = x.copy()
+    out_exp = np.zeros(tokens * dim, dtype=np.uint16)
+    orc.load().orc_add_residual_rmsnorm(BF16, out_exp.ctypes.data, x_exp.ctypes.data, d.ctypes.data,
+                                        w.ctypes.data, tokens, dim, 1e-5)
+    expect_bits_equal(host(xt), x_exp, "residual stream")
+    expect_bits_equal(host(out), out_exp, "normed")
+
+
+def test_swiglu_and_residual(gpu, orc):
+    lib = gpu
+    r = rng()
+    count = 8192 * 3 + 5
+    g = random_elems(r, (count,))
+    u = random_elems(r, (count,))
+    out = zeros_dev(count)
+    ok(lib, lib.lcr_swiglu(p(out), p(dev(g)), p(dev(u)), count, NULL), "swiglu")
+    exp = np.zeros(count, dtype=np.uint16)
+    orc.load().orc_swiglu(BF16, exp.ctypes.data, g.ctypes.data, u.ctypes.data, count)
+    expect_bits_equal(host(out), exp, "swiglu")
+    gt = dev(g)
+    ok(lib, lib.lcr_add_residual(p(gt), p(dev(u)), count, NULL), "add_residual")
+    g2 = g.copy()
+    orc.load().orc_add_residual(BF16, g2.ctypes.data, u.ctypes.data, count)
+    expect_bits_equal(host(gt), g2, "add_residual")
+
+
+@pytest.mark.parametrize("width,stride", [(8192, 16384), (100, 250)])
+def test_swiglu_strided(gpu, orc, width, stride):
+    lib = gpu
+    r = rng(width)
+    tokens = 3
+    rows = random_elems(r, (tokens, stride))
+    out = zeros_dev(tokens * width)
+    rt = dev(rows)
+    ok(lib, lib.lcr_swiglu_strided(p(out), p(rt), p(rt) + 2 * width, tokens, width, stride, NULL), "swiglu_strided")
+    exp = np.zeros(tokens * width, dtype=np.uint16)
+    orc.load().orc_swiglu_strided(BF16, exp.ctypes.data, rows.ctypes.data, rows.ctypes.data + 2 * width, tokens,
+                                  width, stride)
+    expect_bits_equal(host(out), exp, "swiglu_strided")
+
+
+def rope_table(head_dim=64, theta=500000.0):
+    half = head_dim // 2
+    return np.array([theta ** (-2.0 * i / head_dim) for i in range(half)], dtype=np.float32)
+
+
+@pytest.mark.parametrize("start", [11, 4093, 131000])
+def test_rope_q(gpu, orc, start):
+    lib = gpu
+    r = rng(start)
+    tokens, heads, hd = 3, 4, 64
+    stride = heads * hd + 24  # a fused-row stride
+    q = random_elems(r, (tokens, stride))
+    freq = rope_table()
+    out = zeros_dev(tokens * heads * hd)
+    ok(lib, lib.lcr_rope_q(p(out), p(dev(q)), p(dev(freq)), tokens, start, heads, hd, stride, NULL), "rope_q")
+    exp = np.zeros(tokens * heads * hd, dtype=np.uint16)
+    orc.load().orc_rope_q(BF16, exp.ctypes.data, q.ctypes.data, freq.ctypes.data, tokens, start, heads, hd, stride)
+    expect_bits_equal(host(out), exp, "rope_q")
+
+
+def test_merge_heads(gpu, orc):
+    lib = gpu
+    r = rng()
+    tokens, heads, hd = 5, 6, 64
+    x = random_elems(r, (heads, tokens, hd))
+    out = zeros_dev(x.size)
+    ok(lib, lib.lcr_merge_heads(p(out), p(dev(x)), tokens, heads, hd, NULL), "merge_heads")
+    expect_bits_equal(host(out), np.transpose(x, (1, 0, 2)).ravel(), "merge_heads")
+
+
+# ---------------------------------------------------------------------------
+# KV cache write + decode attention (the reference's 11 cases)
+# ---------------------------------------------------------------------------
+
+class Cache:
+    """A one-layer cache in the reference's two layouts (src/kv_cache.cu:24-65,
+    :112-124), with pages handed out in order or through a given table."""
+
+    def __init__(self, kv_heads, head_dim, max_seq, paged, page_size=16, table=None):
+        self.kv_heads, self.hd, self.paged, self.page_size = kv_heads, head_dim, paged, page_size
+        if paged:
+            self.max_pages = -(-max_seq // page_size)
+            self.pool_pages = self.max_pages
+            n = self.pool_pages * kv_heads * page_size * head_dim
+            self.table = (np.arange(self.max_pages, dtype=np.int32) if table is None
+                          else np.asarray(table, dtype=np.int32))
+            self.page_stride = kv_heads * page_size * head_dim
+            self.head_stride = page_size * head_dim
+        else:
+            n = kv_heads * max_seq * head_dim
+            self.table = None
+            self.page_size = max_seq
+            self.page_stride = 0
+            self.head_stride = max_seq * head_dim
+        self.keys = zeros_dev(n)
+        self.values = zeros_dev(n)
+        self.table_t = dev(self.table) if paged else None
+
+    def view(self, lcr):
+        return kv_view_structs(lcr, self.keys, self.values, self.table_t, self.page_size, self.page_stride,
+                               self.head_stride, self.kv_heads, self.hd)
+
+    def host_view(self):
+        self.hk = host(self.keys).copy()
+        self.hv = host(self.values).copy()
+        return oracle_view(self.hk, self.hv, self.table, self.page_size, self.page_stride, self.head_stride,
+                           self.kv_heads, self.hd)
+
+
+def fill_cache(lib, lcr, cache, keys, values, positions, freq=None):
+    kv_dim = cache.kv_heads * cache.hd
+    freq = np.zeros(kv_dim, dtype=np.float32) if freq is None else freq
+    v = cache.view(lcr)
+    ok(lib, lib.lcr_rope_write_kv(ctypes.byref(v), p(dev(keys)), p(dev(values)), p(dev(freq)), positions, 0,
+                                  1 if cache.paged else 0, kv_dim, NULL), "rope_write_kv")
+    sync()
+
+
+ATTENTION_CASES = [
+    # (num_heads, kv_heads, head_dim, positions, splits, paged)
+    (32, 8, 64, 200, 1, False),
+    (32, 8, 64, 200, 8, False),
+    (32, 8, 64, 197, 7, False),
+    (32, 8, 64, 5, 64, False),
+    (8, 8, 64, 130, 4, False),
+    (8, 1, 64, 130, 4, False),
+    (8, 2, 128, 100, 2, False),
+    (32, 8, 64, 1, 1, False),
+    (32, 8, 64, 200, 1, True),
+    (32, 8, 64, 200, 8, True),
+    (32, 8, 64, 201, 4, True),
+    # beyond the reference's list: long ranges, many tiles per wave, odd tails
+    (32, 8, 64, 2049, 3, False),
+    (32, 8, 64, 4100, 16, True),
+    (16, 2, 128, 777, 5, True),
+]
+
+
+@pytest.mark.parametrize("heads,kv,hd,positions,splits,paged", ATTENTION_CASES)
+def test_decode_attention(gpu, lcr, orc, heads, kv, hd, positions, splits, paged):
+    lib = gpu
+    r = rng(positions * 31 + splits)
+    kv_dim = kv * hd
+    keys = random_elems(r, (positions, kv_dim))
+    values = random_elems(r, (positions, kv_dim))
+    q = random_elems(r, (heads, hd))
+    table = None
+    if paged:
+        # a shuffled block table, as the long-context configuration uses
+        pages = -(-(positions + 8) // 16)
+        table = r.permutation(pages).astype(np.int32)
+    cache = Cache(kv, hd, positions + 8, paged, 16, table)
+    fill_cache(lib, lcr, cache, keys, values, positions)
+    # The identity rotation must have landed every vector bit-exactly.
+    hv = cache.host_view()
+    for pos in (0, positions // 2, positions - 1):
+        for h in range(kv):
+            off = orc.load().orc_kv_offset(ctypes.byref(hv), 1 if paged else 0, h, pos)
+            expect_bits_equal(cache.hk[off:off + hd], keys[pos, h * hd:(h + 1) * hd], "cached key")
+            expect_bits_equal(cache.hv[off:off + hd], values[pos, h * hd:(h + 1) * hd], "cached value")
+    scratch_n = max(2, lib.lcr_decode_attention_scratch_floats(heads, hd, splits))
+    scratch = zeros_dev(scratch_n, np.float32)
+    out = zeros_dev(heads * hd)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    v = cache.view(lcr)
+    ok(lib, lib.lcr_decode_attention(p(out), p(dev(q)), ctypes.byref(v), heads, heads // kv, positions,
+                                     float(scale), 1 if paged else 0, splits, p(scratch), NULL), "attention")
+    exp = np.zeros(heads * hd, dtype=np.uint16)
+    orc.load().orc_decode_attention(BF16, exp.ctypes.data, q.ctypes.data, ctypes.byref(hv), heads, heads // kv,
+                                    positions, float(scale), 1 if paged else 0, splits)
+    expect_bits_equal(host(out), exp, f"attention {heads}/{kv}/{hd} n={positions} s={splits} paged={paged}")
+
+
+def test_decode_attention_paged_equals_contiguous(gpu, lcr):
+    lib = gpu
+    r = rng(5)
+    heads, kv, hd, n = 32, 8, 64, 333
+    keys = random_elems(r, (n, kv * hd))
+    values = random_elems(r, (n, kv * hd))
+    q = random_elems(r, (heads, hd))
+    outs = []
+    for paged in (False, True):
+        cache = Cache(kv, hd, n + 5, paged, 16, None if not paged else r.permutation(-(-(n + 5) // 16)))
+        fill_cache(lib, lcr, cache, keys, values, n)
+        out = zeros_dev(heads * hd)
+        scratch = zeros_dev(lib.lcr_decode_attention_scratch_floats(heads, hd, 4), np.float32)
+        v = cache.view(lcr)
+        ok(lib, lib.lcr_decode_attention(p(out), p(dev(q)), ctypes.byref(v), heads, 4, n, 0.125,
+                                         1 if paged else 0, 4, p(scratch), NULL), "attention")
+        outs.append(host(out).copy())
+    expect_bits_equal(outs[1], outs[0], "paged vs contiguous")
+
+
+def test_gather_kv(gpu, lcr, orc):
+    lib = gpu
+    r = rng(9)
+    kv, hd, n = 8, 64, 77
+    keys = random_elems(r, (n, kv * hd))
+    values = random_elems(r, (n, kv * hd))
+    cache = Cache(kv, hd, 96, True, 16, r.permutation(6))
+    fill_cache(lib, lcr, cache, keys, values, n)
+    ok_k = zeros_dev(kv * n * hd)
+    ok_v = zeros_dev(kv * n * hd)
+    v = cache.view(lcr)
+    ok(lib, lib.lcr_gather_kv(p(ok_k), p(ok_v), ctypes.byref(v), n, NULL), "gather")
+    expect_bits_equal(host(ok_k), keys.reshape(n, kv, hd).transpose(1, 0, 2).ravel(), "gathered keys")
+    expect_bits_equal(host(ok_v), values.reshape(n, kv, hd).transpose(1, 0, 2).ravel(), "gathered values")
+
+
+def test_rope_write_kv_rotates(gpu, lcr, orc):
+    lib = gpu
+    r = rng(17)
+    kv, hd, tokens, start = 8, 64, 9, 1000
+    stride = 3 * kv * hd
+    rows = random_elems(r, (tokens, stride))
+    freq = rope_table()
+    for paged in (False, True):
+        cache = Cache(kv, hd, 2048, paged, 16, None if not paged else r.permutation(128))
+        v = cache.view(lcr)
+        kt = dev(rows)
+        ok(lib, lib.lcr_rope_write_kv(ctypes.byref(v), p(kt), p(kt) + 2 * kv * hd, p(dev(freq)), tokens, start,
+                                      1 if paged else 0, stride, NULL), "rope_write_kv")
+        sync()
+        hv = cache.host_view()
+        ek = np.zeros_like(cache.hk)
+        ev = np.zeros_like(cache.hv)
+        ov = oracle_view(ek, ev, cache.table, cache.page_size, cache.page_stride, cache.head_stride, kv, hd)
+        orc.load().orc_rope_write_kv(BF16, ctypes.byref(ov), rows.ctypes.data, rows.ctypes.data + 2 * kv * hd,
+                                     freq.ctypes.data, tokens, start, 1 if paged else 0, stride)
+        expect_bits_equal(cache.hk, ek, f"keys paged={paged}")
+        expect_bits_equal(cache.hv, ev, f"values paged={paged}")
+
+
+def test_causal_softmax(gpu, orc):
+    lib = gpu
+    r = rng()
+    heads, rows, keys, start = 3, 6, 20, 8
+    scores = (r.normal(0, 4.0, size=(heads, rows, keys))).astype(np.float32)
+    out = zeros_dev(scores.size)
+    ok(lib, lib.lcr_causal_softmax(p(out), p(dev(scores)), heads, rows, keys, start, NULL), "softmax")
+    exp = np.zeros(scores.size, dtype=np.uint16)
+    orc.load().orc_causal_softmax(BF16, exp.ctypes.data, scores.ctypes.data, heads, rows, keys, start)
+    got = host(out)
+    expect_bits_equal(got, exp, "causal softmax")
+    probs = to_f32(got).reshape(heads, rows, keys)
+    for rr in range(rows):
+        limit = min(keys, start + rr + 1)
+        assert np.all(probs[:, rr, limit:] == 0.0)
+        assert np.allclose(probs[:, rr, :].sum(-1), 1.0, atol=1e-2)
+
+
+# ---------------------------------------------------------------------------
+# projections
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K", [(3072, 2048), (2048, 2048), (16384, 2048), (2048, 8192), (4097, 2048),
+                                 (1000, 4096), (77, 64), (130, 5000), (513, 2056)])
+@pytest.mark.parametrize("fp32_out", [0, 1])
+def test_gemv(gpu, orc, N, K, fp32_out):
+    lib = gpu
+    r = rng(N + K)
+    W = random_elems(r, (N, K), 0.02)
+    x = random_elems(r, (K,))
+    y = zeros_dev(N, np.float32 if fp32_out else np.uint16)
+    ok(lib, lib.lcr_gemv(p(y), fp32_out, p(dev(W)), p(dev(x)), N, K, NULL), "gemv")
+    exp = np.zeros(N, dtype=np.float32 if fp32_out else np.uint16)
+    orc.load().orc_gemv(BF16, exp.ctypes.data, fp32_out, W.ctypes.data, x.ctypes.data, N, K)
+    got = host(y, np.float32 if fp32_out else np.uint16)
+    if fp32_out:
+        expect_bits_equal(got.view(np.uint32), exp.view(np.uint32), f"gemv {N}x{K} fp32")
+    else:
+        expect_bits_equal(got, exp, f"gemv {N}x{K}")
+
+
+@pytest.mark.parametrize("T,N,K", [(128, 3072, 2048), (37, 2048, 8192), (256, 16384, 2048), (5, 100, 64)])
+def test_gemm_mfma(gpu, orc, T, N, K):
+    lib = gpu
+    r = rng(T * N)
+    X = random_elems(r, (T, K))
+    W = random_elems(r, (N, K), 0.02)
+    Y = zeros_dev(T * N, np.float32)
+    ok(lib, lib.lcr_gemm(p(Y), 1, p(dev(X)), p(dev(W)), T, N, K, NULL), "gemm")
+    Xf = to_f32(X).astype(np.float64)
+    Wf = to_f32(W).astype(np.float64)
+    exp = Xf @ Wf.T
+    got = host(Y, np.float32).reshape(T, N)
+    expect_close(got, exp, 1e-4, f"gemm {T}x{N}x{K}")
+    Yb = zeros_dev(T * N)
+    ok(lib, lib.lcr_gemm(p(Yb), 0, p(dev(X)), p(dev(W)), T, N, K, NULL), "gemm bf16")
+    expect_close(to_f32(host(Yb)), exp, 8e-3, "gemm bf16 out")
+
+
+@pytest.mark.parametrize("tokens,start,paged", [(7, 0, False), (40, 100, True), (65, 3, False)])
+def test_prefill_attention(gpu, lcr, orc, tokens, start, paged):
+    lib = gpu
+    r = rng(tokens + start)
+    heads, kv, hd = 32, 8, 64
+    n = start + tokens
+    keys = random_elems(r, (n, kv * hd))
+    values = random_elems(r, (n, kv * hd))
+    qh = random_elems(r, (heads, tokens, hd))
+    cache = Cache(kv, hd, n + 3, paged, 16, None if not paged else r.permutation(-(-(n + 3) // 16)))
+    fill_cache(lib, lcr, cache, keys, values, n)
+    out = zeros_dev(tokens * heads * hd)
+    v = cache.view(lcr)
+    ok(lib, lib.lcr_prefill_attention(p(out), p(dev(qh)), ctypes.byref(v), heads, heads // kv, tokens, start,
+                                      0.125, 1 if paged else 0, NULL), "prefill attention")
+    hv = cache.host_view()
+    exp = np.zeros(tokens * heads * hd, dtype=np.uint16)
+    orc.load().orc_prefill_attention(BF16, exp.ctypes.data, qh.ctypes.data, ctypes.byref(hv), heads, heads // kv,
+                                     tokens, start, 0.125, 1 if paged else 0)
+    expect_close(to_f32(host(out)), to_f32(exp), 3e-2, "prefill attention")
+
+
+# ---------------------------------------------------------------------------
+# sampling
+# ---------------------------------------------------------------------------
+
+def gpu_sample(lib, logits, temperature, top_k, top_p, uniform):
+    lt = dev(np.asarray(logits, dtype=np.float32))
+    out = zeros_dev(1, np.int32)
+    scratch = zeros_dev(max(4, lib.lcr_sample_scratch_floats(len(logits), top_k)), np.float32)
+    ok(lib, lib.lcr_sample(p(out), p(lt), len(logits), temperature, top_k, top_p, uniform, p(scratch), NULL),
+       "sample")
+    return int(host(out, np.int32)[0])
+
+
+def test_sampling_known_answers(gpu):
+    """tests/test_kernels.cu:468-508."""
+    lib = gpu
+    vocab = 4096
+    logits = np.full(vocab, -20.0, dtype=np.float32)
+    logits[1234], logits[99], logits[7] = 5.0, 4.0, 3.0
+    assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0) == 1234
+    assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.999) == 1234
+    assert gpu_sample(lib, logits, 1.0, 1, 1.0, 0.5) == 1234
+    for u in (0.01, 0.5, 0.99):
+        assert gpu_sample(lib, logits, 1.0, 0, 0.9, u) in (1234, 99)
+    pair = np.full(vocab, -60.0, dtype=np.float32)
+    pair[3] = pair[9] = 1.0
+    assert gpu_sample(lib, pair, 1.0, 0, 1.0, 0.25) == 3
+    assert gpu_sample(lib, pair, 1.0, 0, 1.0, 0.75) == 9
+    assert gpu_sample(lib, pair, 0.0, 0, 1.0, 0.5) == 3
+
+
+def test_sampling_matches_oracle(gpu, orc, lcr):
+    lib = gpu
+    r = rng(77)
+    vocab = 128256
+    uniforms = lcr.philox_uniforms(20260904, 64)
+    for trial in range(16):
+        logits = (r.normal(0, 0.9 + 0.3 * (trial % 4), size=vocab)).astype(np.float32)
+        if trial % 5 == 0:
+            logits[r.integers(0, vocab, 8)] = logits.max()  # exact ties
+        for (T, k, pp) in [(0.8, 40, 0.95), (1.0, 0, 0.9), (0.5, 0, 1.0), (1.3, 5, 0.5), (0.0, 0, 1.0)]:
+            u = uniforms[(trial * 5) % 64]
+            got = gpu_sample(lib, logits, T, k, pp, u)
+            exp = oracle.sample(logits, T, k, pp, u)
+            assert got == exp, f"trial {trial} T={T} k={k} p={pp} u={u}: gpu {got} oracle {exp}"
+
+
+def test_argmax_ties_and_edges(gpu, orc):
+    lib = gpu
+    r = rng(3)
+    for vocab in (1, 7, 255, 256, 257, 65537, 128256):
+        logits = r.normal(0, 1, size=vocab).astype(np.float32)
+        got = gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0)
+        assert got == oracle.argmax(logits) == int(np.argmax(logits))
+        logits[:] = 0.5
+        assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0) == 0
+        logits[vocab - 1] = np.float32(-0.0)
+        logits[:] = -np.inf
+        logits[vocab // 2] = -1e30
+        assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0) == vocab // 2
+
+
+def test_argument_errors(gpu, lcr):
+    lib = gpu
+    v = lcr.KvView(None, None, None, 16, 0, 64, 8, 64)
+    assert lib.lcr_decode_attention(None, None, ctypes.byref(v), 32, 4, 0, 0.125, 0, 1, None, NULL) == -1
+    assert b"at least one cached position" in lib.lcr_last_error_message()
+    assert lib.lcr_decode_attention(None, None, ctypes.byref(v), 32, 4, 10, 0.125, 0, 4, None, NULL) == -1
+    assert b"needs scratch space" in lib.lcr_last_error_message()
+    v.head_dim = 96
+    assert lib.lcr_decode_attention(None, None, ctypes.byref(v), 32, 4, 10, 0.125, 0, 1, None, NULL) == -1
+    assert b"head_dim" in lib.lcr_last_error_message()
+    assert lib.lcr_sample(None, None, 0, 1.0, 0, 0.5, 0.1, None, NULL) == -1
+    assert b"empty vocabulary" in lib.lcr_last_error_message()
+    assert lib.lcr_sample(None, None, 10, 1.0, 0, 1.5, 0.1, None, NULL) == -1
+    assert b"top_p must be in (0, 1]" in lib.lcr_last_error_message()
+    # empty inputs return early and succeed
+    assert lib.lcr_rmsnorm(None, None, None, 0, 2048, 1e-5, NULL) == 0
+    assert lib.lcr_embedding_lookup(None, None, None, 0, 2048, NULL) == 0

@@ -1,0 +1,152 @@
+"""GPU parity of the whole token loop (lcr::Model through the C-ABI) against
+the oracle model, on seeded random-init checkpoints.
+
+The small model keeps the real layer geometry (hidden 2048, ffn 8192, 32/8
+heads of 64, llama3 RoPE), so the fused decode kernels run, with fewer layers
+and a smaller vocabulary so the oracle finishes in seconds. On it:
+  - decode logits are bit-identical to the oracle for the fused step replayed
+    from a hipGraph, the fused step launched eagerly, and the unfused kernel
+    sequence, in both cache layouts, with one and with several attention
+    splits; the argmax of every step is the oracle's;
+  - paged page tables equal the oracle's in-order assignment;
+  - the MFMA prefill path matches the oracle within 2e-2 on the logits and
+    gives the same greedy continuation;
+  - activation taps of the unfused path equal the oracle's.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import expect_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(num_hidden_layers=2, vocab_size=4096)
+
+
+@pytest.fixture(scope="module")
+def small_ckpt(lcr, tmp_path_factory):
+    d = tmp_path_factory.mktemp("small_model")
+    return lcr.write_synthetic_checkpoint(d, lcr.llama_config(**SMALL))
+
+
+def make_pair(lcr, ckpt, max_seq=512, paged=False, splits=0, **opts):
+    m = lcr.Model(ckpt, max_seq=max_seq, paged=paged, attention_splits=splits, **opts)
+    o = oracle.OracleModel(ckpt, max_seq=max_seq, paged=paged, multiprocessors=m.stats().multiprocessors,
+                           attention_splits=splits)
+    return m, o
+
+
+def run_steps(m, o, prompt, steps, check_every=1):
+    """Prefills through decode, then greedy decodes; compares logits bits and
+    argmax each step. Returns the generated ids."""
+    lg = m.logits(m.prefill(prompt))
+    lo = o.prefill(prompt, use_decode_path=True)
+    expect_bits_equal(lg.view(np.uint32), lo.view(np.uint32), "prompt logits")
+    out = []
+    tok = oracle.argmax(lo)
+    for s in range(steps):
+        out.append(tok)
+        lg = m.logits(m.decode(tok))
+        lo = o.decode(tok)
+        if s % check_every == 0 or s == steps - 1:
+            expect_bits_equal(lg.view(np.uint32), lo.view(np.uint32), f"step {s} logits")
+        tok_g = oracle.argmax(lg)
+        tok = oracle.argmax(lo)
+        assert tok_g == tok
+    return out
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("mode", ["graph", "eager", "unfused"])
+def test_decode_bit_exact(lcr, small_ckpt, paged, mode):
+    opts = {"graph": dict(use_graph=1, fused_decode=1, prefill_via_decode=1),
+            "eager": dict(use_graph=0, fused_decode=1, prefill_via_decode=1),
+            "unfused": dict(fused_decode=0, prefill_via_decode=1)}[mode]
+    m, o = make_pair(lcr, small_ckpt, paged=paged, **opts)
+    assert m.stats().fused == (0 if mode == "unfused" else 1)
+    prompt = lcr.synthetic_tokens(24, m.vocab)
+    run_steps(m, o, prompt, 12)
+
+
+@pytest.mark.parametrize("splits", [3, 8])
+def test_decode_bit_exact_split_merge(lcr, small_ckpt, splits):
+    """Forced split counts exercise the fused last-block merge at small contexts."""
+    m, o = make_pair(lcr, small_ckpt, splits=splits, prefill_via_decode=1)
+    prompt = lcr.synthetic_tokens(70, m.vocab, seed=99)
+    run_steps(m, o, prompt, 6, check_every=2)
+
+
+def test_paged_tables_match_oracle(lcr, small_ckpt):
+    m, o = make_pair(lcr, small_ckpt, paged=True, prefill_via_decode=1)
+    prompt = lcr.synthetic_tokens(40, m.vocab)
+    m.prefill(prompt)
+    o.prefill(prompt, use_decode_path=True)
+    g = m.kv_geometry()
+    for layer in range(2):
+        expect_bits_equal(m.kv_page_table(layer), o.page_table(layer, g["max_pages"]), f"page table {layer}")
+    # the cached vectors are where the table says
+    k, v = m.kv_read(1, 3, 33, 64)
+    assert k.any() and v.any()
+
+
+def test_generate_greedy_matches_stepwise(lcr, small_ckpt):
+    m, o = make_pair(lcr, small_ckpt, prefill_via_decode=1)
+    prompt = lcr.synthetic_tokens(16, m.vocab)
+    first = oracle.argmax(m.logits(m.prefill(prompt)))
+    ids, ms = m.generate_greedy(first, 20)
+    lo = o.prefill(prompt, use_decode_path=True)
+    tok = oracle.argmax(lo)
+    assert tok == first
+    expected = []
+    for _ in range(20):
+        tok = oracle.argmax(o.decode(tok))
+        expected.append(tok)
+    assert list(ids) == expected
+    assert ms > 0.0
+
+
+def test_mfma_prefill_close_and_same_continuation(lcr, small_ckpt):
+    m, o = make_pair(lcr, small_ckpt)
+    prompt = lcr.synthetic_tokens(130, m.vocab, seed=7)
+    lg = m.logits(m.prefill(prompt))
+    lo = o.prefill(prompt)  # the oracle's chunked (prefill-attention) path
+    assert np.abs(lg - lo).max() <= 2e-2, np.abs(lg - lo).max()
+    tok_g, tok_o = oracle.argmax(lg), oracle.argmax(lo)
+    assert tok_g == tok_o
+    gen_g, gen_o = [], []
+    for _ in range(8):
+        gen_g.append(tok_g)
+        gen_o.append(tok_o)
+        tok_g = oracle.argmax(m.logits(m.decode(tok_g)))
+        tok_o = oracle.argmax(o.decode(tok_o))
+    assert gen_g == gen_o
+
+
+def test_activation_taps_match_oracle(lcr, small_ckpt):
+    m, o = make_pair(lcr, small_ckpt, fused_decode=0)
+    m.set_capture_activations(True)
+    prompt = lcr.synthetic_tokens(9, m.vocab)
+    m.prefill(prompt)
+    o.prefill(prompt)
+    taps = m.taps()
+    names = ["embed", "layer_0", "layer_1", "final_norm"]
+    assert list(taps) == names
+    for i, name in enumerate(names):
+        ref = o.tap(i, len(prompt))
+        assert taps[name].shape == ref.shape
+        assert np.abs(taps[name] - ref).max() <= 2e-2 * max(1.0, np.abs(ref).max()), name
+
+
+def test_model_errors(lcr, small_ckpt):
+    m = lcr.Model(small_ckpt, max_seq=8)
+    with pytest.raises(lcr.LcrError, match="exceeds the cache"):
+        m.prefill(list(range(9)))
+    with pytest.raises(lcr.LcrError, match="outside the vocabulary"):
+        m.decode(4096)
+    m.prefill([1, 2, 3, 4, 5, 6, 7, 8])
+    with pytest.raises(lcr.LcrError, match="cache limit"):
+        m.decode(1)
+    with pytest.raises(lcr.LcrError, match=r"top_p must be in \(0, 1\]"):
+        m.sample(0, 1.0, 0, 2.0, 0.5)

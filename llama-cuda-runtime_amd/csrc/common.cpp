@@ -54,7 +54,7 @@ DType dtype_from_string(const std::string& s) {
   if (s == "U8") return DType::kU8;
   if (s == "BOOL") return DType::kBool;
   LCR_CHECK(s != "F64", "F64 tensors are not supported");
-  LCR_FAIL("unsupported safetensors dtype \"" << s << "\"");
+  LCR_FAIL("unknown safetensors dtype \"" << s << "\"");
 }
 
 std::string format_bytes(size_t bytes) {

@@ -66,7 +66,36 @@ struct AttnShared {
   float wave_m[kAttnWaves][kGroup];
   float wave_l[kAttnWaves][kGroup];
   float wave_acc[kAttnWaves][kGroup][kHeadDim];
+  float merge_l[kGroup];
+  float merge_m[kGroup];
+  float merge_scale[kGroup][kAttnWaves];  // exp(m_w - M) per head and wave
 };
+
+// Step 3's reduce-scatter: at offset O the lane keeps the half of its N values
+// whose position-index bit matches its own lane bit and adds the partner's
+// copy of that half.
+template <int O, int N>
+__device__ __forceinline__ void reduce_scatter(float* vals, int lane) {
+  const bool upper = (lane & O) != 0;
+#pragma unroll
+  for (int k = 0; k < N / 2; ++k) {
+    const float lo = vals[k];
+    const float hi = vals[k + N / 2];
+    const float send = upper ? lo : hi;
+    const float keep = upper ? hi : lo;
+    vals[k] = keep + xor_lane<O>(send);
+  }
+  if constexpr (O > 1) reduce_scatter<O / 2, N / 2>(vals, lane);
+}
+
+// Step 6's sum over the lanes holding the same chunk: offsets 32, 16, ..., P.
+template <int P>
+__device__ __forceinline__ float sum_over_groups(float v) {
+  v += xor_lane<32>(v);
+  if constexpr (P <= 16) v += xor_lane<16>(v);
+  if constexpr (P <= 8) v += xor_lane<8>(v);
+  return v;
+}
 
 // One (kv_head, split) block. `q` holds num_heads * kHeadDim elements (head h
 // at h * kHeadDim). Writes either out (splits == 1) or partials.
@@ -138,18 +167,7 @@ __device__ __forceinline__ void decode_attention_block(
       }
     }
     // Step 3: reduce-scatter butterfly over the P lanes of a position.
-#pragma unroll
-    for (int o = P / 2, n = P * kGroup; o >= 1; o >>= 1, n >>= 1) {
-      const bool upper = (lane & o) != 0;
-#pragma unroll
-      for (int k = 0; k < n / 2; ++k) {
-        const float lo = vals[k];
-        const float hi = vals[k + n / 2];
-        const float send = upper ? lo : hi;
-        const float keep = upper ? hi : lo;
-        vals[k] = keep + __shfl_xor(send, o, 64);
-      }
-    }
+    reduce_scatter<P / 2, P * kGroup>(vals, lane);
     const int own = j * Q + a;  // owned position index within the tile
     float s[kGroup];
 #pragma unroll
@@ -199,10 +217,7 @@ __device__ __forceinline__ void decode_attention_block(
 #pragma unroll
   for (int g = 0; g < kGroup; ++g) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-#pragma unroll
-      for (int o = 32; o >= P; o >>= 1) acc[g][e] += __shfl_xor(acc[g][e], o, 64);
-    }
+    for (int e = 0; e < 8; ++e) acc[g][e] = sum_over_groups<P>(acc[g][e]);
     l_lane[g] = wave_sum(l_lane[g]);
   }
   if (lane < P) {
@@ -221,19 +236,33 @@ __device__ __forceinline__ void decode_attention_block(
   }
   __syncthreads();
 
-  // Steps 7-8, by wave 0.
+  // Steps 7-8, by wave 0. The per-head factors (M, L, exp(m_w - M)) do not
+  // depend on the element, so lane g computes them once for head g.
   if (wave == 0) {
-    for (int idx = lane; idx < kGroup * kHeadDim; idx += 64) {
-      const int g = idx / kHeadDim;
-      const int d = idx % kHeadDim;
+    if (lane < kGroup) {
+      const int g = lane;
       float tm = sh.wave_m[0][g];
       float tl = sh.wave_l[0][g];
 #pragma unroll
       for (int w = 1; w < kAttnWaves; ++w) softmax_combine(&tm, &tl, sh.wave_m[w][g], sh.wave_l[w][g]);
+      sh.merge_m[g] = tm;
+      sh.merge_l[g] = tl;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) sh.merge_scale[g][w] = lcr_expf(sh.wave_m[w][g] - tm);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int idx = lane; idx < kGroup * kHeadDim; idx += 64) {
+      const int g = idx / kHeadDim;
+      const int d = idx % kHeadDim;
+      const float tm = sh.merge_m[g];
+      const float tl = sh.merge_l[g];
       float merged = 0.0f;
 #pragma unroll
       for (int w = 0; w < kAttnWaves; ++w) {
-        merged = __builtin_fmaf(lcr_expf(sh.wave_m[w][g] - tm), sh.wave_acc[w][g][d], merged);
+        merged = __builtin_fmaf(sh.merge_scale[g][w], sh.wave_acc[w][g][d], merged);
       }
       const int head = kv_head * kGroup + g;
       if (splits == 1) {
@@ -250,24 +279,38 @@ __device__ __forceinline__ void decode_attention_block(
   }
 }
 
-// Merge of the split partials of one query head (threads stride over head_dim).
+constexpr int kMaxSplits = 64;
+
+// Merge of the split partials of one query head. Every thread of the block
+// calls it (it synchronises the block). Thread 0 folds the (m, l) of the
+// splits in order; the factors exp(m_s - M) are then formed once per split and
+// every thread sums its elements over the splits in order. `lds` holds
+// 2 + kMaxSplits floats.
 __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
                                                      const float* __restrict__ partials, int head,
-                                                     int splits, int head_dim) {
+                                                     int splits, int head_dim, float* lds) {
   const int stride = kPartialHeader + head_dim;
   const float* base = partials + static_cast<size_t>(head) * splits * stride;
-  float tm = kSoftmaxIdentity;
-  float tl = 0.0f;
-  for (int s = 0; s < splits; ++s) softmax_combine(&tm, &tl, base[s * stride], base[s * stride + 1]);
-  const float inv = 1.0f / tl;
+  if (threadIdx.x == 0) {
+    float tm = kSoftmaxIdentity;
+    float tl = 0.0f;
+    for (int s = 0; s < splits; ++s) softmax_combine(&tm, &tl, base[s * stride], base[s * stride + 1]);
+    lds[0] = tm;
+    lds[1] = tl;
+  }
+  __syncthreads();
+  const float tm = lds[0];
+  const float inv = 1.0f / lds[1];
+  for (int s = threadIdx.x; s < splits; s += blockDim.x) lds[2 + s] = lcr_expf(base[s * stride] - tm);
+  __syncthreads();
   for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
     float sum = 0.0f;
     for (int s = 0; s < splits; ++s) {
-      const float* slot = base + s * stride;
-      sum = __builtin_fmaf(lcr_expf(slot[0] - tm), slot[kPartialHeader + d], sum);
+      sum = __builtin_fmaf(lds[2 + s], base[s * stride + kPartialHeader + d], sum);
     }
     out[static_cast<size_t>(head) * head_dim + d] = float_to_elem(sum * inv);
   }
+  __syncthreads();
 }
 
 }  // namespace lcr

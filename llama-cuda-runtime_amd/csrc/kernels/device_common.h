@@ -130,23 +130,57 @@ __host__ __device__ __forceinline__ void lcr_sincosf(float angle, float* s_out, 
   *c_out = static_cast<float>(c);
 }
 
+// The value of lane (lane ^ kMask), for a compile-time mask. Lane exchanges
+// only move bits, so which hardware path carries them cannot change a result:
+// DPP quad permutes for masks 1 and 2, a DPP row rotate by 8 for mask 8 (both
+// are plain VALU operand modifiers), the LDS swizzle's xor mode for 4 and 16,
+// and ds_bpermute for 32.
+template <int kMask>
+__device__ __forceinline__ float xor_lane(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (kMask == 1) {
+    r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
+  } else if constexpr (kMask == 2) {
+    r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+  } else if constexpr (kMask == 8) {
+    r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true);  // row_ror:8
+  } else if constexpr (kMask == 4 || kMask == 16) {
+    r = __builtin_amdgcn_ds_swizzle(x, (kMask << 10) | 0x1F);      // xor mode
+  } else {
+    r = __shfl_xor(x, kMask, 64);
+  }
+  return __builtin_bit_cast(float, r);
+}
+
 // Butterfly over the 64 lanes of a wavefront, offsets 32, 16, 8, 4, 2, 1.
 // Lane i adds lane i^o at each step; addition commutes, so every lane ends
 // with the same bits.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v += xor_lane<32>(v);
+  v += xor_lane<16>(v);
+  v += xor_lane<8>(v);
+  v += xor_lane<4>(v);
+  v += xor_lane<2>(v);
+  v += xor_lane<1>(v);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  v = fmaxf(v, xor_lane<32>(v));
+  v = fmaxf(v, xor_lane<16>(v));
+  v = fmaxf(v, xor_lane<8>(v));
+  v = fmaxf(v, xor_lane<4>(v));
+  v = fmaxf(v, xor_lane<2>(v));
+  v = fmaxf(v, xor_lane<1>(v));
   return v;
 }
 // The same butterfly restricted to aligned groups of 32 lanes (offsets 16..1).
 __device__ __forceinline__ float half_wave_sum(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v += xor_lane<16>(v);
+  v += xor_lane<8>(v);
+  v += xor_lane<4>(v);
+  v += xor_lane<2>(v);
+  v += xor_lane<1>(v);
   return v;
 }
 

@@ -29,7 +29,8 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
 
 __global__ void merge_splits_kernel(elem_t* __restrict__ out, const float* __restrict__ partials,
                                     int splits, int head_dim) {
-  merge_split_partials(out, partials, blockIdx.x, splits, head_dim);
+  __shared__ float lds[2 + kMaxSplits];
+  merge_split_partials(out, partials, blockIdx.x, splits, head_dim, lds);
 }
 
 constexpr int kSoftmaxThreads = 256;
@@ -192,7 +193,7 @@ extern "C" int lcr_decode_attention(void* out, const void* q, const lcr_kv_view*
   a.num_heads = num_heads;
   a.seq_len = seq_len;
   a.scale = scale;
-  a.splits = std::min(splits, seq_len);
+  a.splits = std::min(std::min(splits, seq_len), kMaxSplits);
   a.stream = static_cast<hipStream_t>(stream);
   return paged ? launch_by_head_dim<true>(view->head_dim, heads_per_kv, a)
                : launch_by_head_dim<false>(view->head_dim, heads_per_kv, a);

@@ -165,6 +165,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStep
                                                                       float scale) {
   __shared__ AttnShared<HD, G> sh;
   __shared__ int is_last;
+  __shared__ float merge_lds[2 + kMaxSplits];
   const int seq_len = *a.position + 1;
   const int splits = min(a.splits, seq_len);
   // A graph captured for more splits than this position can use: the extra
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStep
   __threadfence();
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    merge_split_partials(a.attn, a.partials, blockIdx.x * G + g, splits, HD);
+    merge_split_partials(a.attn, a.partials, blockIdx.x * G + g, splits, HD, merge_lds);
   }
   if (threadIdx.x == 0) a.counters[blockIdx.x] = 0u;
 }
@@ -203,6 +204,8 @@ __global__ __launch_bounds__(kThreads) void proj_residual_kernel(DecodeStepArgs 
   GemvTile<2, NCH> tile;
   const elem_t* rows[2] = {W + static_cast<size_t>(row0) * K, W + static_cast<size_t>(row0 + 1) * K};
   tile.load(rows, lane);
+  // The residual entries this wave finishes, fetched while the weights stream.
+  const float vold = a.resid[row0 + (lane & 1)];
   vec16 xv[NCH];
   load_x_global<NCH>(xv, x, lane);
   float out[2];
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void proj_residual_kernel(DecodeStepArgs 
   if (lane < 2) {
     const int row = row0 + lane;
     const float proj = elem_to_float(float_to_elem(lane == 0 ? out[0] : out[1]));
-    const float xold = elem_to_float(float_to_elem(a.resid[row]));
+    const float xold = elem_to_float(float_to_elem(vold));
     a.resid[row] = xold + proj;
   }
 }
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(DecodeStepArgs a, Lay
 // ---------------------------------------------------------------------------
 
 template <int NCH>
-__global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
+__global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a, bool finalize) {
   constexpr int H = NCH * 512;
   constexpr int GROUP_ROWS = kWaves * kLmHeadRows;
   __shared__ __attribute__((aligned(16))) elem_t xs[H];
@@ -311,20 +314,35 @@ __global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
   }
   best = block_max_u64(best, lds_best);
   if (threadIdx.x == 0) a.argmax_partials[blockIdx.x] = best;
-}
+  if (!finalize) return;
 
-__global__ __launch_bounds__(kThreads) void argmax_step_kernel(DecodeStepArgs a, int blocks) {
-  __shared__ unsigned long long lds_best[16];
-  unsigned long long best = 0;
-  for (int i = threadIdx.x; i < blocks; i += kThreads) best = umax64(best, a.argmax_partials[i]);
-  best = block_max_u64(best, lds_best);
+  // The last block to finish reduces the block maxima (the maximum key is the
+  // same whichever block does it), publishes the id, advances the position and
+  // returns the arrival counter to zero for the next step.
+  __shared__ int is_last;
+  __threadfence();
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const int32_t id = argmax_id(best);
+    const unsigned prev = atomicAdd(a.head_counter, 1u);
+    is_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  unsigned long long total = 0;
+  for (int i = threadIdx.x; i < static_cast<int>(gridDim.x); i += kThreads) {
+    total = umax64(total, __hip_atomic_load(&a.argmax_partials[i], __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT));
+  }
+  total = block_max_u64(total, lds_best);
+  if (threadIdx.x == 0) {
+    const int32_t id = argmax_id(total);
     const int pos = *a.position;
     *a.sampled = id;
     *a.next_token = id;
     if (pos + 1 < a.history_len) a.history[pos + 1] = id;
     *a.position = pos + 1;
+    *a.head_counter = 0u;
   }
 }
 
@@ -395,10 +413,7 @@ void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
 
 void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t s, bool with_argmax) {
   const int blocks = lm_head_blocks(a.vocab);
-  lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a);
-  HIP_CHECK_LAUNCH();
-  if (!with_argmax) return;
-  argmax_step_kernel<<<1, kThreads, 0, s>>>(a, blocks);
+  lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a, with_argmax);
   HIP_CHECK_LAUNCH();
 }
 

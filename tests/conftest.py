@@ -39,6 +39,13 @@ def orc():
     return oracle
 
 
+@pytest.fixture(autouse=True)
+def _release_device_buffers():
+    yield
+    import helpers
+    helpers.release_all()
+
+
 @pytest.fixture(scope="session")
 def gpu(lcr):
     """Skips unless a HIP device is visible; the library must then be built."""

@@ -37,14 +37,30 @@ def _lcr():
     return load_lcr()
 
 
+# Every device buffer a test creates stays referenced here until the test's
+# teardown (after a device synchronize), so an inline `p(dev(x))` cannot free
+# memory that a queued kernel still reads.
+LIVE = []
+
+
+def release_all():
+    if LIVE:
+        sync()
+        LIVE.clear()
+
+
 def dev(a: np.ndarray):
     """A device copy of a host array (include/lcr_runtime.h memory)."""
-    return _lcr().DeviceBuffer.from_array(np.ascontiguousarray(a))
+    buf = _lcr().DeviceBuffer.from_array(np.ascontiguousarray(a))
+    LIVE.append(buf)
+    return buf
 
 
 def zeros_dev(n, dtype=np.uint16):
     dt = np.dtype(dtype)
-    return _lcr().DeviceBuffer(int(n) * dt.itemsize, dt, int(n))
+    buf = _lcr().DeviceBuffer(int(n) * dt.itemsize, dt, int(n))
+    LIVE.append(buf)
+    return buf
 
 
 def host(buf, dtype=np.uint16) -> np.ndarray:

@@ -108,11 +108,21 @@ def test_generate_greedy_matches_stepwise(lcr, small_ckpt):
 
 
 def test_mfma_prefill_close_and_same_continuation(lcr, small_ckpt):
+    """The MFMA GEMMs accumulate in the matrix cores' own order, so prefill is
+    compared within a tolerance: max |dlogit| <= max(2e-2, the distance between
+    the oracle's own two prefill paths). Those two differ only in where the
+    reference rounds to bf16 (chunked prefill rounds the softmax
+    probabilities, decode does not), which sets the noise floor any
+    fp32-accumulating implementation of the reference's prefill sits in."""
     m, o = make_pair(lcr, small_ckpt)
     prompt = lcr.synthetic_tokens(130, m.vocab, seed=7)
     lg = m.logits(m.prefill(prompt))
     lo = o.prefill(prompt)  # the oracle's chunked (prefill-attention) path
-    assert np.abs(lg - lo).max() <= 2e-2, np.abs(lg - lo).max()
+    od = oracle.OracleModel(small_ckpt, max_seq=512)
+    lod = od.prefill(prompt, use_decode_path=True)
+    floor = float(np.abs(lo - lod).max())
+    dev_ = float(np.abs(lg - lo).max())
+    assert dev_ <= max(2e-2, floor), (dev_, floor)
     tok_g, tok_o = oracle.argmax(lg), oracle.argmax(lo)
     assert tok_g == tok_o
     gen_g, gen_o = [], []

@@ -61,7 +61,6 @@ struct DecodeStepArgs {
   float* partials;           // attention split partials
   unsigned* counters;        // [num_kv_heads] split arrival counters, zero between uses
   unsigned long long* argmax_partials;  // [lm_head blocks]
-  unsigned* head_counter;    // [1] lm_head arrival counter, zero between steps
   bool paged;
   int splits;
 };

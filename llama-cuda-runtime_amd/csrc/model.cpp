@@ -183,7 +183,6 @@ void Model::allocate_arena() {
       sizeof(int32_t),                           // position_dev_
       static_cast<size_t>(config_.num_kv_heads) * sizeof(unsigned),  // split_counters_
       kMaxLmHeadBlocks * sizeof(unsigned long long),                  // argmax_partials_
-      sizeof(unsigned),                                               // head_counter_
       (static_cast<size_t>(options_.max_seq) + 1) * sizeof(int32_t),  // history_
   };
   size_t total = 0;
@@ -205,11 +204,9 @@ void Model::allocate_arena() {
   position_dev_ = arena_.alloc<int32_t>(1);
   split_counters_ = arena_.alloc<unsigned>(static_cast<size_t>(config_.num_kv_heads));
   argmax_partials_ = arena_.alloc<unsigned long long>(kMaxLmHeadBlocks);
-  head_counter_ = arena_.alloc<unsigned>(1);
   history_ = arena_.alloc<int32_t>(static_cast<size_t>(options_.max_seq) + 1);
   // The split counters must start at zero; the kernels return them to zero.
   HIP_CHECK(hipMemset(split_counters_, 0, static_cast<size_t>(config_.num_kv_heads) * sizeof(unsigned)));
-  HIP_CHECK(hipMemset(head_counter_, 0, sizeof(unsigned)));
   HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
   HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
 }
@@ -305,7 +302,6 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.partials = attention_scratch_;
   a.counters = split_counters_;
   a.argmax_partials = argmax_partials_;
-  a.head_counter = head_counter_;
   a.paged = options_.kv_layout == KvLayout::kPaged;
   a.splits = splits;
   return a;

@@ -166,7 +166,6 @@ class Model {
   int32_t* position_dev_ = nullptr;
   unsigned* split_counters_ = nullptr;
   unsigned long long* argmax_partials_ = nullptr;
-  unsigned* head_counter_ = nullptr;
   int32_t* history_ = nullptr;    // [max_seq + 1]
   int32_t* pinned_state_ = nullptr;  // host {token, position}
 

@@ -17,12 +17,19 @@ position at the mean context length prompt + (K+1)/2.
 The JSON line also carries:
   roofline      the dominant kernel (gate_up, 43% of the weight bytes): its
                 algorithmic bytes per launch / its mean launch time, timed live
-                here with a hipEvent pair around each launch on the model's
-                stream, against the 8 TB/s HBM peak; traffic from rocprofv3
-                counters when profiles/ holds them, else null;
+                here (a graph of back-to-back launches cycling through the 16
+                layers, bracketed by hipEvents on the model's stream), against
+                the 8 TB/s HBM peak; traffic = HBM bytes per launch from the
+                rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
+                profiles/, else null;
   cpu_baseline  the CPU oracle (oracle/, the restatement of the reference's
-                decode step) decoding a bounded sample of the same workload on
-                this box's host cores.
+                decode step) on this box's host cores: the same prompt is
+                prefilled untimed, then a bounded number of greedy decode steps
+                (decode + argmax) over the same context range is timed.
+
+--counters runs a short eager (un-captured) decode plus one device copy of
+256 MiB and prints a line: the program to put under rocprofv3 --pmc, where the
+copy calibrates the counters' byte units.
 
 Usage: python bench.py [--gpus 1] [--steps 255] [--warmup 16]
 """
@@ -43,6 +50,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X published HBM3E bandwidth
 BF16_DENSE_PEAK_TFLOPS = 2500.0
 REFERENCE_TOK_S = 322.3      # RTX 4090, docs/benchmarks.md:16
 REFERENCE_PEAK_FRAC = 0.791
+CPU_BASELINE_SECONDS = 30.0  # cap on the timed CPU sample
 
 
 def load_package():
@@ -65,39 +73,67 @@ def checkpoint_dir(lcr, config, seed) -> Path:
     return d
 
 
+COUNTER_SUMMARY = REPO / "profiles" / "gate_up_decode_config2_counters.md"
+
+
 def traffic_from_profiles():
-    """HBM bytes per gate_up launch from the committed rocprofv3 counter
+    """HBM bytes per gate_up launch (FETCH_SIZE + WRITE_SIZE, calibrated
+    against a copy of known size) from the committed rocprofv3 counter
     summary, when present."""
-    f = REPO / "profiles" / "gate_up_decode_counters.json"
-    if not f.exists():
+    import re
+    if not COUNTER_SUMMARY.exists():
         return None
-    try:
-        return json.loads(f.read_text()).get("traffic_bytes_per_launch")
-    except Exception:
-        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)\s*$", COUNTER_SUMMARY.read_text(), re.M)
+    return float(m.group(1)) if m else None
 
 
-def cpu_baseline(model_dir: Path, steps: int):
+def cpu_baseline(model_dir: Path, prompt, steps: int, max_seq: int):
     sys.path.insert(0, str(REPO))
     import oracle  # the checker, timed as the CPU baseline only
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-    ref = oracle.OracleModel(model_dir, max_seq=64)
-    ref.decode(1)  # page the memory-mapped weights in
+    ref = oracle.OracleModel(model_dir, max_seq=max_seq)
+    tok = oracle.argmax(ref.prefill(prompt, use_decode_path=True))  # untimed: fills the KV cache
     t0 = time.perf_counter()
-    for s in range(steps):
-        ref.decode(2 + s)
+    done = 0
+    while done < steps:
+        tok = oracle.argmax(ref.decode(tok))
+        done += 1
+        if time.perf_counter() - t0 > CPU_BASELINE_SECONDS:
+            break  # bounded sample on a slow host
     dt = time.perf_counter() - t0
     ref.close()
+    steps = done
+    n = len(prompt)
     return {
         "value": steps / dt,
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{steps} decode steps of the same 2.47 GB-per-token model at context 2..{steps + 1} "
-                  f"(CPU oracle, OpenMP over GEMV rows, {threads} threads), after one untimed step",
+        "sample": f"{steps} greedy decode steps (decode + argmax) at context {n + 1}..{n + steps} after an "
+                  f"untimed {n}-token prefill of the same prompt and model (CPU oracle, OpenMP over GEMV "
+                  f"rows, {threads} threads)",
         "ms_per_token": 1000.0 * dt / steps,
+        "seconds": dt,
     }
+
+
+def counters_run(lcr, model_dir: Path, prompt, max_seq: int) -> int:
+    """Eager work for a rocprofv3 --pmc pass: every fused decode kernel is a
+    separate dispatch, plus a 256 MiB device-to-device copy whose counter
+    reading calibrates the units."""
+    model = lcr.Model(model_dir, max_seq=max_seq, use_graph=0)
+    tok = model.sample(model.prefill(prompt), 0.0)
+    for _ in range(4):
+        tok = model.sample(model.decode(tok), 0.0)
+    nbytes = 256 << 20
+    src = lcr.DeviceBuffer(nbytes)
+    dst = lcr.DeviceBuffer(nbytes, zero=False)
+    lcr.device_copy(dst, src, nbytes)
+    lcr.synchronize()
+    model.close()
+    print(json.dumps({"counters_run": True, "decode_steps": 4, "copy_bytes": nbytes}))
+    return 0
 
 
 def main() -> int:
@@ -109,7 +145,8 @@ def main() -> int:
     ap.add_argument("--max-seq", type=int, default=2048)
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--kernel-launches", type=int, default=64)
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=256)
+    ap.add_argument("--counters", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -128,12 +165,14 @@ def main() -> int:
     t0 = time.perf_counter()
     model_dir = checkpoint_dir(lcr, config, seed)
     gen_s = time.perf_counter() - t0
+    prompt = lcr.synthetic_tokens(args.prompt, config["vocab_size"], seed=lcr.PROMPT_SEED)
+    if args.counters:
+        return counters_run(lcr, model_dir, prompt, args.max_seq)
     t0 = time.perf_counter()
     model = lcr.Model(model_dir, max_seq=args.max_seq)
     load_s = time.perf_counter() - t0
     st = model.stats()
     assert st.fused == 1, "the benchmark measures the fused decode step"
-    prompt = lcr.synthetic_tokens(args.prompt, config["vocab_size"], seed=lcr.PROMPT_SEED)
 
     # Warmup: prefill, W greedy steps (captures the decode graphs), reset.
     first = model.sample(model.prefill(prompt), 0.0)
@@ -185,7 +224,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(model_dir, args.cpu_steps)
+        cpu = cpu_baseline(model_dir, prompt, args.cpu_steps, args.max_seq)
     model.close()
 
     result = {

@@ -330,6 +330,13 @@ def synchronize(variant: str = "bf16") -> None:
     check(lib, lib.lcr_device_synchronize(), "device_synchronize")
 
 
+def device_copy(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+    """Device-to-device copy of nbytes (both buffers must hold them)."""
+    if nbytes > min(dst.nbytes, src.nbytes):
+        raise LcrError(f"copy of {nbytes} bytes exceeds a buffer ({dst.nbytes}, {src.nbytes})")
+    check(dst.lib, dst.lib.lcr_memcpy_dtod(dst.ptr, src.ptr, nbytes), "memcpy_dtod")
+
+
 class Model:
     """lcr::Model through the C-ABI (include/lcr_model.h)."""
 

@@ -1,7 +1,11 @@
 // Split-K GQA decode attention for one query token, as a device routine shared
 // by the standalone launcher and the fused decode step.
 //
-// Work split. One 256-thread block per (kv head, split); split s covers
+// Work split. One 256-thread block per (kv head, split) and per set of query
+// heads sharing that kv head: all of the group (the reference's shape) or a
+// single head (more, lighter blocks when the context is short). Every value
+// below is computed per query head with no operation mixing heads, so the
+// result does not depend on how heads are grouped into blocks. Split s covers
 // positions [s*chunk, min(seq_len, (s+1)*chunk)) with chunk = ceil(seq_len /
 // splits), as in the reference (src/kernels/attention.cu:129-133). The range
 // is cut into tiles of 64 positions; wave w of the block takes tiles w, w+4,
@@ -97,13 +101,14 @@ __device__ __forceinline__ float sum_over_groups(float v) {
   return v;
 }
 
-// One (kv_head, split) block. `q` holds num_heads * kHeadDim elements (head h
+// One block: query heads qhead0 .. qhead0 + kGroup - 1, all reading kv head
+// `kv_head`, over split `split`. `q` holds num_heads * kHeadDim elements (head h
 // at h * kHeadDim). Writes either out (splits == 1) or partials.
 template <bool kPaged, int kHeadDim, int kGroup>
 __device__ __forceinline__ void decode_attention_block(
     AttnShared<kHeadDim, kGroup>& sh, elem_t* __restrict__ out, float* __restrict__ partials,
-    const elem_t* __restrict__ q, const KvCacheView& view, int kv_head, int split, int splits,
-    int seq_len, float scale) {
+    const elem_t* __restrict__ q, const KvCacheView& view, int kv_head, int qhead0, int split,
+    int splits, int seq_len, float scale) {
   constexpr int P = kHeadDim / 8;   // chunks per position
   constexpr int Q = 64 / P;         // positions per load instruction
   const int lane = lane_id();
@@ -119,7 +124,7 @@ __device__ __forceinline__ void decode_attention_block(
   float qv[kGroup][8];
 #pragma unroll
   for (int g = 0; g < kGroup; ++g) {
-    const vec16 raw = load16(q + static_cast<size_t>(kv_head * kGroup + g) * kHeadDim + 8 * j);
+    const vec16 raw = load16(q + static_cast<size_t>(qhead0 + g) * kHeadDim + 8 * j);
     unpack8(raw, qv[g]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) qv[g][e] *= scale;
@@ -264,7 +269,7 @@ __device__ __forceinline__ void decode_attention_block(
       for (int w = 0; w < kAttnWaves; ++w) {
         merged = __builtin_fmaf(sh.merge_scale[g][w], sh.wave_acc[w][g][d], merged);
       }
-      const int head = kv_head * kGroup + g;
+      const int head = qhead0 + g;
       if (splits == 1) {
         out[static_cast<size_t>(head) * kHeadDim + d] = float_to_elem(merged * (1.0f / tl));
       } else {

@@ -59,7 +59,6 @@ struct DecodeStepArgs {
   elem_t* act;               // [ffn]
   float* logits;             // [vocab]
   float* partials;           // attention split partials
-  unsigned* counters;        // [num_kv_heads] split arrival counters, zero between uses
   unsigned long long* argmax_partials;  // [lm_head blocks]
   bool paged;
   int splits;

@@ -24,7 +24,8 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
     KvCacheView view, int seq_len, float scale, int splits) {
   __shared__ AttnShared<kHeadDim, kGroup> sh;
   decode_attention_block<kPaged, kHeadDim, kGroup>(sh, out, partials, q, view, blockIdx.x,
-                                                   blockIdx.y, splits, seq_len, scale);
+                                                   blockIdx.x * kGroup, blockIdx.y, splits,
+                                                   seq_len, scale);
 }
 
 __global__ void merge_splits_kernel(elem_t* __restrict__ out, const float* __restrict__ partials,

@@ -17,39 +17,67 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kLmHeadMaxBlocks = 1024;
 constexpr int kLmHeadRows = 2;  // rows per wave per group
+constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
+constexpr int kDownWaves = 1;   // waves (rows) per down block
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + lcr_expf(-v)); }
 
 // RMSNorm of the residual sum v into LDS as elements:
 //   normed = rne((f(rne(v)) * scale) * f(w)),  scale from sum(v^2).
-// `load_chunk(c, out8)` yields the 8 floats of chunk c of v. Thread t handles
-// chunks t, t+256, ... as the fixed norm order requires.
+// Split in two so a kernel can issue the norm's loads (v and w, 12 KiB) before
+// its weight stream: loads return in issue order, so inputs fetched after the
+// weight tile would make the norm wait for the whole tile.
+// Thread t handles chunks t, t+256, ... as the fixed norm order requires.
+template <int NCH>
+struct NormInput {
+  static constexpr int kPer = NCH / 4;  // chunks per thread (H / 8 / 256)
+  float v[kPer][8];
+  vec16 w[kPer];
+};
+
+// `load_chunk(c, out8)` yields the 8 floats of chunk c of v.
 template <int NCH, typename LoadChunk>
-__device__ __forceinline__ void norm_into_lds(elem_t* xs, LoadChunk load_chunk,
-                                              const elem_t* __restrict__ w, float eps,
-                                              float* scratch) {
-  constexpr int H = NCH * 512;
-  constexpr int PER = NCH / 4;  // chunks per thread (H / 8 / 256)
+__device__ __forceinline__ void norm_load(NormInput<NCH>& in, LoadChunk load_chunk,
+                                          const elem_t* __restrict__ w) {
   const int t = threadIdx.x;
-  float v[PER][8];
+#pragma unroll
+  for (int c = 0; c < NormInput<NCH>::kPer; ++c) {
+    const int chunk = t + c * kThreads;
+    load_chunk(chunk, in.v[c]);
+    in.w[c] = load16(w + 8 * chunk);
+  }
+}
+
+// Finishes the norm into `xs` (all threads; ends with a barrier). When
+// `resid_out` is set, the thread also stores its v chunks there (layer 0
+// seeding the residual sum with the embedding row).
+template <int NCH>
+__device__ __forceinline__ void norm_finish(elem_t* xs, const NormInput<NCH>& in, float eps,
+                                            float* scratch, float* resid_out) {
+  constexpr int H = NCH * 512;
+  const int t = threadIdx.x;
   float s = 0.0f;
 #pragma unroll
-  for (int c = 0; c < PER; ++c) {
-    load_chunk(t + c * kThreads, v[c]);
+  for (int c = 0; c < NormInput<NCH>::kPer; ++c) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s = __builtin_fmaf(v[c][j], v[c][j], s);
+    for (int j = 0; j < 8; ++j) s = __builtin_fmaf(in.v[c][j], in.v[c][j], s);
   }
   const float scale = norm_scale(block_norm_total(s, scratch), H, eps);
 #pragma unroll
-  for (int c = 0; c < PER; ++c) {
+  for (int c = 0; c < NormInput<NCH>::kPer; ++c) {
     const int chunk = t + c * kThreads;
-    const vec16 wv = load16(w + 8 * chunk);
+    const float* v = in.v[c];
+    if (resid_out != nullptr) {
+      *reinterpret_cast<float4*>(resid_out + 8 * chunk) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(resid_out + 8 * chunk + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
     vec16 out;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x0 = elem_to_float(float_to_elem(v[c][2 * i]));
-      const float x1 = elem_to_float(float_to_elem(v[c][2 * i + 1]));
-      out.w[i] = pack_elems((x0 * scale) * elem_lo(wv.w[i]), (x1 * scale) * elem_hi(wv.w[i]));
+      const float x0 = elem_to_float(float_to_elem(v[2 * i]));
+      const float x1 = elem_to_float(float_to_elem(v[2 * i + 1]));
+      out.w[i] = pack_elems((x0 * scale) * elem_lo(in.w[c].w[i]),
+                            (x1 * scale) * elem_hi(in.w[c].w[i]));
     }
     store16(xs + 8 * chunk, out);
   }
@@ -95,6 +123,22 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
   const int i0 = (blockIdx.x % BLOCKS_PER_HEAD) * 4;
   const int r0 = i0 + (wave & 1) * 2 + ((wave >> 1) ? HALF : 0);  // row within the head
 
+  // Everything the prologue and epilogue read is requested before the weight
+  // tile, so its latency hides under the stream: the position and rotation
+  // frequency (the 4 epilogue threads form sin/cos while the tile arrives), and
+  // the norm inputs.
+  const int pos = *a.position;
+  const float freq = a.inv_freq[i0 + (threadIdx.x & 3)];
+  NormInput<NCH> nin;
+  if (layer == 0) {
+    const elem_t* erow = a.embedding + static_cast<size_t>(*a.token) * H;
+    norm_load<NCH>(nin, [&](int chunk, float* out) { unpack8(load16(erow + 8 * chunk), out); },
+                   w.input_norm);
+  } else {
+    norm_load<NCH>(nin, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
+                   w.input_norm);
+  }
+
   GemvTile<2, NCH> tile;
   {
     const elem_t* rows[2] = {w.qkv + static_cast<size_t>(head * HD + r0) * H,
@@ -102,21 +146,9 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
     tile.load(rows, lane);
   }
 
-  if (layer == 0) {
-    const elem_t* erow = a.embedding + static_cast<size_t>(*a.token) * H;
-    const bool keep = blockIdx.x == 0;
-    norm_into_lds<NCH>(xs, [&](int chunk, float* out) {
-      const vec16 e = load16(erow + 8 * chunk);
-      unpack8(e, out);
-      if (keep) {
-        *reinterpret_cast<float4*>(a.resid + 8 * chunk) = make_float4(out[0], out[1], out[2], out[3]);
-        *reinterpret_cast<float4*>(a.resid + 8 * chunk + 4) = make_float4(out[4], out[5], out[6], out[7]);
-      }
-    }, w.input_norm, a.eps, scratch);
-  } else {
-    norm_into_lds<NCH>(xs, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
-                       w.input_norm, a.eps, scratch);
-  }
+  float sn = 0.0f, cs = 1.0f;
+  if (threadIdx.x < 4) lcr_sincosf(static_cast<float>(pos) * freq, &sn, &cs);
+  norm_finish<NCH>(xs, nin, a.eps, scratch, (layer == 0 && blockIdx.x == 0) ? a.resid : nullptr);
 
   vec16 xv[NCH];
   load_x_lds<NCH>(xv, xs, lane);
@@ -133,12 +165,9 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
     const int i = i0 + k;
     const float lo = rowv[k];
     const float hi = rowv[4 + k];
-    const int pos = *a.position;
     if (head < a.num_heads + a.num_kv_heads) {
-      float s, c;
-      lcr_sincosf(static_cast<float>(pos) * a.inv_freq[i], &s, &c);
-      const float ra = lo * c - hi * s;
-      const float rb = hi * c + lo * s;
+      const float ra = lo * cs - hi * sn;
+      const float rb = hi * cs + lo * sn;
       if (head < a.num_heads) {
         a.q[head * HD + i] = float_to_elem(ra);
         a.q[head * HD + i + HALF] = float_to_elem(rb);
@@ -159,60 +188,84 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
 // 2. Attention (split-K; the last block of a kv head merges the splits)
 // ---------------------------------------------------------------------------
 
+// One block per (query head, split): four times the blocks of a per-kv-head
+// grid, each with a quarter of the arithmetic, which is what a short context
+// needs (the kernel is latency-bound there). The blocks of one (kv head, split)
+// are numbered so they land on the same XCD (consecutive block ids go round
+// robin over the 8 XCDs), where they share the key/value lines in that XCD's
+// L2. The results equal the per-kv-head grid's bit for bit: no arithmetic
+// mixes heads.
+__device__ __forceinline__ void attention_block_coords(int b, int units, int group, int* unit,
+                                                       int* g) {
+  constexpr int kXcds = 8;
+  const int full = (units / kXcds) * kXcds * group;  // blocks in whole rounds of 8 units
+  if (b < full) {
+    const int round = b / (kXcds * group);
+    const int rem = b % (kXcds * group);
+    *g = rem / kXcds;
+    *unit = round * kXcds + rem % kXcds;
+  } else {
+    const int tail = units % kXcds;
+    const int r = b - full;
+    *g = r / tail;
+    *unit = (units / kXcds) * kXcds + r % tail;
+  }
+}
+
 template <bool kPaged, int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStepArgs a,
                                                                       KvCacheView view,
                                                                       float scale) {
-  __shared__ AttnShared<HD, G> sh;
-  __shared__ int is_last;
-  __shared__ float merge_lds[2 + kMaxSplits];
+  __shared__ AttnShared<HD, 1> sh;
   const int seq_len = *a.position + 1;
   const int splits = min(a.splits, seq_len);
+  int unit, g;
+  attention_block_coords(blockIdx.x, a.num_kv_heads * a.splits, G, &unit, &g);
+  const int kv_head = unit / a.splits;
+  const int split = unit % a.splits;
   // A graph captured for more splits than this position can use: the extra
   // blocks have no range and must not touch the partials of other heads.
-  if (blockIdx.y >= static_cast<unsigned>(splits)) return;
-  decode_attention_block<kPaged, HD, G>(sh, a.attn, a.partials, a.q, view, blockIdx.x, blockIdx.y,
-                                        splits, seq_len, scale);
-  if (splits <= 1) return;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&a.counters[blockIdx.x], 1u);
-    is_last = prev == static_cast<unsigned>(splits - 1);
+  if (split >= splits) return;
+  decode_attention_block<kPaged, HD, 1>(sh, a.attn, a.partials, a.q, view, kv_head, kv_head * G + g,
+                                        split, splits, seq_len, scale);
+}
+
+// Split merge (splits > 1 only), one 64-thread block per query head.
+__global__ __launch_bounds__(64) void attention_merge_step_kernel(DecodeStepArgs a, int head_dim) {
+  __shared__ float lds[2 + kMaxSplits];
+  const int splits = min(a.splits, *a.position + 1);
+  if (splits <= 1) {
+    // The attention blocks wrote the output directly. (The merge of one split
+    // would give the same bits; there is nothing to do.)
+    return;
   }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    merge_split_partials(a.attn, a.partials, blockIdx.x * G + g, splits, HD, merge_lds);
-  }
-  if (threadIdx.x == 0) a.counters[blockIdx.x] = 0u;
+  merge_split_partials(a.attn, a.partials, blockIdx.x, splits, head_dim, lds);
 }
 
 // ---------------------------------------------------------------------------
 // 3 / 5. Projection + residual join (o_proj, down)
 // ---------------------------------------------------------------------------
 
-template <int NCH>
-__global__ __launch_bounds__(kThreads) void proj_residual_kernel(DecodeStepArgs a,
-                                                                 const elem_t* __restrict__ W,
-                                                                 const elem_t* __restrict__ x) {
+// One row per wave (WAVES waves per block): the shape that streams these
+// matrices fastest on MI355X (more, smaller waves than two rows per wave).
+template <int NCH, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void proj_residual_kernel(DecodeStepArgs a,
+                                                                   const elem_t* __restrict__ W,
+                                                                   const elem_t* __restrict__ x) {
   constexpr int K = NCH * 512;
   const int lane = lane_id();
-  const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * 2;
-  GemvTile<2, NCH> tile;
-  const elem_t* rows[2] = {W + static_cast<size_t>(row0) * K, W + static_cast<size_t>(row0 + 1) * K};
+  const int row = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  GemvTile<1, NCH> tile;
+  const elem_t* rows[1] = {W + static_cast<size_t>(row) * K};
   tile.load(rows, lane);
-  // The residual entries this wave finishes, fetched while the weights stream.
-  const float vold = a.resid[row0 + (lane & 1)];
+  // The residual entry this wave finishes, fetched while the weights stream.
+  const float vold = a.resid[row];
   vec16 xv[NCH];
   load_x_global<NCH>(xv, x, lane);
-  float out[2];
+  float out[1];
   tile.dot(out, xv);
-  if (lane < 2) {
-    const int row = row0 + lane;
-    const float proj = elem_to_float(float_to_elem(lane == 0 ? out[0] : out[1]));
+  if (lane == 0) {
+    const float proj = elem_to_float(float_to_elem(out[0]));
     const float xold = elem_to_float(float_to_elem(vold));
     a.resid[row] = xold + proj;
   }
@@ -229,12 +282,14 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(DecodeStepArgs a, Lay
   __shared__ float scratch[9];
   const int lane = lane_id();
   const int i = blockIdx.x * kWaves + (threadIdx.x >> 6);  // activation index of this wave
+  NormInput<NCH> nin;
+  norm_load<NCH>(nin, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
+                 w.post_norm);
   GemvTile<2, NCH> tile;
   const elem_t* rows[2] = {w.gate_up + static_cast<size_t>(i) * H,
                            w.gate_up + static_cast<size_t>(a.ffn + i) * H};
   tile.load(rows, lane);
-  norm_into_lds<NCH>(xs, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
-                     w.post_norm, a.eps, scratch);
+  norm_finish<NCH>(xs, nin, a.eps, scratch, nullptr);
   vec16 xv[NCH];
   load_x_lds<NCH>(xv, xs, lane);
   float out[2];
@@ -270,6 +325,9 @@ __global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
     }
   };
 
+  NormInput<NCH> nin;
+  norm_load<NCH>(nin, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
+                 a.final_norm);
   GemvTile<kLmHeadRows, NCH> t0, t1;
   int g = blockIdx.x;
   if (g < groups) {
@@ -277,8 +335,7 @@ __global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
     row_ptrs(g, rows);
     t0.load(rows, lane);
   }
-  norm_into_lds<NCH>(xs, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
-                     a.final_norm, a.eps, scratch);
+  norm_finish<NCH>(xs, nin, a.eps, scratch, nullptr);
   vec16 xv[NCH];
   load_x_lds<NCH>(xv, xs, lane);
 
@@ -346,11 +403,15 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
   if (mask & kDecodeAttention) {
     const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
     attention_step_kernel<kPaged, HD, G>
-        <<<dim3(a.num_kv_heads, a.splits), kAttnThreads, 0, s>>>(a, view, scale);
+        <<<a.num_kv_heads * a.splits * G, kAttnThreads, 0, s>>>(a, view, scale);
     HIP_CHECK_LAUNCH();
+    if (a.splits > 1) {
+      attention_merge_step_kernel<<<a.num_heads, 64, 0, s>>>(a, HD);
+      HIP_CHECK_LAUNCH();
+    }
   }
   if (mask & kDecodeOProj) {
-    proj_residual_kernel<NCH><<<a.hidden / (2 * kWaves), kThreads, 0, s>>>(a, w.o, a.attn);
+    proj_residual_kernel<NCH, kOProjWaves><<<a.hidden / kOProjWaves, kOProjWaves * 64, 0, s>>>(a, w.o, a.attn);
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeGateUp) {
@@ -358,7 +419,7 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeDown) {
-    proj_residual_kernel<NCH_F><<<a.hidden / (2 * kWaves), kThreads, 0, s>>>(a, w.down, a.act);
+    proj_residual_kernel<NCH_F, kDownWaves><<<a.hidden / kDownWaves, kDownWaves * 64, 0, s>>>(a, w.down, a.act);
     HIP_CHECK_LAUNCH();
   }
 }

@@ -181,7 +181,6 @@ void Model::allocate_arena() {
       sizeof(int32_t),                           // sampled_id_
       H * sizeof(float),                         // resid_
       sizeof(int32_t),                           // position_dev_
-      static_cast<size_t>(config_.num_kv_heads) * sizeof(unsigned),  // split_counters_
       kMaxLmHeadBlocks * sizeof(unsigned long long),                  // argmax_partials_
       (static_cast<size_t>(options_.max_seq) + 1) * sizeof(int32_t),  // history_
   };
@@ -202,11 +201,8 @@ void Model::allocate_arena() {
   sampled_id_ = arena_.alloc<int32_t>(1);
   resid_ = arena_.alloc<float>(H);
   position_dev_ = arena_.alloc<int32_t>(1);
-  split_counters_ = arena_.alloc<unsigned>(static_cast<size_t>(config_.num_kv_heads));
   argmax_partials_ = arena_.alloc<unsigned long long>(kMaxLmHeadBlocks);
   history_ = arena_.alloc<int32_t>(static_cast<size_t>(options_.max_seq) + 1);
-  // The split counters must start at zero; the kernels return them to zero.
-  HIP_CHECK(hipMemset(split_counters_, 0, static_cast<size_t>(config_.num_kv_heads) * sizeof(unsigned)));
   HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
   HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
 }
@@ -300,7 +296,6 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.act = act_;
   a.logits = logits_;
   a.partials = attention_scratch_;
-  a.counters = split_counters_;
   a.argmax_partials = argmax_partials_;
   a.paged = options_.kv_layout == KvLayout::kPaged;
   a.splits = splits;

@@ -164,7 +164,6 @@ class Model {
   // Fused decode state.
   float* resid_ = nullptr;        // [hidden] fp32 residual sum
   int32_t* position_dev_ = nullptr;
-  unsigned* split_counters_ = nullptr;
   unsigned long long* argmax_partials_ = nullptr;
   int32_t* history_ = nullptr;    // [max_seq + 1]
   int32_t* pinned_state_ = nullptr;  // host {token, position}

@@ -46,6 +46,7 @@ struct DecodeStepArgs {
   const elem_t* final_norm;
   const elem_t* lm_head;
   const float* inv_freq;
+  const float2* rope_table;  // [max_seq][head_dim / 2] (cos, sin) of position * inv_freq
   // device state
   const int32_t* token;      // [1] token id of this step
   int32_t* position;         // [1] position of this step; incremented at the end

@@ -75,10 +75,11 @@ __device__ __forceinline__ void unpack8(const vec16& v, float* out) {
   }
 }
 
-__host__ __device__ __forceinline__ float lcr_expf(float x) {
-  if (x != x) return x;
-  if (x < -87.0f) return 0.0f;
-  if (x > 88.72283f) return __builtin_huge_valf();
+__host__ __device__ __forceinline__ float lcr_expf(float in) {
+  // The polynomial runs on the input clamped into its range and the special
+  // cases are selected afterwards, so a wavefront never diverges here; inside
+  // the range the clamp is the identity and the value is the same.
+  const float x = __builtin_fminf(__builtin_fmaxf(in, -87.0f), 88.72283f);
   const float k = __builtin_rintf(x * 1.44269504088896341f);
   float r = __builtin_fmaf(k, -0.693145751953125f, x);
   r = __builtin_fmaf(k, -1.428606765330187045e-06f, r);
@@ -90,7 +91,10 @@ __host__ __device__ __forceinline__ float lcr_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  return __builtin_ldexpf(p, static_cast<int>(k));
+  const float y = __builtin_ldexpf(p, static_cast<int>(k));
+  const float special = in < -87.0f ? 0.0f : __builtin_huge_valf();
+  const bool in_range = in >= -87.0f && in <= 88.72283f;
+  return in != in ? in : (in_range ? y : special);
 }
 
 __host__ __device__ __forceinline__ void lcr_sincosf(float angle, float* s_out, float* c_out) {

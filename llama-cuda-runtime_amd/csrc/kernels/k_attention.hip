@@ -18,14 +18,14 @@
 namespace lcr {
 namespace {
 
+// One block per (query head, split); query head h reads kv head h / kGroup.
 template <bool kPaged, int kHeadDim, int kGroup>
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
     elem_t* __restrict__ out, float* __restrict__ partials, const elem_t* __restrict__ q,
     KvCacheView view, int seq_len, float scale, int splits) {
-  __shared__ AttnShared<kHeadDim, kGroup> sh;
-  decode_attention_block<kPaged, kHeadDim, kGroup>(sh, out, partials, q, view, blockIdx.x,
-                                                   blockIdx.x * kGroup, blockIdx.y, splits,
-                                                   seq_len, scale);
+  __shared__ AttnShared<kHeadDim> sh;
+  decode_attention_block<kPaged, kHeadDim>(sh, out, partials, q, view, blockIdx.x / kGroup,
+                                           blockIdx.x, blockIdx.y, splits, seq_len, scale);
 }
 
 __global__ void merge_splits_kernel(elem_t* __restrict__ out, const float* __restrict__ partials,
@@ -109,7 +109,7 @@ struct DecodeArgs {
 
 template <bool kPaged, int kHeadDim, int kGroup>
 int launch_decode(const DecodeArgs& a) {
-  const dim3 grid(static_cast<unsigned>(a.num_heads / kGroup), static_cast<unsigned>(a.splits));
+  const dim3 grid(static_cast<unsigned>(a.num_heads), static_cast<unsigned>(a.splits));
   decode_attention_kernel<kPaged, kHeadDim, kGroup><<<grid, kAttnThreads, 0, a.stream>>>(
       a.out, a.partials, a.q, a.view, a.seq_len, a.scale, a.splits);
   CAPI_LAUNCHED();

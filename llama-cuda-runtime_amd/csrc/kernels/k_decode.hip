@@ -124,11 +124,11 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
   const int r0 = i0 + (wave & 1) * 2 + ((wave >> 1) ? HALF : 0);  // row within the head
 
   // Everything the prologue and epilogue read is requested before the weight
-  // tile, so its latency hides under the stream: the position and rotation
-  // frequency (the 4 epilogue threads form sin/cos while the tile arrives), and
-  // the norm inputs.
+  // tile, so its latency hides under the stream: the position, the rotation
+  // (cos, sin) of this position from the precomputed table, and the norm
+  // inputs.
   const int pos = *a.position;
-  const float freq = a.inv_freq[i0 + (threadIdx.x & 3)];
+  const float2 rot = a.rope_table[static_cast<size_t>(pos) * HALF + i0 + (threadIdx.x & 3)];
   NormInput<NCH> nin;
   if (layer == 0) {
     const elem_t* erow = a.embedding + static_cast<size_t>(*a.token) * H;
@@ -146,8 +146,6 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
     tile.load(rows, lane);
   }
 
-  float sn = 0.0f, cs = 1.0f;
-  if (threadIdx.x < 4) lcr_sincosf(static_cast<float>(pos) * freq, &sn, &cs);
   norm_finish<NCH>(xs, nin, a.eps, scratch, (layer == 0 && blockIdx.x == 0) ? a.resid : nullptr);
 
   vec16 xv[NCH];
@@ -166,8 +164,8 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
     const float lo = rowv[k];
     const float hi = rowv[4 + k];
     if (head < a.num_heads + a.num_kv_heads) {
-      const float ra = lo * cs - hi * sn;
-      const float rb = hi * cs + lo * sn;
+      const float ra = lo * rot.x - hi * rot.y;
+      const float rb = hi * rot.x + lo * rot.y;
       if (head < a.num_heads) {
         a.q[head * HD + i] = float_to_elem(ra);
         a.q[head * HD + i + HALF] = float_to_elem(rb);
@@ -216,7 +214,7 @@ template <bool kPaged, int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStepArgs a,
                                                                       KvCacheView view,
                                                                       float scale) {
-  __shared__ AttnShared<HD, 1> sh;
+  __shared__ AttnShared<HD> sh;
   const int seq_len = *a.position + 1;
   const int splits = min(a.splits, seq_len);
   int unit, g;
@@ -226,7 +224,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStep
   // A graph captured for more splits than this position can use: the extra
   // blocks have no range and must not touch the partials of other heads.
   if (split >= splits) return;
-  decode_attention_block<kPaged, HD, 1>(sh, a.attn, a.partials, a.q, view, kv_head, kv_head * G + g,
+  decode_attention_block<kPaged, HD>(sh, a.attn, a.partials, a.q, view, kv_head, kv_head * G + g,
                                         split, splits, seq_len, scale);
 }
 

@@ -2,6 +2,8 @@
 // counter-based stream (splitmix64 of seed and pair index, two 32-bit
 // uniforms, Box-Muller), so the content depends only on (seed, i) and not on
 // the launch shape.
+#include <algorithm>
+
 #include "../hip_utils.h"
 #include "device_common.h"
 #include "fill.h"
@@ -31,7 +33,29 @@ __global__ void fill_normal_kernel(elem_t* __restrict__ data, size_t count, uint
   }
 }
 
+__global__ void rope_table_kernel(float2* __restrict__ table, const float* __restrict__ inv_freq,
+                                  int positions, int half) {
+  const size_t n = static_cast<size_t>(positions) * half;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t e = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    const int p = static_cast<int>(e / half);
+    const int i = static_cast<int>(e % half);
+    float s, c;
+    lcr_sincosf(static_cast<float>(p) * inv_freq[i], &s, &c);
+    table[e] = make_float2(c, s);
+  }
+}
+
 }  // namespace
+
+void build_rope_table(float2* table, const float* inv_freq, int positions, int half,
+                      hipStream_t stream) {
+  const size_t n = static_cast<size_t>(positions) * half;
+  if (n == 0) return;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 4096));
+  rope_table_kernel<<<blocks, 256, 0, stream>>>(table, inv_freq, positions, half);
+  HIP_CHECK_LAUNCH();
+}
 
 void fill_normal(elem_t* data, size_t count, uint64_t seed, float stddev, hipStream_t stream) {
   if (count == 0) return;

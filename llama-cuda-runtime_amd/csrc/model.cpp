@@ -54,6 +54,13 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
                                  config_.num_heads, config_.num_kv_heads, config_.head_dim) &&
            config_.vocab_size > 0;
 
+  if (fused_) {
+    const int half = config_.head_dim / 2;
+    HIP_CHECK(hipMalloc(&rope_table_, static_cast<size_t>(options_.max_seq) * half * sizeof(float2)));
+    build_rope_table(rope_table_, inv_freq_, options_.max_seq, half, stream_);
+    HIP_CHECK(hipStreamSynchronize(stream_));
+  }
+
   stats_.kv_bytes_per_position = config_.kv_bytes_per_token(sizeof(elem_t));
   // Weight bytes streamed per decoded token, counted as the reference does
   // (src/model.cu:86-102): every projection, both norms per layer, the final
@@ -79,6 +86,7 @@ Model::~Model() {
   if (stream_ != nullptr) (void)hipStreamDestroy(stream_);
   (void)hipFree(weight_block_);
   (void)hipFree(inv_freq_);
+  (void)hipFree(rope_table_);
 }
 
 // Layout and checks follow the reference's src/model.cu:112-213: one device
@@ -284,6 +292,7 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.final_norm = final_norm_;
   a.lm_head = lm_head_;
   a.inv_freq = inv_freq_;
+  a.rope_table = rope_table_;
   a.token = token_ids_;
   a.position = position_dev_;
   a.sampled = sampled_id_;

@@ -145,6 +145,7 @@ class Model {
   const elem_t* lm_head_ = nullptr;
   std::vector<LayerWeights> layers_;
   float* inv_freq_ = nullptr;
+  float2* rope_table_ = nullptr;  // fused step: [max_seq][head_dim / 2] (cos, sin)
 
   DeviceArena arena_;
   std::unique_ptr<KvCache> kv_cache_;

@@ -310,6 +310,8 @@ inline int64_t kv_off(const orc_kv_view& v, bool paged, int head, int pos) {
   return paged ? kv_offset<true>(v, head, pos) : kv_offset<false>(v, head, pos);
 }
 
+constexpr int kAttnWaves = 8;  // waves per attention block (kernels/attention_decode.h)
+
 struct SplitResult {
   std::vector<float> m, l, acc;  // [G], [G], [G][hd]
 };
@@ -320,14 +322,15 @@ SplitResult attention_split(int kind, const std::vector<float>& qs, const orc_kv
   const int P = hd / 8;
   const int Q = 64 / P;
   const int length = std::max(0, end - begin);
-  std::vector<float> wm(4 * G), wl(4 * G), wacc(static_cast<size_t>(4) * G * hd);
-  for (int w = 0; w < 4; ++w) {
+  constexpr int W = kAttnWaves;
+  std::vector<float> wm(W * G), wl(W * G), wacc(static_cast<size_t>(W) * G * hd);
+  for (int w = 0; w < W; ++w) {
     std::vector<float> m(G, -FLT_MAX);
     std::vector<float> l_lane(static_cast<size_t>(64) * G, 0.0f);
     std::vector<float> acc(static_cast<size_t>(64) * G * 8, 0.0f);
     std::vector<float> s(static_cast<size_t>(64) * G), p(static_cast<size_t>(64) * G);
     std::vector<float> kf(static_cast<size_t>(64) * hd), vf(static_cast<size_t>(64) * hd);
-    for (int tile = w; tile * 64 < length; tile += 4) {
+    for (int tile = w; tile * 64 < length; tile += W) {
       const int tb = begin + tile * 64;
       const int count = std::min(64, end - tb);
       for (int pi = 0; pi < 64; ++pi) {
@@ -412,19 +415,21 @@ SplitResult attention_split(int kind, const std::vector<float>& qs, const orc_kv
   res.m.resize(G);
   res.l.resize(G);
   res.acc.resize(static_cast<size_t>(G) * hd);
+  // Waves merge max first: M = max m_w, c_w = exp(m_w - M), then L and acc
+  // accumulated in wave order (kernels/attention_decode.h step 7).
   for (int g = 0; g < G; ++g) {
     float tm = wm[g];
-    float tl = wl[g];
-    for (int w = 1; w < 4; ++w) {
-      softmax_combine(&tm, &tl, wm[static_cast<size_t>(w) * G + g], wl[static_cast<size_t>(w) * G + g]);
-    }
+    for (int w = 1; w < W; ++w) tm = std::fmax(tm, wm[static_cast<size_t>(w) * G + g]);
+    float c[W];
+    for (int w = 0; w < W; ++w) c[w] = expf_fixed(wm[static_cast<size_t>(w) * G + g] - tm);
+    float tl = 0.0f;
+    for (int w = 0; w < W; ++w) tl = std::fma(wl[static_cast<size_t>(w) * G + g], c[w], tl);
     res.m[g] = tm;
     res.l[g] = tl;
     for (int d = 0; d < hd; ++d) {
       float merged = 0.0f;
-      for (int w = 0; w < 4; ++w) {
-        merged = std::fma(expf_fixed(wm[static_cast<size_t>(w) * G + g] - tm),
-                          wacc[(static_cast<size_t>(w) * G + g) * hd + d], merged);
+      for (int w = 0; w < W; ++w) {
+        merged = std::fma(c[w], wacc[(static_cast<size_t>(w) * G + g) * hd + d], merged);
       }
       res.acc[static_cast<size_t>(g) * hd + d] = merged;
     }
@@ -462,14 +467,18 @@ void decode_attention_impl(int kind, uint16_t* out, const uint16_t* q, const orc
         }
         continue;
       }
-      float tm = -FLT_MAX;
+      // Splits merge max first, like the waves (attention_decode.h step 8).
+      float tm = parts[0].m[g];
+      for (int sp = 1; sp < splits; ++sp) tm = std::fmax(tm, parts[sp].m[g]);
+      std::vector<float> c(static_cast<size_t>(splits));
+      for (int sp = 0; sp < splits; ++sp) c[static_cast<size_t>(sp)] = expf_fixed(parts[sp].m[g] - tm);
       float tl = 0.0f;
-      for (int sp = 0; sp < splits; ++sp) softmax_combine(&tm, &tl, parts[sp].m[g], parts[sp].l[g]);
+      for (int sp = 0; sp < splits; ++sp) tl = std::fma(parts[sp].l[g], c[static_cast<size_t>(sp)], tl);
       const float inv = 1.0f / tl;
       for (int d = 0; d < hd; ++d) {
         float sum = 0.0f;
         for (int sp = 0; sp < splits; ++sp) {
-          sum = std::fma(expf_fixed(parts[sp].m[g] - tm), parts[sp].acc[static_cast<size_t>(g) * hd + d], sum);
+          sum = std::fma(c[static_cast<size_t>(sp)], parts[sp].acc[static_cast<size_t>(g) * hd + d], sum);
         }
         out[static_cast<size_t>(head) * hd + d] = f2e(sum * inv, kind);
       }

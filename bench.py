@@ -118,6 +118,63 @@ def cpu_baseline(model_dir: Path, prompt, steps: int, max_seq: int):
     }
 
 
+def prefill_flops(config: dict, T: int) -> float:
+    """Linear-layer and causal-attention FLOPs of a T-token prefill (the lm_head
+    runs on the last row only)."""
+    H, F, V = config["hidden_size"], config["intermediate_size"], config["vocab_size"]
+    L = config["num_hidden_layers"]
+    qkv_n = (config["num_attention_heads"] + 2 * config["num_key_value_heads"]) * config["head_dim"]
+    lin = 2.0 * T * (qkv_n * H + H * H + 2 * F * H + H * F) * L + 2.0 * V * H
+    attn = 2.0 * 2.0 * config["num_attention_heads"] * config["head_dim"] * T * (T + 1) / 2.0 * L
+    return lin + attn
+
+
+def long_context(lcr, model_dir: Path, config: dict, ctx: int, steps: int = 64) -> dict:
+    """paged cache (16-token pages, seeded random
+    page permutation) pre-filled with N(0, 1) at `ctx`, then `steps` greedy
+    decode steps on the graph; attention timed on its own as well."""
+    import numpy as np
+    layers = config["num_hidden_layers"]
+    m = lcr.Model(model_dir, max_seq=ctx + steps + 1, paged=1, page_size=16)
+    geo = m.kv_geometry()
+    m.fill_kv_normal(20260904 + ctx, 1.0)
+    tables = np.random.default_rng(ctx).permutation(layers * geo["max_pages"]).astype(np.int32)
+    m.set_kv_page_tables(tables, ctx)
+    m.set_position(ctx)
+    m.generate_greedy(1, 4)  # captures the graph for this split count
+    m.set_position(ctx)
+    _, ms = m.generate_greedy(1, steps)
+    att_ms, att_bytes = m.time_decode_kernel("attention", 16)
+    st = m.stats()
+    splits = m.decode_splits(ctx + steps // 2)
+    m.close()
+    mean_ctx = ctx + (steps + 1) / 2.0
+    token_bytes = st.weight_bytes_per_token + mean_ctx * st.kv_bytes_per_position
+    return {
+        "context": ctx, "decode_steps": steps, "splits": splits,
+        "ms_per_token": ms / steps, "tok_s": steps / (ms / 1000.0),
+        "token_gbs": token_bytes / (ms / steps / 1000.0) / 1e9,
+        "attention_us_per_layer": att_ms * 1000.0,
+        "attention_bytes_per_layer": att_bytes,
+        "attention_gbs": att_bytes / (att_ms / 1000.0) / 1e9,
+    }
+
+
+def prefill_run(lcr, model_dir: Path, config: dict, T: int) -> dict:
+    """one T-token prefill (chunks of 256 through the
+    MFMA GEMMs and the prefill attention), timed on the model's stream."""
+    ids = lcr.synthetic_tokens(T, config["vocab_size"], seed=lcr.PROMPT_SEED + T)
+    m = lcr.Model(model_dir, max_seq=T + 1)
+    m.prefill(ids)  # warm-up
+    m.reset()
+    m.prefill(ids)
+    ms = m.stats().last_prefill_ms
+    m.close()
+    tflops = prefill_flops(config, T) / (ms / 1000.0) / 1e12
+    return {"tokens": T, "ms": ms, "tok_s": T / (ms / 1000.0), "tflops": tflops,
+            "mfma_frac": tflops / BF16_DENSE_PEAK_TFLOPS}
+
+
 def counters_run(lcr, model_dir: Path, prompt, max_seq: int) -> int:
     """Eager work for a rocprofv3 --pmc pass: every fused decode kernel is a
     separate dispatch, plus a 256 MiB device-to-device copy whose counter
@@ -147,6 +204,7 @@ def main() -> int:
     ap.add_argument("--kernel-launches", type=int, default=64)
     ap.add_argument("--cpu-steps", type=int, default=256)
     ap.add_argument("--counters", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config 3 / config 4 measurements")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -214,18 +272,18 @@ def main() -> int:
     dom = kernels["gate_up"]
 
     # Prefill MFMA figures for the 128-token prompt.
-    H, F, V = config["hidden_size"], config["intermediate_size"], config["vocab_size"]
-    L = config["num_hidden_layers"]
-    qkv_n = (config["num_attention_heads"] + 2 * config["num_key_value_heads"]) * config["head_dim"]
     T = args.prompt
-    lin_flops = 2.0 * T * (qkv_n * H + H * H + 2 * F * H + H * F) * L + 2.0 * V * H
-    attn_flops = 2.0 * 2.0 * config["num_attention_heads"] * config["head_dim"] * T * (T + 1) / 2.0 * L
-    prefill_tflops = (lin_flops + attn_flops) / (prefill_ms / 1000.0) / 1e12
+    prefill_tflops = prefill_flops(config, T) / (prefill_ms / 1000.0) / 1e12
+    model.close()
+
+    extra = {}
+    if not args.no_extra:
+        extra["long_context"] = [long_context(lcr, model_dir, config, ctx) for ctx in (8192, 32768)]
+        extra["prefill_config4"] = [prefill_run(lcr, model_dir, config, t) for t in (512, 2048)]
 
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(model_dir, prompt, args.cpu_steps, args.max_seq)
-    model.close()
 
     result = {
         "metric": "decode tok/s + HBM GB/s (% of peak), Llama-3.2-1B-arch bf16 batch 1",
@@ -272,6 +330,7 @@ def main() -> int:
             "bytes_per_launch": dom["bytes_per_launch"],
         },
         "kernels": kernels,
+        **extra,
         "cpu_baseline": cpu,
         "generated_first_ids": [int(x) for x in ids[:8]],
         "setup_s": {"checkpoint": gen_s, "load": load_s},

@@ -109,6 +109,11 @@ int lcr_model_set_position(lcr_model* model, int position);
  * (layer, kv head, position). */
 int lcr_model_kv_read(const lcr_model* model, int layer, int head, int position, void* key_out,
                       void* value_out);
+/* Copies positions [0, positions) of every kv head of a layer, in logical
+ * order: out[head][position][head_dim] elements, whatever the layout (paged
+ * caches are gathered page by page through the page table). */
+int lcr_model_kv_export(const lcr_model* model, int layer, int positions, void* keys_out,
+                        void* values_out);
 
 /* extension: seeded random-init checkpoint (config.json + model.safetensors)
  * and seeded prompt ids; see llama-cuda-runtime_amd/csrc/synth.cpp. */

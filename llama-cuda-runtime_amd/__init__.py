@@ -172,6 +172,7 @@ SIGNATURES = {
     "lcr_model_fill_kv_normal": (_I, [_P, _U64, _F]),
     "lcr_model_set_position": (_I, [_P, _I]),
     "lcr_model_kv_read": (_I, [_P, _I, _I, _I, _P, _P]),
+    "lcr_model_kv_export": (_I, [_P, _I, _I, _P, _P]),
     "lcr_write_synthetic_checkpoint": (_I, [ctypes.c_char_p, ctypes.c_char_p, _U64, _F, _I, _I]),
     "lcr_synthetic_tokens": (_I, [_U64, _I, _I, _P]),
     "lcr_device_count": (_I, []),
@@ -475,4 +476,14 @@ class Model:
         v = np.zeros(head_dim, dtype=np.uint16)
         check(self.lib, self.lib.lcr_model_kv_read(self.handle, layer, head, position, k.ctypes.data,
                                                    v.ctypes.data), "kv_read")
+        return k, v
+
+    def kv_export(self, layer: int, positions: int, num_kv_heads: int, head_dim: int):
+        """Keys and values of positions [0, positions) of a layer, as uint16
+        element bits in logical [kv_head][position][head_dim] order."""
+        import numpy as np
+        k = np.zeros((num_kv_heads, positions, head_dim), dtype=np.uint16)
+        v = np.zeros((num_kv_heads, positions, head_dim), dtype=np.uint16)
+        check(self.lib, self.lib.lcr_model_kv_export(self.handle, layer, positions, k.ctypes.data,
+                                                     v.ctypes.data), "kv_export")
         return k, v

@@ -1,5 +1,7 @@
 // extern "C" wrapper of lcr::Model (include/lcr_model.h).
+#include <algorithm>
 #include <cstring>
+#include <vector>
 
 #include "../../include/lcr_model.h"
 #include "capi_util.h"
@@ -275,6 +277,52 @@ extern "C" int lcr_model_kv_read(const lcr_model* m, int layer, int head, int po
     const size_t bytes = static_cast<size_t>(v.head_dim) * sizeof(elem_t);
     if (key_out) HIP_CHECK(hipMemcpy(key_out, v.keys + offset, bytes, hipMemcpyDeviceToHost));
     if (value_out) HIP_CHECK(hipMemcpy(value_out, v.values + offset, bytes, hipMemcpyDeviceToHost));
+    return LCR_OK;
+  });
+}
+
+extern "C" int lcr_model_kv_export(const lcr_model* m, int layer, int positions, void* keys_out,
+                                   void* values_out) {
+  CAPI_MODEL(m);
+  const KvCache& kv = M(m).kv_cache();
+  const ModelConfig& c = M(m).config();
+  CAPI_CHECK(layer >= 0 && layer < c.num_layers, "layer " << layer << " out of range");
+  CAPI_CHECK(positions >= 0 && positions <= kv.length(),
+             "positions " << positions << " exceeds the cache length " << kv.length());
+  CAPI_CHECK(keys_out != nullptr && values_out != nullptr, "output buffers needed");
+  return capi::guarded([&]() -> int {
+    const KvCacheView v = kv.view(layer);
+    const int heads = c.num_kv_heads;
+    const size_t hd = static_cast<size_t>(v.head_dim);
+    auto* ko = static_cast<elem_t*>(keys_out);
+    auto* vo = static_cast<elem_t*>(values_out);
+    if (kv.layout() != KvLayout::kPaged) {
+      for (int h = 0; h < heads; ++h) {
+        const size_t bytes = static_cast<size_t>(positions) * hd * sizeof(elem_t);
+        HIP_CHECK(hipMemcpy(ko + h * positions * hd, v.keys + static_cast<size_t>(h) * v.head_stride, bytes,
+                            hipMemcpyDeviceToHost));
+        HIP_CHECK(hipMemcpy(vo + h * positions * hd, v.values + static_cast<size_t>(h) * v.head_stride, bytes,
+                            hipMemcpyDeviceToHost));
+      }
+      return LCR_OK;
+    }
+    std::vector<int32_t> table(static_cast<size_t>(kv.max_pages()));
+    HIP_CHECK(hipMemcpy(table.data(), v.page_table, table.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+    std::vector<elem_t> kpage(static_cast<size_t>(v.page_stride)), vpage(static_cast<size_t>(v.page_stride));
+    for (int p = 0; p * v.page_size < positions; ++p) {
+      const size_t phys = static_cast<size_t>(table[static_cast<size_t>(p)]);
+      HIP_CHECK(hipMemcpy(kpage.data(), v.keys + phys * v.page_stride, kpage.size() * sizeof(elem_t),
+                          hipMemcpyDeviceToHost));
+      HIP_CHECK(hipMemcpy(vpage.data(), v.values + phys * v.page_stride, vpage.size() * sizeof(elem_t),
+                          hipMemcpyDeviceToHost));
+      const int n = std::min(v.page_size, positions - p * v.page_size);
+      for (int h = 0; h < heads; ++h) {
+        const size_t dst = (static_cast<size_t>(h) * positions + static_cast<size_t>(p) * v.page_size) * hd;
+        const size_t src = static_cast<size_t>(h) * v.head_stride;
+        std::memcpy(ko + dst, kpage.data() + src, static_cast<size_t>(n) * hd * sizeof(elem_t));
+        std::memcpy(vo + dst, vpage.data() + src, static_cast<size_t>(n) * hd * sizeof(elem_t));
+      }
+    }
     return LCR_OK;
   });
 }

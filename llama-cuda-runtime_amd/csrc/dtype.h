@@ -49,12 +49,40 @@ __host__ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// fp16 conversions are written with integer operations, as the bf16 ones
+// are. With the hardware conversions the compiler merges a multiply and the
+// following f32 -> f16 rounding into one mixed-precision fma with a +0 addend,
+// which turns a -0 product into +0; here every product is rounded to f32 first
+// and the conversion cannot be merged, so device, host and oracle agree.
 __host__ __device__ __forceinline__ float half_bits_to_float(uint32_t b) {
-  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+  const uint32_t sign = (b & 0x8000u) << 16;
+  const uint32_t exp = (b >> 10) & 0x1fu;
+  const uint32_t man = b & 0x3ffu;
+  const uint32_t normal = sign | ((exp + 112u) << 23) | (man << 13);
+  const uint32_t special = sign | 0x7f800000u | (man << 13);  // inf / nan
+  // zero and subnormals: man * 2^-24, exact in float
+  const uint32_t small = sign | f32_as_u32(static_cast<float>(man) * 5.9604644775390625e-08f);
+  return u32_as_f32(exp == 0x1fu ? special : (exp == 0u ? small : normal));
 }
 
 __host__ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  const uint32_t u = f32_as_u32(f);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t a = u & 0x7fffffffu;
+  // normal: rebias the exponent, round the 13 dropped mantissa bits to even
+  const uint32_t h = (a >> 13) - (112u << 10);
+  const uint32_t rem = a & 0x1fffu;
+  const uint32_t normal = h + ((rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ? 1u : 0u);
+  // below the smallest normal (2^-14): round a * 2^24 (exact scaling) to even;
+  // the clamp only keeps the conversion defined for the inputs that take
+  // another branch
+  const uint32_t small =
+      static_cast<uint32_t>(__builtin_rintf(__builtin_fminf(u32_as_f32(a) * 16777216.0f, 2048.0f)));
+  const uint32_t mag = a > 0x7f800000u   ? 0x7e00u | ((a >> 13) & 0x3ffu)  // quiet nan
+                       : a >= 0x477ff000u ? 0x7c00u                         // rounds to inf
+                       : a < 0x38800000u  ? small
+                                          : normal;
+  return static_cast<uint16_t>(sign | mag);
 }
 
 #if defined(LCR_ELEM_FP16)

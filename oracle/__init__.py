@@ -112,6 +112,8 @@ SIGNATURES = {
     "orc_model_prefill": (_I, [_P, _P, _I, _I, _P]),
     "orc_model_tap": (ctypes.c_size_t, [_P, _I, _P, ctypes.c_size_t]),
     "orc_model_page_table": (_P, [_P, _I]),
+    "orc_model_set_kv": (_I, [_P, _I, _I, _P, _P]),
+    "orc_model_set_position": (_I, [_P, _I]),
     "orc_last_error": (ctypes.c_char_p, []),
 }
 
@@ -295,6 +297,19 @@ class OracleModel:
         out = np.empty(tokens * h, dtype=np.float32)
         n = self.lib.orc_model_tap(self.handle, index, ptr(out), out.size)
         return out[:n].reshape(-1, h)
+
+    def set_kv(self, layer: int, keys: np.ndarray, values: np.ndarray):
+        """Writes a layer's cache from logical [kv_head][position][head_dim]
+        element arrays (uint16 bits)."""
+        k = np.ascontiguousarray(keys, dtype=np.uint16)
+        v = np.ascontiguousarray(values, dtype=np.uint16)
+        assert k.shape == v.shape and k.ndim == 3
+        if self.lib.orc_model_set_kv(self.handle, layer, k.shape[1], ptr(k), ptr(v)) != 0:
+            raise RuntimeError(self.lib.orc_last_error().decode())
+
+    def set_position(self, position: int):
+        if self.lib.orc_model_set_position(self.handle, position) != 0:
+            raise RuntimeError(self.lib.orc_last_error().decode())
 
     def page_table(self, layer: int, max_pages: int) -> np.ndarray:
         p = self.lib.orc_model_page_table(self.handle, layer)

@@ -1030,6 +1030,38 @@ void orc_model_reset(orc_model* model) {
 }
 int orc_model_position(const orc_model* model) { return model->position; }
 
+// Test hooks for the long-context case: the cache is filled from outside (the
+// GPU's pre-filled cache, read back in logical order) and the position moved.
+int orc_model_set_kv(orc_model* m, int layer, int positions, const uint16_t* keys,
+                     const uint16_t* values) {
+  if (layer < 0 || layer >= m->cfg.num_layers || positions < 0 || positions > m->max_seq) {
+    g_error = "set_kv: layer or positions out of range";
+    return -1;
+  }
+  m->reserve(positions);
+  const orc_kv_view v = m->view(layer);
+  const int hd = m->cfg.head_dim;
+  for (int h = 0; h < m->cfg.num_kv_heads; ++h) {
+    for (int pos = 0; pos < positions; ++pos) {
+      const int64_t off = kv_off(v, m->paged, h, pos);
+      const size_t src = (static_cast<size_t>(h) * positions + pos) * hd;
+      std::memcpy(v.keys + off, keys + src, static_cast<size_t>(hd) * 2);
+      std::memcpy(v.values + off, values + src, static_cast<size_t>(hd) * 2);
+    }
+  }
+  return 0;
+}
+
+int orc_model_set_position(orc_model* m, int position) {
+  if (position < 0 || position > m->max_seq) {
+    g_error = "set_position: out of range";
+    return -1;
+  }
+  m->reserve(position);
+  m->position = position;
+  return 0;
+}
+
 int orc_model_decode(orc_model* m, int token, float* logits) {
   if (m->position >= m->max_seq) {
     g_error = "sequence reached the cache limit";

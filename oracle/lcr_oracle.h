@@ -142,6 +142,12 @@ int orc_model_prefill(orc_model* model, const int32_t* tokens, int count, int us
  * Returns the number of floats copied into out (capacity in floats). */
 size_t orc_model_tap(const orc_model* model, int index, float* out, size_t capacity);
 const int32_t* orc_model_page_table(const orc_model* model, int layer);
+/* Test hooks: writes positions [0, positions) of a layer's cache from logical
+ * [kv_head][position][head_dim] arrays; moves the position (the cache keeps
+ * its content). */
+int orc_model_set_kv(orc_model* model, int layer, int positions, const uint16_t* keys,
+                     const uint16_t* values);
+int orc_model_set_position(orc_model* model, int position);
 const char* orc_last_error(void);
 
 #ifdef __cplusplus

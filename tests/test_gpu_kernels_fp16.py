@@ -1,0 +1,123 @@
+"""The fp16 build (liblcr_amd_fp16.so) against the CPU oracle's fp16 kernels,
+bit for bit, plus signed-zero edge cases for both element types.
+
+The element type changes only the conversions, so these cases aim at them:
+exact cancellations (x + (-x) = +0 multiplied by a negative weight must give
+-0), -0 inputs, values that round to fp16 subnormals and to infinity. A
+compiler that merges a multiply with the following f32 -> f16 rounding into a
+mixed-precision fma with a +0 addend fails the cancellation case.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import BF16, FP16, dev, expect_bits_equal, host, p, random_elems, rng, zeros_dev
+
+pytestmark = pytest.mark.gpu
+
+KINDS = [pytest.param(BF16, "bf16", id="bf16"), pytest.param(FP16, "fp16", id="fp16")]
+
+
+def ok(lib, status, what):
+    if status != 0:
+        raise AssertionError(f"{what}: {lib.lcr_last_error_message().decode()}")
+
+
+@pytest.mark.parametrize("kind,variant", KINDS)
+def test_residual_norm_signed_zeros(gpu, lcr, kind, variant):
+    lib = lcr.load_library(variant)
+    ol = oracle.load()
+    r = rng(41)
+    tokens, dim = 3, 2048
+    x = random_elems(r, (tokens, dim), kind=kind)
+    d = random_elems(r, (tokens, dim), kind=kind)
+    w = random_elems(r, (dim,), 0.5, kind=kind)
+    d[0, :64] = x[0, :64] ^ 0x8000        # x + (-x) = +0
+    x[1, :8] = 0x8000                     # -0 + -0 = -0
+    d[1, :8] = 0x8000
+    xd = dev(x)
+    out = zeros_dev(tokens * dim)
+    ok(lib, lib.lcr_add_residual_rmsnorm(p(out), p(xd), p(dev(d)), p(dev(w)), tokens, dim, 1e-5, None),
+       "add_residual_rmsnorm")
+    xe = x.copy()
+    want = np.zeros(tokens * dim, dtype=np.uint16)
+    ol.orc_add_residual_rmsnorm(kind, want.ctypes.data, xe.ctypes.data, d.ctypes.data, w.ctypes.data, tokens,
+                                dim, 1e-5)
+    expect_bits_equal(host(out), want, f"{variant} residual+norm")
+    expect_bits_equal(host(xd), xe.ravel(), f"{variant} residual")
+    assert np.any(want == 0x8000), "the case should produce negative zeros"
+    # plain norm with -0 inputs
+    x2 = x.copy()
+    x2[2, :16] = 0x8000
+    out2 = zeros_dev(tokens * dim)
+    ok(lib, lib.lcr_rmsnorm(p(out2), p(dev(x2)), p(dev(w)), tokens, dim, 1e-5, None), "rmsnorm")
+    want2 = np.zeros(tokens * dim, dtype=np.uint16)
+    ol.orc_rmsnorm(kind, want2.ctypes.data, x2.ctypes.data, w.ctypes.data, tokens, dim, 1e-5)
+    expect_bits_equal(host(out2), want2, f"{variant} rmsnorm -0")
+
+
+@pytest.mark.parametrize("N,K,fp32_out", [(257, 2048, 0), (300, 8192, 1), (64, 520, 0)])
+def test_gemv_fp16(gpu, lcr, N, K, fp32_out):
+    lib = lcr.load_library("fp16")
+    ol = oracle.load()
+    r = rng(N + K)
+    W = random_elems(r, (N, K), 0.05, kind=FP16)
+    x = random_elems(r, (K,), kind=FP16)
+    x[:40] = 0x8000
+    y = zeros_dev(N * (2 if fp32_out else 1))
+    ok(lib, lib.lcr_gemv(p(y), fp32_out, p(dev(W)), p(dev(x)), N, K, None), "gemv")
+    if fp32_out:
+        want = np.zeros(N, dtype=np.float32)
+        ol.orc_gemv(FP16, want.ctypes.data, 1, W.ctypes.data, x.ctypes.data, N, K)
+        assert np.array_equal(host(y, np.float32)[:N].view(np.uint32), want.view(np.uint32))
+    else:
+        want = np.zeros(N, dtype=np.uint16)
+        ol.orc_gemv(FP16, want.ctypes.data, 0, W.ctypes.data, x.ctypes.data, N, K)
+        expect_bits_equal(host(y)[:N], want, "gemv fp16")
+
+
+def test_swiglu_rope_fp16_extremes(gpu, lcr):
+    lib = lcr.load_library("fp16")
+    ol = oracle.load()
+    r = rng(43)
+    n = 4099
+    g = oracle.f32_to_elems(np.concatenate([r.normal(0, 3, n - 6), [0.0, -0.0, 1e-6, -3e-7, 60000.0, -65504.0]])
+                            .astype(np.float32), FP16)
+    u = random_elems(r, (n,), 4.0, kind=FP16)
+    out = zeros_dev(n)
+    ok(lib, lib.lcr_swiglu(p(out), p(dev(g)), p(dev(u)), n, None), "swiglu")
+    want = np.zeros(n, dtype=np.uint16)
+    ol.orc_swiglu(FP16, want.ctypes.data, g.ctypes.data, u.ctypes.data, n)
+    expect_bits_equal(host(out)[:n], want, "swiglu fp16")
+
+    tokens, heads, hd = 3, 4, 64
+    q = random_elems(r, (tokens, heads * hd), kind=FP16)
+    q[0, :8] = 0x8000
+    inv = np.array([500000.0 ** (-2 * i / hd) for i in range(hd // 2)], dtype=np.float32)
+    qh = zeros_dev(tokens * heads * hd)
+    ok(lib, lib.lcr_rope_q(p(qh), p(dev(q)), p(dev(inv)), tokens, 11, heads, hd, heads * hd, None), "rope_q")
+    want = np.zeros(tokens * heads * hd, dtype=np.uint16)
+    ol.orc_rope_q(FP16, want.ctypes.data, q.ctypes.data, inv.ctypes.data, tokens, 11, heads, hd, heads * hd)
+    expect_bits_equal(host(qh)[:want.size], want, "rope_q fp16")
+
+
+def test_small_model_fp16_all_paths(gpu, lcr, tmp_path):
+    """The whole fp16 step (graph, eager and unfused) against the oracle."""
+    cfg = lcr.llama_config(num_hidden_layers=2, vocab_size=4096)
+    lcr.write_synthetic_checkpoint(tmp_path, cfg, seed=5, fp16=True)
+    prompt = [11, 22, 33, 44, 55, 66, 77]
+    for opts in ({}, {"use_graph": 0}, {"fused_decode": 0}):
+        m = lcr.Model(tmp_path, variant="fp16", max_seq=64, prefill_via_decode=1, **opts)
+        ref = oracle.OracleModel(tmp_path, kind=FP16, max_seq=64)
+        got = m.logits(m.prefill(prompt))
+        want = ref.prefill(prompt, use_decode_path=True)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), opts
+        tok = oracle.argmax(want)
+        for _ in range(3):
+            got = m.logits(m.decode(tok))
+            want = ref.decode(tok)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), opts
+            tok = oracle.argmax(want)
+        m.close()
+        ref.close()

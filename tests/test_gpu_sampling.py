@@ -1,0 +1,59 @@
+"""Stochastic sampling variant ("config 5"): the fp16
+build (liblcr_amd_fp16.so, the reference's -DLCR_DTYPE=fp16), the full-size
+model with fp16 seeded random-init weights, a paged cache of 16-token pages, a
+seeded 512-token prompt and 256 tokens sampled at temperature 0.8, top-k 40,
+top-p 0.95.
+
+The uniform draws come from one counter-based stream (Philox4x32-10, the
+published known-answer vectors are checked in test_host.py) fed to both the
+GPU sampler and the CPU oracle's, so with bit-identical logits (checked every
+step) the sampled ids must be identical. The sampler's own selection rules are
+pinned separately against a float64 brute force (test_oracle.py).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+PROMPT = 512
+STEPS = 256
+T, TOP_K, TOP_P = 0.8, 40, 0.95
+UNIFORM_SEED = 20260904
+
+
+@pytest.fixture(scope="module")
+def fp16_ckpt(lcr, tmp_path_factory):
+    d = tmp_path_factory.mktemp("fp16_model")
+    lcr.write_synthetic_checkpoint(d, lcr.llama_config(torch_dtype="float16"), seed=lcr.WEIGHT_SEED, fp16=True)
+    return d
+
+
+def test_fp16_paged_stochastic_sampling_matches_oracle(lcr, fp16_ckpt):
+    cfg = lcr.llama_config()
+    prompt = lcr.synthetic_tokens(PROMPT, cfg["vocab_size"], seed=lcr.PROMPT_SEED, variant="fp16")
+    uniforms = lcr.philox_uniforms(UNIFORM_SEED, STEPS)
+    max_seq = PROMPT + STEPS + 1
+    m = lcr.Model(fp16_ckpt, variant="fp16", max_seq=max_seq, paged=1, page_size=16, prefill_via_decode=1)
+    assert m.lib.lcr_elem_name() == b"fp16"
+    ref = oracle.OracleModel(fp16_ckpt, kind=oracle.FP16, max_seq=max_seq, paged=True, page_size=16,
+                             multiprocessors=m.stats().multiprocessors)
+    ptr = m.prefill(prompt)
+    want = ref.prefill(prompt, use_decode_path=True)
+    tokens = []
+    for step in range(STEPS):
+        got = m.logits(ptr)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"logits differ at step {step}"
+        u = uniforms[step]
+        tok = m.sample(ptr, T, TOP_K, TOP_P, u)
+        assert tok == oracle.sample(want, T, TOP_K, TOP_P, u), f"sampled id differs at step {step}"
+        tokens.append(tok)
+        if step + 1 < STEPS:
+            ptr = m.decode(tok)
+            want = ref.decode(tok)
+    # the draws really sample: not the greedy sequence, and several distinct ids
+    assert len(set(tokens)) > STEPS // 4
+    ref.close()
+    m.close()

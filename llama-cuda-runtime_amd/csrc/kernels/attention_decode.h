@@ -1,13 +1,15 @@
 // Split-K GQA decode attention for one query token, as a device routine shared
 // by the standalone launcher and the fused decode step.
 //
-// Work split. One 512-thread block (8 waves) per (query head, split): a query
-// head reads kv head head / group. Split s covers positions
+// Work split. One 512-thread block (8 waves) per (split, query heads): either
+// one query head (short contexts: the most, lightest blocks) or the whole GQA
+// group sharing a kv head (long contexts: each key/value loaded once for all
+// the group's heads). Split s covers positions
 // [s*chunk, min(seq_len, (s+1)*chunk)) with chunk = ceil(seq_len / splits), as
 // in the reference (src/kernels/attention.cu:129-133). The range is cut into
 // tiles of 64 positions; wave w takes tiles w, w+8, w+16, ... . Every value
-// below belongs to one query head, so how heads are spread over blocks cannot
-// change a result.
+// below belongs to one query head and no operation mixes heads, so how heads
+// are grouped into blocks cannot change a result.
 //
 // Tile layout. A position's key (or value) is head_dim/8 = P chunks of 16
 // bytes. Lane L holds chunk j = L % P of positions i*(64/P) + L/P for
@@ -66,14 +68,14 @@ __host__ __device__ __forceinline__ void softmax_combine(float* m, float* l, flo
   *m = merged;
 }
 
-template <int kHeadDim>
+template <int kHeadDim, int kHeads>
 struct AttnShared {
-  float probs[kAttnWaves][64];
-  float wave_m[kAttnWaves];
-  float wave_l[kAttnWaves];
-  float wave_acc[kAttnWaves][kHeadDim];
-  float scale[kAttnWaves];  // c_w of step 7
-  float merged_m;           // M of step 7
+  float probs[kAttnWaves][64 * kHeads];
+  float wave_m[kAttnWaves][kHeads];
+  float wave_l[kAttnWaves][kHeads];
+  float wave_acc[kAttnWaves][kHeads][kHeadDim];
+  float scale[kHeads][kAttnWaves];  // c_w of step 7
+  float merged_m[kHeads];           // M of step 7
 };
 
 // Step 3's reduce-scatter: at offset O the lane keeps the half of its N values
@@ -102,16 +104,20 @@ __device__ __forceinline__ float sum_over_groups(float v) {
   return v;
 }
 
-// One block: query head `head` reading kv head `kv_head`, over split `split`
-// of `splits` (split < splits). `q` holds num_heads * kHeadDim elements (head
-// h at h * kHeadDim). Writes out (splits == 1) or partials[head][split].
-template <bool kPaged, int kHeadDim>
+// One block: query heads head0 .. head0 + kHeads - 1 (all reading kv head
+// `kv_head`) over split `split` of `splits` (split < splits). One head per
+// block gives short contexts the most blocks; a whole GQA group per block
+// loads each key/value once for all its heads, which is what long contexts,
+// bound by the cache bytes, need. `q` holds num_heads * kHeadDim elements
+// (head h at h * kHeadDim). Writes out (splits == 1) or partials[head][split].
+template <bool kPaged, int kHeadDim, int kHeads>
 __device__ __forceinline__ void decode_attention_block(
-    AttnShared<kHeadDim>& sh, elem_t* __restrict__ out, float* __restrict__ partials,
-    const elem_t* __restrict__ q, const KvCacheView& view, int kv_head, int head, int split,
+    AttnShared<kHeadDim, kHeads>& sh, elem_t* __restrict__ out, float* __restrict__ partials,
+    const elem_t* __restrict__ q, const KvCacheView& view, int kv_head, int head0, int split,
     int splits, int seq_len, float scale) {
   constexpr int P = kHeadDim / 8;   // chunks per position
   constexpr int Q = 64 / P;         // positions per load instruction
+  constexpr int G = kHeads;
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) >> 6;
   const int j = lane % P;
@@ -122,17 +128,23 @@ __device__ __forceinline__ void decode_attention_block(
   const int end = min(seq_len, begin + chunk);
   const int length = max(0, end - begin);
 
-  float qv[8];
-  {
-    const vec16 raw = load16(q + static_cast<size_t>(head) * kHeadDim + 8 * j);
-    unpack8(raw, qv);
+  float qv[G][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qv[e] *= scale;
+  for (int g = 0; g < G; ++g) {
+    const vec16 raw = load16(q + static_cast<size_t>(head0 + g) * kHeadDim + 8 * j);
+    unpack8(raw, qv[g]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[g][e] *= scale;
   }
 
-  float m = kSoftmaxIdentity, l_lane = 0.0f, acc[8];
+  float m[G], l_lane[G], acc[G][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int g = 0; g < G; ++g) {
+    m[g] = kSoftmaxIdentity;
+    l_lane[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+  }
 
   // Requests the P chunks this lane holds of tile `tile`. Every load is
   // issued (positions past the range are clamped to the last valid one), so
@@ -149,112 +161,230 @@ __device__ __forceinline__ void decode_attention_block(
     }
   };
 
-  auto process_tile = [&](int tile, const vec16 (&kr)[P], const vec16 (&vr)[P]) {
+  // Steps 2-4 for one tile: scores, the online softmax update, and the
+  // probabilities into LDS; returns nothing, leaves r[] for step 5.
+  float r[G];
+  auto score_tile = [&](int tile, const vec16 (&kr)[P]) {
     const int count = min(kAttnTile, end - (begin + tile * kAttnTile));
-    // Step 2: partial dots (positions past the range contribute zeros).
-    float vals[P];
+    // Step 2: partial dots (positions past the range contribute zeros), value
+    // index i * G + g.
+    float vals[P * G];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
       const bool keep = i * Q + a < count;
       float kf[8];
       unpack8(kr[i], kf);
-      float d = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = __builtin_fmaf(qv[e], keep ? kf[e] : 0.0f, d);
-      vals[i] = d;
+      for (int e = 0; e < 8; ++e) kf[e] = keep ? kf[e] : 0.0f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = __builtin_fmaf(qv[g][e], kf[e], d);
+        vals[i * G + g] = d;
+      }
     }
     // Step 3.
-    reduce_scatter<P / 2, P>(vals, lane);
+    reduce_scatter<P / 2, P * G>(vals, lane);
     const int own = j * Q + a;  // owned position index within the tile
-    const float s = own < count ? vals[0] : kSoftmaxIdentity;
     // Step 4.
-    const float mnew = fmaxf(m, wave_max(s));
-    const float r = lcr_expf(m - mnew);
-    const float p = lcr_expf(s - mnew);
-    l_lane = __builtin_fmaf(l_lane, r, p);
-    m = mnew;
-    sh.probs[wave][lane] = p;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // Step 5.
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = acc[e] * r;
-    const float* pr = &sh.probs[wave][a * P];
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
-      const bool keep = i * Q + a < count;
-      float vf[8];
-      unpack8(vr[i], vf);
-      const float pi = pr[i];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(pi, keep ? vf[e] : 0.0f, acc[e]);
+    for (int g = 0; g < G; ++g) {
+      const float s = own < count ? vals[g] : kSoftmaxIdentity;
+      const float mnew = fmaxf(m[g], wave_max(s));
+      r[g] = lcr_expf(m[g] - mnew);
+      const float p = lcr_expf(s - mnew);
+      l_lane[g] = __builtin_fmaf(l_lane[g], r[g], p);
+      m[g] = mnew;
+      sh.probs[wave][lane * G + g] = p;
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
+  // Step 5 for one tile.
+  auto value_tile = [&](int tile, const vec16 (&vr)[P]) {
+    const int count = min(kAttnTile, end - (begin + tile * kAttnTile));
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] = acc[g][e] * r[g];
+    }
+    const float* pr = &sh.probs[wave][a * P * G];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const bool keep = i * Q + a < count;
+      float vf[8];
+      unpack8(vr[i], vf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vf[e] = keep ? vf[e] : 0.0f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pi = pr[i * G + g];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = __builtin_fmaf(pi, vf[e], acc[g][e]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  auto load_keys = [&](int tile, vec16 (&kr)[P]) {
+    const int tile_begin = begin + tile * kAttnTile;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int pos = min(tile_begin + i * Q + a, end - 1);
+      kr[i] = load16(view.keys + view.offset<kPaged>(kv_head, pos) + 8 * j);
+    }
+  };
+  auto load_values = [&](int tile, vec16 (&vr)[P]) {
+    const int tile_begin = begin + tile * kAttnTile;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int pos = min(tile_begin + i * Q + a, end - 1);
+      vr[i] = load16(view.values + view.offset<kPaged>(kv_head, pos) + 8 * j);
+    }
+  };
 
-  // Tiles wave, wave + 8, ...: two register sets, the next tile's loads in
-  // flight while the current one is processed.
+  // Tiles wave, wave + 8, ... . One head per block: two register sets, the
+  // next tile's loads in flight while the current one is processed. A group
+  // per block needs its registers for the heads, so it keeps one set and
+  // refills the keys as soon as the scores are taken and the values as soon
+  // as they are used.
   if (wave * kAttnTile < length) {
-    vec16 ka[P], va[P], kb[P], vb[P];
-    int tile = wave;
-    load_tile(tile, ka, va);
-    while (true) {
-      const int t1 = tile + kAttnWaves;
-      const bool more1 = t1 * kAttnTile < length;
-      if (more1) load_tile(t1, kb, vb);
-      process_tile(tile, ka, va);
-      if (!more1) break;
-      const int t2 = t1 + kAttnWaves;
-      const bool more2 = t2 * kAttnTile < length;
-      if (more2) load_tile(t2, ka, va);
-      process_tile(t1, kb, vb);
-      if (!more2) break;
-      tile = t2;
+    if constexpr (G == 1) {
+      // The single-head tile, steps 2-5 in one pass (the same arithmetic as
+      // score_tile + value_tile, in the instruction order that runs fastest
+      // for the latency-bound short-context case).
+      auto process_tile = [&](int tile, const vec16 (&kr)[P], const vec16 (&vr)[P]) {
+        const int count = min(kAttnTile, end - (begin + tile * kAttnTile));
+        float vals[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+          const bool keep = i * Q + a < count;
+          float kf[8];
+          unpack8(kr[i], kf);
+          float d = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d = __builtin_fmaf(qv[0][e], keep ? kf[e] : 0.0f, d);
+          vals[i] = d;
+        }
+        reduce_scatter<P / 2, P>(vals, lane);
+        const int own = j * Q + a;
+        const float s = own < count ? vals[0] : kSoftmaxIdentity;
+        const float mnew = fmaxf(m[0], wave_max(s));
+        const float rr = lcr_expf(m[0] - mnew);
+        const float p = lcr_expf(s - mnew);
+        l_lane[0] = __builtin_fmaf(l_lane[0], rr, p);
+        m[0] = mnew;
+        sh.probs[wave][lane] = p;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[0][e] = acc[0][e] * rr;
+        const float* pr = &sh.probs[wave][a * P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+          const bool keep = i * Q + a < count;
+          float vf[8];
+          unpack8(vr[i], vf);
+          const float pi = pr[i];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[0][e] = __builtin_fmaf(pi, keep ? vf[e] : 0.0f, acc[0][e]);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      };
+      vec16 ka[P], va[P], kb[P], vb[P];
+      int tile = wave;
+      load_tile(tile, ka, va);
+      while (true) {
+        const int t1 = tile + kAttnWaves;
+        const bool more1 = t1 * kAttnTile < length;
+        if (more1) load_tile(t1, kb, vb);
+        process_tile(tile, ka, va);
+        if (!more1) break;
+        const int t2 = t1 + kAttnWaves;
+        const bool more2 = t2 * kAttnTile < length;
+        if (more2) load_tile(t2, ka, va);
+        process_tile(t1, kb, vb);
+        if (!more2) break;
+        tile = t2;
+      }
+    } else {
+      vec16 kr[P], vr[P];
+      int tile = wave;
+      load_keys(tile, kr);
+      load_values(tile, vr);
+      while (true) {
+        const int next = tile + kAttnWaves;
+        const bool more = next * kAttnTile < length;
+        score_tile(tile, kr);
+        if (more) load_keys(next, kr);
+        value_tile(tile, vr);
+        if (!more) break;
+        load_values(next, vr);
+        tile = next;
+      }
     }
   }
 
   // Step 6.
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = sum_over_groups<P>(acc[e]);
-  l_lane = wave_sum(l_lane);
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = sum_over_groups<P>(acc[g][e]);
+    l_lane[g] = wave_sum(l_lane[g]);
+  }
   if (lane < P) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sh.wave_acc[wave][8 * lane + e] = acc[e];
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sh.wave_acc[wave][g][8 * lane + e] = acc[g][e];
+    }
   }
   if (lane == 0) {
-    sh.wave_m[wave] = m;
-    sh.wave_l[wave] = l_lane;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      sh.wave_m[wave][g] = m[g];
+      sh.wave_l[wave][g] = l_lane[g];
+    }
   }
   __syncthreads();
 
-  // Step 7: the wave factors in parallel, then every output element.
-  if (threadIdx.x < kAttnWaves) {
-    float tm = sh.wave_m[0];
+  // Step 7: the wave factors of every head in parallel, then every output.
+  if (static_cast<int>(threadIdx.x) < G * kAttnWaves) {
+    const int g = threadIdx.x / kAttnWaves;
+    const int w = threadIdx.x % kAttnWaves;
+    float tm = sh.wave_m[0][g];
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) tm = fmaxf(tm, sh.wave_m[w]);
-    sh.scale[threadIdx.x] = lcr_expf(sh.wave_m[threadIdx.x] - tm);
-    if (threadIdx.x == 0) sh.merged_m = tm;
+    for (int v = 1; v < kAttnWaves; ++v) tm = fmaxf(tm, sh.wave_m[v][g]);
+    sh.scale[g][w] = lcr_expf(sh.wave_m[w][g] - tm);
+    if (w == 0) sh.merged_m[g] = tm;
   }
   __syncthreads();
-  if (threadIdx.x < kHeadDim) {
-    const int d = threadIdx.x;
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kAttnThreads) {
+    const int g = idx / kHeadDim;
+    const int d = idx % kHeadDim;
     float tl = 0.0f, merged = 0.0f;
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) {
-      tl = __builtin_fmaf(sh.wave_l[w], sh.scale[w], tl);
-      merged = __builtin_fmaf(sh.scale[w], sh.wave_acc[w][d], merged);
+      tl = __builtin_fmaf(sh.wave_l[w][g], sh.scale[g][w], tl);
+      merged = __builtin_fmaf(sh.scale[g][w], sh.wave_acc[w][g][d], merged);
     }
+    const int head = head0 + g;
     if (splits == 1) {
       out[static_cast<size_t>(head) * kHeadDim + d] = float_to_elem(merged * (1.0f / tl));
     } else {
       float* slot = partials + (static_cast<size_t>(head) * splits + split) * (kPartialHeader + kHeadDim);
       if (d == 0) {
-        slot[0] = sh.merged_m;
+        slot[0] = sh.merged_m[g];
         slot[1] = tl;
       }
       slot[kPartialHeader + d] = merged;
@@ -262,36 +392,37 @@ __device__ __forceinline__ void decode_attention_block(
   }
 }
 
-// Merge of the split partials of one query head (step 8). Every thread of the
-// block calls it (it synchronises the block); `lds` holds 2 + kMaxSplits
-// floats.
+// Merge of the split partials of one query head (step 8), by a block of
+// kMergeThreads threads. The partials are first copied into LDS with every
+// thread loading (they come from other XCDs' writes, so each load is a trip to
+// the memory side; issued together they cost one such trip, not one per
+// split), then folded from LDS in split order.
+constexpr int kMergeThreads = 256;
+constexpr int kMaxHeadDim = 128;
+constexpr int kMergeLdsFloats = kMaxSplits * (kPartialHeader + kMaxHeadDim) + kMaxSplits;
+
 __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
                                                      const float* __restrict__ partials, int head,
                                                      int splits, int head_dim, float* lds) {
   const int stride = kPartialHeader + head_dim;
   const float* base = partials + static_cast<size_t>(head) * splits * stride;
-  if (threadIdx.x == 0) {
-    float tm = base[0];
-    for (int s = 1; s < splits; ++s) tm = fmaxf(tm, base[s * stride]);
-    lds[0] = tm;
+  const int n = splits * stride;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) lds[i] = base[i];
+  __syncthreads();
+  float* c = lds + kMaxSplits * (kPartialHeader + kMaxHeadDim);
+  if (static_cast<int>(threadIdx.x) < splits) {
+    float tm = lds[0];
+    for (int s = 1; s < splits; ++s) tm = fmaxf(tm, lds[s * stride]);
+    c[threadIdx.x] = lcr_expf(lds[threadIdx.x * stride] - tm);
   }
   __syncthreads();
-  const float tm = lds[0];
-  for (int s = threadIdx.x; s < splits; s += blockDim.x) lds[2 + s] = lcr_expf(base[s * stride] - tm);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float tl = 0.0f;
-    for (int s = 0; s < splits; ++s) tl = __builtin_fmaf(base[s * stride + 1], lds[2 + s], tl);
-    lds[1] = tl;
-  }
-  __syncthreads();
-  const float inv = 1.0f / lds[1];
   for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
-    float sum = 0.0f;
+    float tl = 0.0f, sum = 0.0f;
     for (int s = 0; s < splits; ++s) {
-      sum = __builtin_fmaf(lds[2 + s], base[s * stride + kPartialHeader + d], sum);
+      tl = __builtin_fmaf(lds[s * stride + 1], c[s], tl);
+      sum = __builtin_fmaf(c[s], lds[s * stride + kPartialHeader + d], sum);
     }
-    out[static_cast<size_t>(head) * head_dim + d] = float_to_elem(sum * inv);
+    out[static_cast<size_t>(head) * head_dim + d] = float_to_elem(sum * (1.0f / tl));
   }
   __syncthreads();
 }

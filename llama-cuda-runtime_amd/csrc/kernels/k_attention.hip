@@ -23,14 +23,15 @@ template <bool kPaged, int kHeadDim, int kGroup>
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
     elem_t* __restrict__ out, float* __restrict__ partials, const elem_t* __restrict__ q,
     KvCacheView view, int seq_len, float scale, int splits) {
-  __shared__ AttnShared<kHeadDim> sh;
-  decode_attention_block<kPaged, kHeadDim>(sh, out, partials, q, view, blockIdx.x / kGroup,
+  __shared__ AttnShared<kHeadDim, 1> sh;
+  decode_attention_block<kPaged, kHeadDim, 1>(sh, out, partials, q, view, blockIdx.x / kGroup,
                                            blockIdx.x, blockIdx.y, splits, seq_len, scale);
 }
 
-__global__ void merge_splits_kernel(elem_t* __restrict__ out, const float* __restrict__ partials,
-                                    int splits, int head_dim) {
-  __shared__ float lds[2 + kMaxSplits];
+__global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(elem_t* __restrict__ out,
+                                                                   const float* __restrict__ partials,
+                                                                   int splits, int head_dim) {
+  __shared__ float lds[kMergeLdsFloats];
   merge_split_partials(out, partials, blockIdx.x, splits, head_dim, lds);
 }
 
@@ -114,7 +115,7 @@ int launch_decode(const DecodeArgs& a) {
       a.out, a.partials, a.q, a.view, a.seq_len, a.scale, a.splits);
   CAPI_LAUNCHED();
   if (a.splits > 1) {
-    merge_splits_kernel<<<a.num_heads, 64, 0, a.stream>>>(a.out, a.partials, a.splits, kHeadDim);
+    merge_splits_kernel<<<a.num_heads, kMergeThreads, 0, a.stream>>>(a.out, a.partials, a.splits, kHeadDim);
     CAPI_LAUNCHED();
   }
   return LCR_OK;

@@ -19,6 +19,12 @@ constexpr int kLmHeadMaxBlocks = 1024;
 constexpr int kLmHeadRows = 2;  // rows per wave per group
 constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
 constexpr int kDownWaves = 1;   // waves (rows) per down block
+// Largest GQA group one attention block serves (register budget: the group's
+// q, scores and accumulators next to two key/value tiles per lane).
+constexpr int kMaxGroupedHeads = 4;
+// From this many splits on (the model's policy gives them to contexts of 16384
+// and more) attention runs one block per (kv head, split) for the whole group.
+constexpr int kGroupedMinSplits = 16;
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + lcr_expf(-v)); }
 
@@ -210,27 +216,35 @@ __device__ __forceinline__ void attention_block_coords(int b, int units, int gro
   }
 }
 
-template <bool kPaged, int HD, int G>
+// kHeads = 1: one block per (query head, split), numbered so the blocks of a
+// kv head share an XCD. kHeads = G: one block per (kv head, split) for the
+// whole group.
+template <bool kPaged, int HD, int G, int kHeads>
 __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStepArgs a,
                                                                       KvCacheView view,
                                                                       float scale) {
-  __shared__ AttnShared<HD> sh;
+  __shared__ AttnShared<HD, kHeads> sh;
   const int seq_len = *a.position + 1;
   const int splits = min(a.splits, seq_len);
-  int unit, g;
-  attention_block_coords(blockIdx.x, a.num_kv_heads * a.splits, G, &unit, &g);
+  int unit, g = 0;
+  if (kHeads == 1) {
+    attention_block_coords(blockIdx.x, a.num_kv_heads * a.splits, G, &unit, &g);
+  } else {
+    unit = blockIdx.x;
+  }
   const int kv_head = unit / a.splits;
   const int split = unit % a.splits;
   // A graph captured for more splits than this position can use: the extra
   // blocks have no range and must not touch the partials of other heads.
   if (split >= splits) return;
-  decode_attention_block<kPaged, HD>(sh, a.attn, a.partials, a.q, view, kv_head, kv_head * G + g,
-                                        split, splits, seq_len, scale);
+  decode_attention_block<kPaged, HD, kHeads>(sh, a.attn, a.partials, a.q, view, kv_head,
+                                             kv_head * G + g, split, splits, seq_len, scale);
 }
 
-// Split merge (splits > 1 only), one 64-thread block per query head.
-__global__ __launch_bounds__(64) void attention_merge_step_kernel(DecodeStepArgs a, int head_dim) {
-  __shared__ float lds[2 + kMaxSplits];
+// Split merge (splits > 1 only), one kMergeThreads-thread block per query head.
+__global__ __launch_bounds__(kMergeThreads) void attention_merge_step_kernel(DecodeStepArgs a,
+                                                                            int head_dim) {
+  __shared__ float lds[kMergeLdsFloats];
   const int splits = min(a.splits, *a.position + 1);
   if (splits <= 1) {
     // The attention blocks wrote the output directly. (The merge of one split
@@ -400,11 +414,16 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
   }
   if (mask & kDecodeAttention) {
     const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
-    attention_step_kernel<kPaged, HD, G>
-        <<<a.num_kv_heads * a.splits * G, kAttnThreads, 0, s>>>(a, view, scale);
+    if (a.splits >= kGroupedMinSplits && G <= kMaxGroupedHeads) {
+      attention_step_kernel<kPaged, HD, G, (G <= kMaxGroupedHeads ? G : 1)>
+          <<<a.num_kv_heads * a.splits, kAttnThreads, 0, s>>>(a, view, scale);
+    } else {
+      attention_step_kernel<kPaged, HD, G, 1>
+          <<<a.num_kv_heads * a.splits * G, kAttnThreads, 0, s>>>(a, view, scale);
+    }
     HIP_CHECK_LAUNCH();
     if (a.splits > 1) {
-      attention_merge_step_kernel<<<a.num_heads, 64, 0, s>>>(a, HD);
+      attention_merge_step_kernel<<<a.num_heads, kMergeThreads, 0, s>>>(a, HD);
       HIP_CHECK_LAUNCH();
     }
   }

@@ -220,10 +220,31 @@ void Model::reset() {
   taps_.clear();
 }
 
+// The split count of the decode step. The reference sizes it for one block
+// per (kv head, split), two per multiprocessor (src/kernels/attention.cu:
+// 419-431). Here, as measured on MI355X:
+//  - below 4096 positions, a single split: one 8-wave block per query head,
+//    up to 8 tiles per wave, no merge pass;
+//  - below 16384, ceil(CUs / num_heads) splits of per-query-head blocks
+//    (about one block per compute unit);
+//  - from 16384 on the step is bound by the cache bytes: ceil(CUs /
+//    num_kv_heads) splits, which the kernel runs as one block per (kv head,
+//    split) loading each key and value once for the whole group.
+// Always at least 512 positions (one 64-position tile per wave) per split and
+// at most 64 splits.
+static int decode_attention_splits(int num_heads, int num_kv_heads, int seq_len, int compute_units) {
+  if (seq_len < 4096) return 1;
+  const int per = seq_len < 16384 ? std::max(1, num_heads) : std::max(1, num_kv_heads);
+  const int want = std::max(1, (compute_units + per - 1) / per);
+  const int useful = std::max(1, seq_len / 512);
+  return std::max(1, std::min(std::min(want, useful), kMaxAttentionSplits));
+}
+
 int Model::decode_splits(int seq_len) const {
   const int s = options_.attention_splits > 0
                     ? std::min(options_.attention_splits, kMaxAttentionSplits)
-                    : choose_attention_splits(config_.num_kv_heads, seq_len, multiprocessors_);
+                    : decode_attention_splits(config_.num_heads, config_.num_kv_heads, seq_len,
+                                              multiprocessors_);
   return std::max(1, std::min(s, seq_len));
 }
 

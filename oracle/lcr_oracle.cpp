@@ -678,6 +678,18 @@ int orc_choose_attention_splits(int num_kv_heads, int seq_len, int multiprocesso
   return std::max(1, std::min(splits, 64));
 }
 
+// The model's split policy (llama-cuda-runtime_amd/csrc/model.cpp,
+// decode_attention_splits): one split below 4096 positions; below 16384,
+// ceil(CUs / num_heads) splits; from 16384, ceil(CUs / num_kv_heads); always
+// at least 512 positions per split and at most 64 splits.
+int orc_decode_step_splits(int num_heads, int num_kv_heads, int seq_len, int multiprocessors) {
+  if (seq_len < 4096) return 1;
+  const int per = seq_len < 16384 ? std::max(1, num_heads) : std::max(1, num_kv_heads);
+  const int want = std::max(1, (multiprocessors + per - 1) / per);
+  const int useful = std::max(1, seq_len / 512);
+  return std::max(1, std::min(std::min(want, useful), 64));
+}
+
 void orc_decode_attention(int kind, uint16_t* out, const uint16_t* q, const orc_kv_view* view,
                           int num_heads, int heads_per_kv, int seq_len, float scale, int paged,
                           int splits) {
@@ -948,7 +960,8 @@ struct orc_model {
       if (tokens == 1) {
         const int seq = start + 1;
         const int splits = forced_splits > 0 ? std::min(forced_splits, 64)
-                                             : orc_choose_attention_splits(cfg.num_kv_heads, seq, multiprocessors);
+                                             : orc_decode_step_splits(cfg.num_heads, cfg.num_kv_heads, seq,
+                                                                      multiprocessors);
         orc_decode_attention(kind, attn.data(), qh.data(), &vw, cfg.num_heads, G, seq, scale, paged, splits);
       } else {
         orc_prefill_attention(kind, attn.data(), qh.data(), &vw, cfg.num_heads, G, tokens, start, scale, paged);

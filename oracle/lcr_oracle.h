@@ -142,6 +142,11 @@ int orc_model_prefill(orc_model* model, const int32_t* tokens, int count, int us
  * Returns the number of floats copied into out (capacity in floats). */
 size_t orc_model_tap(const orc_model* model, int index, float* out, size_t capacity);
 const int32_t* orc_model_page_table(const orc_model* model, int layer);
+/* Split count of the whole-model decode step (both the HIP model and this
+ * oracle use it): 1 below 4096 positions; below 16384 ceil(CUs / num_heads);
+ * from 16384 ceil(CUs / num_kv_heads); at least 512 positions per split, at
+ * most 64 splits. */
+int orc_decode_step_splits(int num_heads, int num_kv_heads, int seq_len, int multiprocessors);
 /* Test hooks: writes positions [0, positions) of a layer's cache from logical
  * [kv_head][position][head_dim] arrays; moves the position (the cache keeps
  * its content). */

@@ -6,8 +6,9 @@ context 8192 and 32768, then decoded greedily.
 The GPU's cache is read back in logical order (lcr_model_kv_export) and loaded
 into the CPU oracle, so both sides attend over the same values; every step's
 fp32 logits must then be bit-identical, which also pins the page indexing and
-the split-K attention at 32 and 64 splits (the split count the reference's
-heuristic picks for these lengths on 256 compute units).
+the split-K attention and its merge (on 256 compute units: 8 splits of
+per-query-head blocks at 8192, 32 splits of whole-group blocks at 32768), and
+a forced 64-split run (the reference heuristic's count at 32768).
 """
 
 from pathlib import Path
@@ -35,12 +36,12 @@ def permuted_tables(layers: int, max_pages: int, seed: int) -> np.ndarray:
     return np.random.default_rng(seed).permutation(layers * max_pages).astype(np.int32).reshape(layers, max_pages)
 
 
-@pytest.mark.parametrize("ctx", [8192, 32768])
-def test_long_context_paged_decode_matches_oracle(lcr, ckpt, ctx):
+@pytest.mark.parametrize("ctx,forced", [(8192, 0), (32768, 0), (32768, 64)])
+def test_long_context_paged_decode_matches_oracle(lcr, ckpt, ctx, forced):
     cfg = lcr.llama_config()
     layers, kvh, hd = cfg["num_hidden_layers"], cfg["num_key_value_heads"], cfg["head_dim"]
     max_seq = ctx + STEPS
-    m = lcr.Model(ckpt, max_seq=max_seq, paged=1, page_size=16)
+    m = lcr.Model(ckpt, max_seq=max_seq, paged=1, page_size=16, attention_splits=forced)
     geo = m.kv_geometry()
     assert geo["pool_pages"] == layers * geo["max_pages"]
     m.fill_kv_normal(20260904 + ctx, 1.0)
@@ -49,9 +50,10 @@ def test_long_context_paged_decode_matches_oracle(lcr, ckpt, ctx):
     m.set_position(ctx)
     assert np.array_equal(m.kv_page_table(5), tables[5])
     splits = m.decode_splits(ctx + 1)
-    assert splits == {8192: 32, 32768: 64}[ctx] or m.stats().multiprocessors != 256
+    assert splits == (forced or {8192: 8, 32768: 32}[ctx]) or m.stats().multiprocessors != 256
 
-    ref = oracle.OracleModel(ckpt, max_seq=max_seq, multiprocessors=m.stats().multiprocessors)
+    ref = oracle.OracleModel(ckpt, max_seq=max_seq, multiprocessors=m.stats().multiprocessors,
+                             attention_splits=forced)
     for layer in range(layers):
         k, v = m.kv_export(layer, ctx, kvh, hd)
         if layer == 0:

@@ -161,8 +161,8 @@ def long_context(lcr, model_dir: Path, config: dict, ctx: int, steps: int = 64) 
 
 
 def prefill_run(lcr, model_dir: Path, config: dict, T: int) -> dict:
-    """one T-token prefill (chunks of 256 through the
-    MFMA GEMMs and the prefill attention), timed on the model's stream."""
+    """one T-token prefill (one chunk through the
+    MFMA GEMMs and the MFMA prefill attention), timed on the model's stream."""
     ids = lcr.synthetic_tokens(T, config["vocab_size"], seed=lcr.PROMPT_SEED + T)
     m = lcr.Model(model_dir, max_seq=T + 1)
     m.prefill(ids)  # warm-up

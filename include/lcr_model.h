@@ -30,7 +30,7 @@ typedef struct lcr_model_options {
   int max_seq;
   int paged;            /* KvLayout::kPaged when non-zero */
   int page_size;
-  int prefill_chunk;
+  int prefill_chunk;    /* tokens per prefill pass (default 2048; the reference's is 256) */
   int attention_splits; /* 0 = choose from sequence length and CU count */
   int fused_decode;     /* extension: fused decode kernels (default 1) */
   int use_graph;        /* extension: replay the decode step from a hipGraph (default 1) */

@@ -33,7 +33,7 @@ extern "C" void lcr_model_default_options(lcr_model_options* o) {
   o->max_seq = 4096;
   o->paged = 0;
   o->page_size = 16;
-  o->prefill_chunk = 256;
+  o->prefill_chunk = 2048;
   o->attention_splits = 0;
   o->fused_decode = 1;
   o->use_graph = 1;

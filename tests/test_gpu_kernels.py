@@ -345,29 +345,50 @@ def test_gemv(gpu, orc, N, K, fp32_out):
         expect_bits_equal(got, exp, f"gemv {N}x{K}")
 
 
-@pytest.mark.parametrize("T,N,K", [(128, 3072, 2048), (37, 2048, 8192), (256, 16384, 2048), (5, 100, 64)])
+GEMM_CASES = [
+    # (T, N, K): the model's projections at prefill sizes, then ragged edges
+    (128, 3072, 2048), (37, 2048, 8192), (256, 16384, 2048), (5, 100, 64),
+    (2048, 3072, 2048), (512, 2048, 8192), (300, 2048, 2048), (1000, 520, 72), (33, 1001, 136),
+]
+
+
+@pytest.mark.parametrize("T,N,K", GEMM_CASES)
 def test_gemm_mfma(gpu, orc, T, N, K):
+    """Every tile shape (256x256 for the bf16 output of large problems,
+    256x128 and 128x128 otherwise) against a float64 product; K tails that
+    end mid-stage, token and feature counts that end mid-tile, and N that is
+    not a multiple of 4 (scalar epilogue)."""
     lib = gpu
-    r = rng(T * N)
+    r = rng(T * N + K)
     X = random_elems(r, (T, K))
     W = random_elems(r, (N, K), 0.02)
+    Xd, Wd = dev(X), dev(W)
+    exp = to_f32(X).astype(np.float64) @ to_f32(W).astype(np.float64).T
     Y = zeros_dev(T * N, np.float32)
-    ok(lib, lib.lcr_gemm(p(Y), 1, p(dev(X)), p(dev(W)), T, N, K, NULL), "gemm")
-    Xf = to_f32(X).astype(np.float64)
-    Wf = to_f32(W).astype(np.float64)
-    exp = Xf @ Wf.T
-    got = host(Y, np.float32).reshape(T, N)
-    expect_close(got, exp, 1e-4, f"gemm {T}x{N}x{K}")
+    ok(lib, lib.lcr_gemm(p(Y), 1, p(Xd), p(Wd), T, N, K, NULL), "gemm")
+    expect_close(host(Y, np.float32).reshape(T, N), exp, 1e-4, f"gemm {T}x{N}x{K}")
     Yb = zeros_dev(T * N)
-    ok(lib, lib.lcr_gemm(p(Yb), 0, p(dev(X)), p(dev(W)), T, N, K, NULL), "gemm bf16")
+    ok(lib, lib.lcr_gemm(p(Yb), 0, p(Xd), p(Wd), T, N, K, NULL), "gemm bf16")
     expect_close(to_f32(host(Yb)), exp, 8e-3, "gemm bf16 out")
 
 
-@pytest.mark.parametrize("tokens,start,paged", [(7, 0, False), (40, 100, True), (65, 3, False)])
-def test_prefill_attention(gpu, lcr, orc, tokens, start, paged):
+PREFILL_CASES = [
+    # (num_heads, kv_heads, head_dim, tokens, start, paged)
+    (32, 8, 64, 7, 0, False),
+    (32, 8, 64, 40, 100, True),
+    (32, 8, 64, 65, 3, False),
+    (32, 8, 64, 1024, 0, False),    # two row fragments per wave
+    (32, 8, 64, 300, 700, True),    # a later chunk over a permuted paged cache
+    (8, 2, 128, 150, 37, False),    # head_dim 128
+    (12, 2, 64, 90, 5, True),       # groups of 6: a second block of heads, two idle waves
+    (4, 4, 32, 50, 10, False),      # head_dim 32: the generic kernel
+]
+
+
+@pytest.mark.parametrize("heads,kv,hd,tokens,start,paged", PREFILL_CASES)
+def test_prefill_attention(gpu, lcr, orc, heads, kv, hd, tokens, start, paged):
     lib = gpu
-    r = rng(tokens + start)
-    heads, kv, hd = 32, 8, 64
+    r = rng(tokens + start + hd)
     n = start + tokens
     keys = random_elems(r, (n, kv * hd))
     values = random_elems(r, (n, kv * hd))
@@ -376,12 +397,13 @@ def test_prefill_attention(gpu, lcr, orc, tokens, start, paged):
     fill_cache(lib, lcr, cache, keys, values, n)
     out = zeros_dev(tokens * heads * hd)
     v = cache.view(lcr)
+    scale = 1.0 / np.sqrt(hd)
     ok(lib, lib.lcr_prefill_attention(p(out), p(dev(qh)), ctypes.byref(v), heads, heads // kv, tokens, start,
-                                      0.125, 1 if paged else 0, NULL), "prefill attention")
+                                      scale, 1 if paged else 0, NULL), "prefill attention")
     hv = cache.host_view()
     exp = np.zeros(tokens * heads * hd, dtype=np.uint16)
     orc.load().orc_prefill_attention(BF16, exp.ctypes.data, qh.ctypes.data, ctypes.byref(hv), heads, heads // kv,
-                                     tokens, start, 0.125, 1 if paged else 0)
+                                     tokens, start, scale, 1 if paged else 0)
     expect_close(to_f32(host(out)), to_f32(exp), 3e-2, "prefill attention")
 
 

@@ -142,6 +142,20 @@ int lcr_gemv(void* y, int y_fp32, const void* W, const void* x, int N, int K, vo
 int lcr_gemm(void* Y, int y_fp32, const void* X, const void* W, int T, int N, int K,
              void* stream);
 
+/* lcr_gemm with a caller-provided device workspace (16-byte aligned): when the
+ * output tiles alone would leave compute units idle, K is split into slices
+ * whose fp32 partial products go to the workspace and are summed in slice
+ * order by a second kernel. A workspace smaller than the preferred split needs
+ * gives a plan that fits (down to no split). No counterpart in the reference,
+ * which hands this choice to cuBLAS and its internal workspace
+ * (src/model.cu:38-45). */
+int lcr_gemm_ws(void* Y, int y_fp32, const void* X, const void* W, int T, int N, int K,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes lcr_gemm_ws uses for its preferred plan at this shape on the
+ * current device (0: no split). */
+size_t lcr_gemm_workspace_bytes(int T, int N, int K);
+
 /* Causal GQA attention for a prefill chunk: the two strided-batched GEMMs and
  * the softmax of src/model.cu:509-560 (K13 gather + G6 + K10 + G7 + K7) in
  * one flash-style pass reading the cache through the view.

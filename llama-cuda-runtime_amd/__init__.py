@@ -146,6 +146,8 @@ SIGNATURES = {
     "lcr_sample_scratch_floats": (_SZ, [_I, _I]),
     "lcr_gemv": (_I, [_P, _I, _P, _P, _I, _I, _P]),
     "lcr_gemm": (_I, [_P, _I, _P, _P, _I, _I, _I, _P]),
+    "lcr_gemm_ws": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, ctypes.c_size_t, _P]),
+    "lcr_gemm_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I]),
     "lcr_prefill_attention": (_I, [_P, _P, ctypes.POINTER(KvView), _I, _I, _I, _I, _F, _I, _P]),
     # lcr_model.h
     "lcr_model_default_options": (None, [ctypes.POINTER(ModelOptions)]),

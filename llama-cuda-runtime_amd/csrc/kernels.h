@@ -119,6 +119,11 @@ inline void launch_gemm(void* Y, bool y_fp32, const elem_t* X, const elem_t* W, 
   check_kernel_status(lcr_gemm(Y, y_fp32 ? 1 : 0, X, W, T, N, K, stream));
 }
 
+inline void launch_gemm(void* Y, bool y_fp32, const elem_t* X, const elem_t* W, int T, int N,
+                        int K, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  check_kernel_status(lcr_gemm_ws(Y, y_fp32 ? 1 : 0, X, W, T, N, K, workspace, workspace_bytes, stream));
+}
+
 inline void launch_prefill_attention(elem_t* out, const elem_t* q_heads, const KvCacheView& view,
                                      int num_heads, int heads_per_kv, int tokens,
                                      int start_position, float scale, bool paged,

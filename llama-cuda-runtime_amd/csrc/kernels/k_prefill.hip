@@ -61,6 +61,18 @@ __device__ __forceinline__ mfma_in8 lds_operand(const elem_t* p) {
   return *reinterpret_cast<const mfma_in8*>(p);
 }
 
+// Two floats rounded to the element type (nearest even) by the packed
+// hardware conversion, low half first.
+__device__ __forceinline__ uint32_t pack_rounded(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+#if defined(LCR_ELEM_FP16)
+  typedef _Float16 e16x2 __attribute__((ext_vector_type(2)));
+#else
+  typedef __bf16 e16x2 __attribute__((ext_vector_type(2)));
+#endif
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, e16x2));
+}
+
 int device_compute_units() {
   static int cached[64] = {};
   int dev = 0;
@@ -83,12 +95,85 @@ int device_compute_units() {
 constexpr int kStageK = 64;
 constexpr int kGemmPitch = kStageK + 8;  // LDS row pitch in elements: fragment reads hit 64 banks once
 
+// The work of one launch: tiles of W rows x tokens, each optionally split
+// over K into `splits` slices of k_chunk elements. A split launch writes
+// fp32 partial products, slice s to partial + s * T * N, and a second kernel
+// sums the slices in slice order.
+struct GemmGrid {
+  int tiles_t;
+  int tiles_w;
+  int splits;
+  int k_chunk;
+  float* partial;  // nullptr: no split, write Y
+};
+
+struct GemmWork {
+  int w0, t0, k_first, k_len, split;
+};
+
+// XCD-aware order: XCD x (block id mod 8) takes work units [x*per, (x+1)*per),
+// tokens fastest, so the blocks of one XCD share W slices in its L2.
+__device__ __forceinline__ bool gemm_work(const GemmGrid& g, int BW, int BT, int K, GemmWork& w) {
+  const int units = g.tiles_t * g.tiles_w * g.splits;
+  const int per_xcd = (units + 7) / 8;
+  const int u = static_cast<int>(blockIdx.x % 8u) * per_xcd + static_cast<int>(blockIdx.x / 8u);
+  if (u >= units) return false;
+  const int tt = u % g.tiles_t;
+  const int rest = u / g.tiles_t;
+  w.split = rest % g.splits;
+  w.w0 = (rest / g.splits) * BW;
+  w.t0 = tt * BT;
+  w.k_first = w.split * g.k_chunk;
+  w.k_len = min(K, w.k_first + g.k_chunk) - w.k_first;
+  return true;
+}
+
+// acc[i][j][v] is output (token t0 + tw + 16j + col, feature w0 + ww + 16i + 4grp + v).
+template <int FW, int FT, bool kFp32Out>
+__device__ __forceinline__ void store_gemm_tile(const mfma_acc4 (&acc)[FW][FT], void* Y, float* partial,
+                                                int T, int N, int t_base, int w_base, int col, int grp) {
+  const bool whole_words = (N & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < FT; ++j) {
+    const int t = t_base + j * 16 + col;
+    if (t >= T) continue;
+#pragma unroll
+    for (int i = 0; i < FW; ++i) {
+      const int w = w_base + i * 16 + 4 * grp;
+      const size_t at = static_cast<size_t>(t) * N + w;
+      const bool fp32 = kFp32Out || partial != nullptr;
+      float* out32 = partial != nullptr ? partial : static_cast<float*>(Y);
+      if (whole_words && w + 4 <= N) {
+        if (fp32) {
+          *reinterpret_cast<float4*>(out32 + at) = float4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        } else {
+          uint2 packed;
+          packed.x = pack_elems(acc[i][j][0], acc[i][j][1]);
+          packed.y = pack_elems(acc[i][j][2], acc[i][j][3]);
+          *reinterpret_cast<uint2*>(static_cast<elem_t*>(Y) + at) = packed;
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          if (w + v >= N) break;
+          if (fp32) {
+            out32[at + v] = acc[i][j][v];
+          } else {
+            static_cast<elem_t*>(Y)[at + v] = float_to_elem(acc[i][j][v]);
+          }
+        }
+      }
+    }
+  }
+}
+
 // Block tile BW x BT (W rows x tokens) over kWavesW x kWavesT waves; each
-// wave owns a (BW / kWavesW) x (BT / kWavesT) piece.
+// wave owns a (BW / kWavesW) x (BT / kWavesT) piece. Operands go global ->
+// registers -> LDS, a stage of 64 K ahead, through two LDS buffers.
 template <int BW, int BT, int kWavesW, int kWavesT, bool kFp32Out>
 __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
     void* __restrict__ Y, const elem_t* __restrict__ X, const elem_t* __restrict__ W, int T, int N,
-    int K, int tiles_t, int total_tiles) {
+    int K, GemmGrid grid) {
   constexpr int kThreads = 64 * kWavesW * kWavesT;
   constexpr int kWaveW = BW / kWavesW, kWaveT = BT / kWavesT;
   constexpr int FW = kWaveW / 16, FT = kWaveT / 16;
@@ -97,12 +182,9 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
   static_assert(BW % kRowsPerPass == 0 && BT % kRowsPerPass == 0, "stage must split evenly");
   __shared__ __attribute__((aligned(16))) elem_t stage[2][(BW + BT) * kGemmPitch];
 
-  // XCD-aware tile order: XCD x (block id mod 8) takes tiles [x*per, (x+1)*per).
-  const int per_xcd = (total_tiles + 7) / 8;
-  const int tile = static_cast<int>(blockIdx.x % 8u) * per_xcd + static_cast<int>(blockIdx.x / 8u);
-  if (tile >= total_tiles) return;
-  const int w0 = (tile / tiles_t) * BW;
-  const int t0 = (tile % tiles_t) * BT;
+  GemmWork work;
+  if (!gemm_work(grid, BW, BT, K, work)) return;
+  const int w0 = work.w0, t0 = work.t0;
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -124,22 +206,23 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
   for (int c = 0; c < kPerW; ++c) {
     const int row = w0 + kRowsPerPass * c + trow;
     live |= (row < N ? 1u : 0u) << c;
-    wsrc[c] = W + static_cast<size_t>(min(row, N - 1)) * K + kc;
+    wsrc[c] = W + static_cast<size_t>(min(row, N - 1)) * K + work.k_first;
   }
 #pragma unroll
   for (int c = 0; c < kPerT; ++c) {
     const int row = t0 + kRowsPerPass * c + trow;
     live |= (row < T ? 1u : 0u) << (kPerW + c);
-    xsrc[c] = X + static_cast<size_t>(min(row, T - 1)) * K + kc;
+    xsrc[c] = X + static_cast<size_t>(min(row, T - 1)) * K + work.k_first;
   }
   // The loads of a stage are issued a stage ahead; the zeroing select waits
   // until the data is written to LDS, so nothing waits on the loads before
   // the matrix work of the current stage.
+  const int k_len = work.k_len;
   vec16 held[kPerW + kPerT];
   uint32_t held_ok = 0;
   auto fetch = [&](int k0) {
-    const int k = min(k0, K - 8 - kc);  // a tail stage reads in bounds; deposit zeroes it
-    held_ok = k0 + kc < K ? live : 0u;
+    const int k = min(k0 + kc, k_len - 8);  // a tail stage reads in bounds; deposit zeroes it
+    held_ok = k0 + kc < k_len ? live : 0u;
 #pragma unroll
     for (int c = 0; c < kPerW + kPerT; ++c) held[c] = load16((c < kPerW ? wsrc[c] : xsrc[c - kPerW]) + k);
   };
@@ -161,7 +244,7 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
     for (int j = 0; j < FT; ++j) acc[i][j] = mfma_acc4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int stages = (K + kStageK - 1) / kStageK;
+  const int stages = (k_len + kStageK - 1) / kStageK;
   fetch(0);
   deposit(0);
   __syncthreads();
@@ -196,67 +279,205 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
     __syncthreads();
   }
 
-  // acc[i][j][v] = Y[token t0 + wt + 16j + col][feature w0 + ww + 16i + 4grp + v]
-  const bool whole_words = (N & 3) == 0;
+  float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
+  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp);
+}
+
+// The large-tile GEMM with a ring of kStages LDS stages of 32 K each, filled
+// by direct global-to-LDS loads (global_load_lds_dwordx4: lane L's 16 bytes
+// land at the wave's LDS address in M0 + 16 L), so loads run kStages - 1
+// stages ahead of the matrix work without holding registers. A stage holds
+// 256 W rows then 256 token rows of 32 elements (64 bytes); 16-byte chunk g
+// of row r sits at position g ^ ((r >> 2) & 3), which makes the fragment
+// reads of 16 consecutive rows hit all 64 banks once. Rows past the end read
+// the last row (their outputs are not stored); K must be a multiple of 32.
+//
+// The loads are issued from inline assembly and the stages are fenced by
+// hand: each wave waits until its loads of the stage it is about to read have
+// landed (vector-memory count down to the younger stages' loads) and until
+// its fragment reads of the previous stage are done, then the block meets at
+// a plain s_barrier. Had the compiler seen the loads as LDS writes, it would
+// drain every load in flight at each barrier and the ring would be one stage
+// deep. Loads the compiler does not count can only make its own in-order
+// count waits stricter.
+constexpr int kRingK = 32;
+constexpr int kRingRows = 512;                       // 256 W rows + 256 token rows
+constexpr int kRingStage = kRingRows * kRingK;       // elements per stage (32 KB)
+
+__device__ __forceinline__ void load_to_lds16(const elem_t* src, uint32_t lds_address) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_address) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address_of(const elem_t* p) {
+  typedef const __attribute__((address_space(3))) elem_t* lds_elem_ptr;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_elem_ptr)p));
+}
+
+// Wait until at most kCount vector-memory operations of this wave are in
+// flight and every LDS read has returned (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 zero).
+template <int kCount>
+__device__ __forceinline__ void wait_stage_landed() {
+  static_assert(kCount >= 0 && kCount < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((kCount & 15) | ((kCount >> 4) << 14) | (7 << 4));
+}
+
+template <int kStages, bool kFp32Out>
+__global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, const elem_t* __restrict__ X,
+                                                        const elem_t* __restrict__ W, int T, int N, int K,
+                                                        GemmGrid grid) {
+  constexpr int FW = 8, FT = 4;  // wave tile 128 W rows x 64 tokens
+  __shared__ __attribute__((aligned(1024))) elem_t ring[kStages * kRingStage];
+
+  GemmWork work;
+  if (!gemm_work(grid, 256, 256, K, work)) return;
+  const int w0 = work.w0, t0 = work.t0;
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int ww = (wave >> 2) * 128;
+  const int wt = (wave & 3) * 64;
+
+  // Load i (0..3) of a wave fills 1 KB block 8i + wave of the stage: rows
+  // 16 block .. +15, four lanes per row.
+  const elem_t* src[4];
 #pragma unroll
-  for (int j = 0; j < FT; ++j) {
-    const int t = t0 + wt + j * 16 + col;
-    if (t >= T) continue;
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * (8 * i + wave) + (lane >> 2);
+    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+    src[i] = (row < 256 ? W + static_cast<size_t>(min(w0 + row, N - 1)) * K
+                        : X + static_cast<size_t>(min(t0 + row - 256, T - 1)) * K) + work.k_first + 8 * chunk;
+  }
+  const uint32_t ring_base = lds_address_of(ring) + static_cast<uint32_t>(wave * 16 * kRingK * 2);
+  auto issue = [&](int s) {
+    const uint32_t base = ring_base + static_cast<uint32_t>((s % kStages) * kRingStage * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_to_lds16(src[i] + s * kRingK, base + static_cast<uint32_t>(i * 8 * 16 * kRingK * 2));
+  };
+
+  mfma_acc4 acc[FW][FT];
+#pragma unroll
+  for (int i = 0; i < FW; ++i) {
+#pragma unroll
+    for (int j = 0; j < FT; ++j) acc[i][j] = mfma_acc4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int swz = 8 * (grp ^ ((col >> 2) & 3));
+  const int stages = work.k_len / kRingK;
+  for (int s = 0; s < kStages - 1 && s < stages; ++s) issue(s);
+  for (int s = 0; s < stages; ++s) {
+    // this wave's loads of stage s are done once at most the younger stages' remain
+    if (s + kStages - 2 < stages) {
+      wait_stage_landed<4 * (kStages - 2)>();
+    } else {
+      wait_stage_landed<0>();
+    }
+    __builtin_amdgcn_s_barrier();  // every wave's stage s has landed; stage s - 1 is no longer read
+    if (s + kStages - 1 < stages) issue(s + kStages - 1);
+    const elem_t* base = ring + (s % kStages) * kRingStage;
+    mfma_in8 bt[FT], aw[FW];
+#pragma unroll
+    for (int j = 0; j < FT; ++j) bt[j] = lds_operand(base + (256 + wt + 16 * j + col) * kRingK + swz);
+#pragma unroll
+    for (int i = 0; i < FW; ++i) aw[i] = lds_operand(base + (ww + 16 * i + col) * kRingK + swz);
 #pragma unroll
     for (int i = 0; i < FW; ++i) {
-      const int w = w0 + ww + i * 16 + 4 * grp;
-      const size_t at = static_cast<size_t>(t) * N + w;
-      if (whole_words && w + 4 <= N) {
-        if (kFp32Out) {
-          *reinterpret_cast<float4*>(static_cast<float*>(Y) + at) =
-              float4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-        } else {
-          uint2 packed;
-          packed.x = pack_elems(acc[i][j][0], acc[i][j][1]);
-          packed.y = pack_elems(acc[i][j][2], acc[i][j][3]);
-          *reinterpret_cast<uint2*>(static_cast<elem_t*>(Y) + at) = packed;
-        }
-      } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          if (w + v >= N) break;
-          if (kFp32Out) {
-            static_cast<float*>(Y)[at + v] = acc[i][j][v];
-          } else {
-            static_cast<elem_t*>(Y)[at + v] = float_to_elem(acc[i][j][v]);
-          }
-        }
-      }
+      for (int j = 0; j < FT; ++j) acc[i][j] = mfma16x16x32(aw[i], bt[j], acc[i][j]);
+    }
+  }
+
+  float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
+  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp);
+}
+
+constexpr int kRingStages = 4;
+
+// Y = sum over slices of the fp32 partial products, in slice order.
+template <bool kFp32Out>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(void* __restrict__ Y, const float* __restrict__ partial,
+                                                          int splits, size_t count) {
+  const size_t i = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= count) return;
+  if (i + 4 <= count) {
+    float4 sum = *reinterpret_cast<const float4*>(partial + i);
+    for (int s = 1; s < splits; ++s) {
+      const float4 v = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(s) * count + i);
+      sum.x += v.x;
+      sum.y += v.y;
+      sum.z += v.z;
+      sum.w += v.w;
+    }
+    if (kFp32Out) {
+      *reinterpret_cast<float4*>(static_cast<float*>(Y) + i) = sum;
+    } else {
+      uint2 packed;
+      packed.x = pack_elems(sum.x, sum.y);
+      packed.y = pack_elems(sum.z, sum.w);
+      *reinterpret_cast<uint2*>(static_cast<elem_t*>(Y) + i) = packed;
+    }
+    return;
+  }
+  for (size_t e = i; e < count; ++e) {
+    float sum = partial[e];
+    for (int s = 1; s < splits; ++s) sum += partial[static_cast<size_t>(s) * count + e];
+    if (kFp32Out) {
+      static_cast<float*>(Y)[e] = sum;
+    } else {
+      static_cast<elem_t*>(Y)[e] = float_to_elem(sum);
     }
   }
 }
 
-enum class GemmShape { k256x256, k256x128, k128x128 };
+enum class GemmShape { kRing256x256, k256x256, k256x128, k128x128 };
 
-// The tile shape with the least estimated time: whole rounds of tiles over
-// the compute units, each tile costing its area over the shape's relative
-// efficiency (larger tiles reuse each LDS fragment more often and move fewer
-// bytes per flop).
-GemmShape choose_gemm_shape(int T, int N, int cus) {
+struct GemmPlan {
+  GemmShape shape;
+  int bw, bt;
+  int splits;
+  int k_chunk;
+  size_t workspace_bytes;
+};
+
+// The plan with the least estimated time. Work units (tile x K slice) run in
+// whole rounds over the compute units; a unit costs its flops at the shape's
+// measured fraction of a compute unit's MFMA peak. Splitting K is considered
+// only when the tiles alone leave compute units idle, and costs the fp32
+// partials' round trip through memory plus a launch. Each slice keeps at
+// least 256 K and is a whole number of the shape's K stages.
+GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes) {
   struct Option {
     GemmShape shape;
-    int bw, bt;
-    double efficiency;
+    int bw, bt, stage_k;
+    double efficiency;  // fraction of a compute unit's MFMA peak, measured on MI355X
   };
-  static const Option options[] = {{GemmShape::k256x256, 256, 256, 1.0},
-                                   {GemmShape::k256x128, 256, 128, 0.85},
-                                   {GemmShape::k128x128, 128, 128, 0.6}};
-  GemmShape best = GemmShape::k128x128;
-  double best_cost = 0.0;
-  bool first = true;
+  const bool ring = K % kRingK == 0;
+  const Option options[] = {
+      {ring ? GemmShape::kRing256x256 : GemmShape::k256x256, 256, 256, ring ? kRingK : kStageK, ring ? 0.37 : 0.31},
+      {GemmShape::k256x128, 256, 128, kStageK, 0.23},
+      {GemmShape::k128x128, 128, 128, kStageK, 0.20}};
+  constexpr double kCuPeak = 9.8e12;     // bf16 dense flop/s per compute unit
+  constexpr double kBandwidth = 5.0e12;  // sustained bytes/s for the partials' round trip
+  constexpr double kLaunch = 4e-6;
+  GemmPlan best{GemmShape::k128x128, 128, 128, 1, K, 0};
+  double best_time = -1.0;
   for (const Option& o : options) {
     const long long tiles = static_cast<long long>((N + o.bw - 1) / o.bw) * ((T + o.bt - 1) / o.bt);
-    const long long rounds = (tiles + cus - 1) / cus;
-    const double cost = static_cast<double>(rounds) * o.bw * o.bt / o.efficiency;
-    if (first || cost < best_cost) {
-      best = o.shape;
-      best_cost = cost;
-      first = false;
+    for (int splits = 1; splits <= 16; splits *= 2) {
+      if (splits > 1 && tiles * (splits / 2) >= cus) break;  // already enough units
+      const int k_chunk = ((K + splits - 1) / splits + o.stage_k - 1) / o.stage_k * o.stage_k;
+      if (splits > 1 && k_chunk < 256) break;
+      const int used = (K + k_chunk - 1) / k_chunk;
+      const size_t bytes = used > 1 ? static_cast<size_t>(used) * T * N * sizeof(float) : 0;
+      if (bytes > workspace_bytes) break;
+      const long long rounds = (tiles * used + cus - 1) / cus;
+      double time = static_cast<double>(rounds) * 2.0 * o.bw * o.bt * k_chunk / (o.efficiency * kCuPeak);
+      if (used > 1) time += (static_cast<double>(bytes) + static_cast<double>(T) * N * 4.0) / kBandwidth + kLaunch;
+      if (best_time < 0.0 || time < best_time) {
+        best = GemmPlan{o.shape, o.bw, o.bt, used, k_chunk, bytes};
+        best_time = time;
+      }
     }
   }
   return best;
@@ -264,15 +485,55 @@ GemmShape choose_gemm_shape(int T, int N, int cus) {
 
 template <int BW, int BT, int kWavesW, int kWavesT>
 void launch_gemm_tiles(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K,
-                       hipStream_t s) {
-  const int tiles_t = (T + BT - 1) / BT;
-  const int total = ((N + BW - 1) / BW) * tiles_t;
-  const unsigned blocks = static_cast<unsigned>(((total + 7) / 8) * 8);
+                       const GemmGrid& grid, hipStream_t s) {
+  const int units = grid.tiles_t * grid.tiles_w * grid.splits;
+  const unsigned blocks = static_cast<unsigned>(((units + 7) / 8) * 8);
   constexpr unsigned kThreads = 64u * kWavesW * kWavesT;
   if (fp32_out) {
-    gemm_nt_kernel<BW, BT, kWavesW, kWavesT, true><<<blocks, kThreads, 0, s>>>(Y, X, W, T, N, K, tiles_t, total);
+    gemm_nt_kernel<BW, BT, kWavesW, kWavesT, true><<<blocks, kThreads, 0, s>>>(Y, X, W, T, N, K, grid);
   } else {
-    gemm_nt_kernel<BW, BT, kWavesW, kWavesT, false><<<blocks, kThreads, 0, s>>>(Y, X, W, T, N, K, tiles_t, total);
+    gemm_nt_kernel<BW, BT, kWavesW, kWavesT, false><<<blocks, kThreads, 0, s>>>(Y, X, W, T, N, K, grid);
+  }
+}
+
+void launch_gemm_ring(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K,
+                      const GemmGrid& grid, hipStream_t s) {
+  const int units = grid.tiles_t * grid.tiles_w * grid.splits;
+  const unsigned blocks = static_cast<unsigned>(((units + 7) / 8) * 8);
+  if (fp32_out) {
+    gemm_ring_kernel<kRingStages, true><<<blocks, 512, 0, s>>>(Y, X, W, T, N, K, grid);
+  } else {
+    gemm_ring_kernel<kRingStages, false><<<blocks, 512, 0, s>>>(Y, X, W, T, N, K, grid);
+  }
+}
+
+void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K, void* workspace,
+              size_t workspace_bytes, hipStream_t s) {
+  const GemmPlan plan = plan_gemm(T, N, K, device_compute_units(), workspace != nullptr ? workspace_bytes : 0);
+  GemmGrid grid{(T + plan.bt - 1) / plan.bt, (N + plan.bw - 1) / plan.bw, plan.splits, plan.k_chunk,
+                plan.splits > 1 ? static_cast<float*>(workspace) : nullptr};
+  switch (plan.shape) {
+    case GemmShape::kRing256x256:
+      launch_gemm_ring(Y, fp32_out, X, W, T, N, K, grid, s);
+      break;
+    case GemmShape::k256x256:
+      launch_gemm_tiles<256, 256, 2, 4>(Y, fp32_out, X, W, T, N, K, grid, s);
+      break;
+    case GemmShape::k256x128:
+      launch_gemm_tiles<256, 128, 4, 2>(Y, fp32_out, X, W, T, N, K, grid, s);
+      break;
+    case GemmShape::k128x128:
+      launch_gemm_tiles<128, 128, 2, 2>(Y, fp32_out, X, W, T, N, K, grid, s);
+      break;
+  }
+  if (plan.splits > 1) {
+    const size_t count = static_cast<size_t>(T) * N;
+    const unsigned blocks = static_cast<unsigned>((count + 1023) / 1024);
+    if (fp32_out) {
+      gemm_reduce_kernel<true><<<blocks, 256, 0, s>>>(Y, grid.partial, plan.splits, count);
+    } else {
+      gemm_reduce_kernel<false><<<blocks, 256, 0, s>>>(Y, grid.partial, plan.splits, count);
+    }
   }
 }
 
@@ -303,8 +564,7 @@ struct FlashShared {
 template <bool kPaged, int kHeadDim, int kRF>
 __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
     elem_t* __restrict__ out, const elem_t* __restrict__ q_heads, KvCacheView view, int num_heads,
-    int group, int tokens, int start_position, float scale) {
-  constexpr float kLog2e = 1.44269504088896341f;
+    int group, int tokens, int start_position, float scale_log2e) {
   constexpr int kRows = 16 * kRF;                         // query positions per block
   constexpr int kSteps = kHeadDim / 32;                   // MFMA k-steps over head_dim
   constexpr int kDFrags = kHeadDim / 16;                  // output fragments over head_dim
@@ -373,9 +633,9 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
       }
     }
   };
-  // Scaled scores of one staged tile, transposed: s[rf][kf][v] is the score of
-  // row 16rf + col against key 16kf + 4grp + v; keys past a row's position are
-  // -inf.
+  // Scores of one staged tile in base-2 units (scale * log2(e) * q . k),
+  // transposed: s[rf][kf][v] is row 16rf + col against key 16kf + 4grp + v;
+  // keys past a row's position are -inf.
   auto scores = [&](int buf, int tile, mfma_acc4 (&s)[kRF][4]) {
 #pragma unroll
     for (int kf = 0; kf < 4; ++kf) {
@@ -388,17 +648,25 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
         for (int rf = 0; rf < kRF; ++rf) s[rf][kf] = mfma16x16x32(a, qf[rf][ks], s[rf][kf]);
       }
     }
-    const int key0 = tile * kFlashKeys;
-    const bool masked = key0 + kFlashKeys - 1 > start_position + r0;
 #pragma unroll
     for (int rf = 0; rf < kRF; ++rf) {
-      const int limit = start_position + r0 + rf * 16 + col;  // last key this row sees
 #pragma unroll
       for (int kf = 0; kf < 4; ++kf) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float x = s[rf][kf][v] * scale;
-          s[rf][kf][v] = (masked && key0 + kf * 16 + 4 * grp + v > limit) ? -__builtin_huge_valf() : x;
+        for (int v = 0; v < 4; ++v) s[rf][kf][v] *= scale_log2e;
+      }
+    }
+    const int key0 = tile * kFlashKeys;
+    if (key0 + kFlashKeys - 1 > start_position + r0) {  // a tile that crosses the diagonal
+#pragma unroll
+      for (int rf = 0; rf < kRF; ++rf) {
+        const int over = key0 + 4 * grp - (start_position + r0 + rf * 16 + col);  // key - last visible key
+#pragma unroll
+        for (int kf = 0; kf < 4; ++kf) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            if (over + kf * 16 + v > 0) s[rf][kf][v] = -__builtin_huge_valf();
+          }
         }
       }
     }
@@ -436,9 +704,9 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
 #pragma unroll
         for (int kf = 0; kf < 4; ++kf) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) sum += __builtin_amdgcn_exp2f((s[rf][kf][v] - m_new) * kLog2e);
+          for (int v = 0; v < 4; ++v) sum += __builtin_amdgcn_exp2f(s[rf][kf][v] - m_new);
         }
-        l[rf] = __builtin_fmaf(l[rf], __builtin_amdgcn_exp2f((m[rf] - m_new) * kLog2e), sum);
+        l[rf] = __builtin_fmaf(l[rf], __builtin_amdgcn_exp2f(m[rf] - m_new), sum);
         m[rf] = m_new;
       }
     }
@@ -478,9 +746,9 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
         for (int kf = 0; kf < 4; ++kf) {
           float pr[4];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) pr[v] = __builtin_amdgcn_exp2f((s[rf][kf][v] - m[rf]) * kLog2e) * inv[rf];
-          pk[kf][0] = pack_elems(pr[0], pr[1]);
-          pk[kf][1] = pack_elems(pr[2], pr[3]);
+          for (int v = 0; v < 4; ++v) pr[v] = __builtin_amdgcn_exp2f(s[rf][kf][v] - m[rf]) * inv[rf];
+          pk[kf][0] = pack_rounded(pr[0], pr[1]);
+          pk[kf][1] = pack_rounded(pr[2], pr[3]);
         }
 #pragma unroll
         for (int step = 0; step < 2; ++step) {
@@ -581,17 +849,18 @@ __global__ __launch_bounds__(kGenericThreads) void prefill_attention_generic_ker
 template <bool kPaged, int kHeadDim>
 void launch_flash(elem_t* o, const elem_t* q, const KvCacheView& v, int num_heads, int group,
                   int tokens, int start_position, float scale, hipStream_t s) {
+  const float scale_log2e = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   const unsigned zs = static_cast<unsigned>((group + 3) / 4);
   // Two row fragments per wave when that still gives two blocks per compute unit.
   const long long wide_blocks = static_cast<long long>((tokens + 31) / 32) * v.num_kv_heads * zs;
   if (wide_blocks >= 2LL * device_compute_units()) {
     const dim3 grid(static_cast<unsigned>((tokens + 31) / 32), static_cast<unsigned>(v.num_kv_heads), zs);
     flash_prefill_kernel<kPaged, kHeadDim, 2><<<grid, kFlashThreads, 0, s>>>(
-        o, q, v, num_heads, group, tokens, start_position, scale);
+        o, q, v, num_heads, group, tokens, start_position, scale_log2e);
   } else {
     const dim3 grid(static_cast<unsigned>((tokens + 15) / 16), static_cast<unsigned>(v.num_kv_heads), zs);
     flash_prefill_kernel<kPaged, kHeadDim, 1><<<grid, kFlashThreads, 0, s>>>(
-        o, q, v, num_heads, group, tokens, start_position, scale);
+        o, q, v, num_heads, group, tokens, start_position, scale_log2e);
   }
 }
 
@@ -600,8 +869,7 @@ void launch_flash(elem_t* o, const elem_t* q, const KvCacheView& v, int num_head
 
 using namespace lcr;
 
-extern "C" int lcr_gemm(void* Y, int y_fp32, const void* X, const void* W, int T, int N, int K,
-                        void* stream) {
+static int gemm_checks(const void* Y, const void* X, const void* W, int T, int N, int K) {
   CAPI_CHECK(T >= 0 && N >= 0 && K >= 0, "gemm needs non-negative sizes");
   if (T == 0 || N == 0) return LCR_OK;
   CAPI_CHECK(K > 0 && K % 8 == 0, "gemm needs K to be a positive multiple of 8, got " << K);
@@ -609,20 +877,33 @@ extern "C" int lcr_gemm(void* Y, int y_fp32, const void* X, const void* W, int T
                  (reinterpret_cast<uintptr_t>(W) & 15u) == 0 &&
                  (reinterpret_cast<uintptr_t>(Y) & 15u) == 0,
              "gemm needs 16-byte aligned operands");
-  auto s = static_cast<hipStream_t>(stream);
-  auto* x = static_cast<const elem_t*>(X);
-  auto* w = static_cast<const elem_t*>(W);
-  switch (choose_gemm_shape(T, N, device_compute_units())) {
-    case GemmShape::k256x256:
-      launch_gemm_tiles<256, 256, 2, 4>(Y, y_fp32 != 0, x, w, T, N, K, s);
-      break;
-    case GemmShape::k256x128:
-      launch_gemm_tiles<256, 128, 4, 2>(Y, y_fp32 != 0, x, w, T, N, K, s);
-      break;
-    case GemmShape::k128x128:
-      launch_gemm_tiles<128, 128, 2, 2>(Y, y_fp32 != 0, x, w, T, N, K, s);
-      break;
-  }
+  return LCR_OK;
+}
+
+extern "C" int lcr_gemm(void* Y, int y_fp32, const void* X, const void* W, int T, int N, int K,
+                        void* stream) {
+  const int status = gemm_checks(Y, X, W, T, N, K);
+  if (status != LCR_OK || T == 0 || N == 0) return status;
+  run_gemm(Y, y_fp32 != 0, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W), T, N, K, nullptr, 0,
+           static_cast<hipStream_t>(stream));
+  CAPI_LAUNCHED();
+  return LCR_OK;
+}
+
+extern "C" size_t lcr_gemm_workspace_bytes(int T, int N, int K) {
+  if (T <= 0 || N <= 0 || K <= 0 || K % 8 != 0) return 0;
+  return plan_gemm(T, N, K, device_compute_units(), static_cast<size_t>(-1)).workspace_bytes;
+}
+
+extern "C" int lcr_gemm_ws(void* Y, int y_fp32, const void* X, const void* W, int T, int N, int K,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  const int status = gemm_checks(Y, X, W, T, N, K);
+  if (status != LCR_OK || T == 0 || N == 0) return status;
+  CAPI_CHECK(workspace != nullptr || workspace_bytes == 0, "gemm workspace of " << workspace_bytes
+                                                                               << " bytes has no pointer");
+  CAPI_CHECK((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "gemm workspace must be 16-byte aligned");
+  run_gemm(Y, y_fp32 != 0, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W), T, N, K, workspace,
+           workspace_bytes, static_cast<hipStream_t>(stream));
   CAPI_LAUNCHED();
   return LCR_OK;
 }

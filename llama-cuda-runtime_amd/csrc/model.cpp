@@ -164,6 +164,24 @@ void Model::load_weights(const SafetensorsArchive& archive) {
   if (!has_lm_head) lm_head_ = embedding_;
 }
 
+// The split-K workspace the prefill projections use: the largest the GEMM
+// plans ask for over the four projection shapes at chunk lengths from the
+// maximum chunk down by halves (a chunk between two of these gets the plan
+// that fits).
+size_t Model::gemm_workspace_bytes() const {
+  const int hidden = config_.hidden_size;
+  const int ffn = config_.intermediate_size;
+  const int shapes[4][2] = {{config_.q_dim() + 2 * config_.kv_dim(), hidden},
+                            {hidden, config_.q_dim()},
+                            {2 * ffn, hidden},
+                            {hidden, ffn}};
+  size_t bytes = 0;
+  for (int T = max_tokens_; T >= 2; T /= 2) {
+    for (const auto& s : shapes) bytes = std::max(bytes, lcr_gemm_workspace_bytes(T, s[0], s[1]));
+  }
+  return align_up(bytes, 256);
+}
+
 void Model::allocate_arena() {
   const size_t H = static_cast<size_t>(config_.hidden_size);
   const size_t F = static_cast<size_t>(config_.intermediate_size);
@@ -191,6 +209,7 @@ void Model::allocate_arena() {
       sizeof(int32_t),                           // position_dev_
       kMaxLmHeadBlocks * sizeof(unsigned long long),                  // argmax_partials_
       (static_cast<size_t>(options_.max_seq) + 1) * sizeof(int32_t),  // history_
+      gemm_workspace_bytes(),                                         // gemm_workspace_
   };
   size_t total = 0;
   for (size_t s : sizes) total = align_up(total, 256) + s;
@@ -211,6 +230,8 @@ void Model::allocate_arena() {
   position_dev_ = arena_.alloc<int32_t>(1);
   argmax_partials_ = arena_.alloc<unsigned long long>(kMaxLmHeadBlocks);
   history_ = arena_.alloc<int32_t>(static_cast<size_t>(options_.max_seq) + 1);
+  gemm_workspace_size_ = gemm_workspace_bytes();
+  gemm_workspace_ = gemm_workspace_size_ > 0 ? arena_.alloc<float>(gemm_workspace_size_ / sizeof(float)) : nullptr;
   HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
   HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
 }
@@ -560,7 +581,8 @@ void Model::run_layers(int tokens, int start_position) {
       if (tokens == 1) {
         launch_gemv(qkv_, false, w.qkv_proj, normed_, qkv_stride, hidden, stream_);
       } else {
-        launch_gemm(qkv_, false, normed_, w.qkv_proj, tokens, qkv_stride, hidden, stream_);
+        launch_gemm(qkv_, false, normed_, w.qkv_proj, tokens, qkv_stride, hidden, gemm_workspace_,
+                    gemm_workspace_size_, stream_);
       }
     }
     const KvCacheView view = kv_cache_->view(layer);
@@ -584,7 +606,8 @@ void Model::run_layers(int tokens, int start_position) {
       if (tokens == 1) {
         launch_gemv(proj_out_, false, w.o_proj, attn_out_, hidden, config_.q_dim(), stream_);
       } else {
-        launch_gemm(proj_out_, false, attn_out_, w.o_proj, tokens, hidden, config_.q_dim(), stream_);
+        launch_gemm(proj_out_, false, attn_out_, w.o_proj, tokens, hidden, config_.q_dim(),
+                    gemm_workspace_, gemm_workspace_size_, stream_);
       }
     }
     {
@@ -597,7 +620,8 @@ void Model::run_layers(int tokens, int start_position) {
       if (tokens == 1) {
         launch_gemv(gate_up_, false, w.gate_up_proj, normed_, 2 * ffn, hidden, stream_);
       } else {
-        launch_gemm(gate_up_, false, normed_, w.gate_up_proj, tokens, 2 * ffn, hidden, stream_);
+        launch_gemm(gate_up_, false, normed_, w.gate_up_proj, tokens, 2 * ffn, hidden,
+                    gemm_workspace_, gemm_workspace_size_, stream_);
       }
     }
     {
@@ -609,7 +633,8 @@ void Model::run_layers(int tokens, int start_position) {
       if (tokens == 1) {
         launch_gemv(proj_out_, false, w.down_proj, act_, hidden, ffn, stream_);
       } else {
-        launch_gemm(proj_out_, false, act_, w.down_proj, tokens, hidden, ffn, stream_);
+        launch_gemm(proj_out_, false, act_, w.down_proj, tokens, hidden, ffn, gemm_workspace_,
+                    gemm_workspace_size_, stream_);
       }
     }
     {

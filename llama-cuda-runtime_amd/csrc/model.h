@@ -126,6 +126,7 @@ class Model {
  private:
   void load_weights(const SafetensorsArchive& archive);
   void allocate_arena();
+  size_t gemm_workspace_bytes() const;
   void run_layers(int tokens, int start_position);
   void attention_prefill(int layer, int tokens, int start_position);
   void attention_decode(int layer, int position);
@@ -164,6 +165,8 @@ class Model {
   elem_t* act_ = nullptr;         // [max_tokens][ffn]
   float* logits_ = nullptr;       // [vocab]
   float* attention_scratch_ = nullptr;
+  float* gemm_workspace_ = nullptr;  // split-K partial products of the prefill projections
+  size_t gemm_workspace_size_ = 0;
   int32_t* token_ids_ = nullptr;  // [max_tokens]
   int32_t* sampled_id_ = nullptr;
   // Fused decode state.

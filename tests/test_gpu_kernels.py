@@ -349,15 +349,18 @@ GEMM_CASES = [
     # (T, N, K): the model's projections at prefill sizes, then ragged edges
     (128, 3072, 2048), (37, 2048, 8192), (256, 16384, 2048), (5, 100, 64),
     (2048, 3072, 2048), (512, 2048, 8192), (300, 2048, 2048), (1000, 520, 72), (33, 1001, 136),
+    # 256 x 256 tiles: the LDS ring at K = 2048 with ragged tokens, K shorter
+    # than the ring (64, 32), and a K that is not a multiple of 32
+    (1000, 16384, 2048), (512, 65536, 64), (512, 65536, 32), (1024, 16384, 520),
 ]
 
 
 @pytest.mark.parametrize("T,N,K", GEMM_CASES)
 def test_gemm_mfma(gpu, orc, T, N, K):
-    """Every tile shape (256x256 for the bf16 output of large problems,
-    256x128 and 128x128 otherwise) against a float64 product; K tails that
-    end mid-stage, token and feature counts that end mid-tile, and N that is
-    not a multiple of 4 (scalar epilogue)."""
+    """Every tile shape (256x256 for large problems, through the LDS ring when
+    K is a multiple of 32; 256x128 and 128x128 otherwise) against a float64
+    product; K tails that end mid-stage, token and feature counts that end
+    mid-tile, and N that is not a multiple of 4 (scalar epilogue)."""
     lib = gpu
     r = rng(T * N + K)
     X = random_elems(r, (T, K))
@@ -370,6 +373,28 @@ def test_gemm_mfma(gpu, orc, T, N, K):
     Yb = zeros_dev(T * N)
     ok(lib, lib.lcr_gemm(p(Yb), 0, p(Xd), p(Wd), T, N, K, NULL), "gemm bf16")
     expect_close(to_f32(host(Yb)), exp, 8e-3, "gemm bf16 out")
+    # With a workspace, shapes that leave compute units idle split K; the
+    # slices are summed in a fixed order, so a repeat gives the same bits.
+    ws_bytes = lib.lcr_gemm_workspace_bytes(T, N, K)
+    ws = zeros_dev(max(ws_bytes, 16) // 4, np.float32)
+    for fp32_out, tol in ((1, 1e-4), (0, 8e-3)):
+        runs = []
+        for _ in range(2):
+            Ys = zeros_dev(T * N, np.float32 if fp32_out else np.uint16)
+            ok(lib, lib.lcr_gemm_ws(p(Ys), fp32_out, p(Xd), p(Wd), T, N, K, p(ws), ws_bytes, NULL), "gemm_ws")
+            runs.append(host(Ys, np.float32 if fp32_out else np.uint16))
+        assert np.array_equal(runs[0], runs[1])
+        got = runs[0] if fp32_out else to_f32(runs[0])
+        expect_close(np.asarray(got).reshape(T, N), exp, tol, f"gemm_ws {T}x{N}x{K} ({ws_bytes} B workspace)")
+
+
+def test_gemm_workspace_plans(gpu):
+    """Small token counts ask for a split (the projections of a 512-token
+    chunk), large ones do not."""
+    lib = gpu
+    assert lib.lcr_gemm_workspace_bytes(512, 2048, 8192) > 0
+    assert lib.lcr_gemm_workspace_bytes(2048, 16384, 2048) == 0
+    assert lib.lcr_gemm_workspace_bytes(0, 2048, 2048) == 0
 
 
 PREFILL_CASES = [

@@ -93,7 +93,11 @@ int device_compute_units() {
 // ---------------------------------------------------------------------------
 
 constexpr int kStageK = 64;
-constexpr int kGemmPitch = kStageK + 8;  // LDS row pitch in elements: fragment reads hit 64 banks once
+// A stage row is 64 elements (128 bytes) with its 16-byte chunk c stored at
+// position c ^ (row & 7): the fragment reads of 16 consecutive rows are then
+// free of bank conflicts (measured on MI355X; a padded 72-element pitch costs
+// about half again as much per read).
+constexpr int kGemmPitch = kStageK;
 
 // The work of one launch: tiles of W rows x tokens, each optionally split
 // over K into `splits` slices of k_chunk elements. A split launch writes
@@ -233,7 +237,7 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
       vec16 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v.w[e] = ok ? held[c].w[e] : 0u;
-      store16(&stage[buf][(kRowsPerPass * c + trow) * kGemmPitch + kc], v);
+      store16(&stage[buf][(kRowsPerPass * c + trow) * kGemmPitch + (((tid & 7) ^ (trow & 7)) << 3)], v);
     }
   };
 
@@ -251,15 +255,16 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
   for (int s = 0; s < stages; ++s) {
     const int buf = s & 1;
     if (s + 1 < stages) fetch((s + 1) * kStageK);
-    const elem_t* wl = &stage[buf][(ww + col) * kGemmPitch + 8 * grp];
-    const elem_t* tl = &stage[buf][(BW + wt + col) * kGemmPitch + 8 * grp];
+    const elem_t* wl = &stage[buf][(ww + col) * kGemmPitch];
+    const elem_t* tl = &stage[buf][(BW + wt + col) * kGemmPitch];
 #pragma unroll
     for (int kk = 0; kk < kStageK; kk += 32) {
       mfma_in8 bt[FT], aw[FW];
+      const int at = ((((kk >> 3) + grp) ^ (col & 7)) << 3);  // rows 16m + col: row & 7 == col & 7
 #pragma unroll
-      for (int j = 0; j < FT; ++j) bt[j] = lds_operand(tl + j * 16 * kGemmPitch + kk);
+      for (int j = 0; j < FT; ++j) bt[j] = lds_operand(tl + j * 16 * kGemmPitch + at);
 #pragma unroll
-      for (int i = 0; i < FW; ++i) aw[i] = lds_operand(wl + i * 16 * kGemmPitch + kk);
+      for (int i = 0; i < FW; ++i) aw[i] = lds_operand(wl + i * 16 * kGemmPitch + at);
 #pragma unroll
       for (int i = 0; i < FW; ++i) {
 #pragma unroll
@@ -288,8 +293,9 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
 // land at the wave's LDS address in M0 + 16 L), so loads run kStages - 1
 // stages ahead of the matrix work without holding registers. A stage holds
 // 256 W rows then 256 token rows of 32 elements (64 bytes); 16-byte chunk g
-// of row r sits at position g ^ ((r >> 2) & 3), which makes the fragment
-// reads of 16 consecutive rows hit all 64 banks once. Rows past the end read
+// of row r sits at position g ^ ((r >> 1) & 3), the placement that measured
+// free of bank conflicts for the fragment reads of 16 consecutive rows on
+// MI355X. Rows past the end read
 // the last row (their outputs are not stored); K must be a multiple of 32.
 //
 // The loads are issued from inline assembly and the stages are fenced by
@@ -346,7 +352,7 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 16 * (8 * i + wave) + (lane >> 2);
-    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
     src[i] = (row < 256 ? W + static_cast<size_t>(min(w0 + row, N - 1)) * K
                         : X + static_cast<size_t>(min(t0 + row - 256, T - 1)) * K) + work.k_first + 8 * chunk;
   }
@@ -363,29 +369,66 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
 #pragma unroll
     for (int j = 0; j < FT; ++j) acc[i][j] = mfma_acc4{0.f, 0.f, 0.f, 0.f};
   }
-  const int swz = 8 * (grp ^ ((col >> 2) & 3));
+  const int swz = 8 * (grp ^ ((col >> 1) & 3));
   const int stages = work.k_len / kRingK;
-  for (int s = 0; s < kStages - 1 && s < stages; ++s) issue(s);
-  for (int s = 0; s < stages; ++s) {
-    // this wave's loads of stage s are done once at most the younger stages' remain
-    if (s + kStages - 2 < stages) {
-      wait_stage_landed<4 * (kStages - 2)>();
-    } else {
-      wait_stage_landed<0>();
-    }
-    __builtin_amdgcn_s_barrier();  // every wave's stage s has landed; stage s - 1 is no longer read
-    if (s + kStages - 1 < stages) issue(s + kStages - 1);
+  // The next stage's fragments are read during the current stage's products,
+  // so LDS reads overlap matrix work: its token fragments into the second of
+  // two sets, and each W fragment into the registers of the current one as
+  // soon as that one's four products are issued. After the barrier that
+  // precedes reading stage s + 1, every wave's reads of stage s have
+  // returned, and stage s's buffer takes stage s + kStages.
+  mfma_in8 aw[FW], bt_a[FT], bt_b[FT];
+  auto read_tokens = [&](int s, mfma_in8 (&bt)[FT]) {
     const elem_t* base = ring + (s % kStages) * kRingStage;
-    mfma_in8 bt[FT], aw[FW];
 #pragma unroll
     for (int j = 0; j < FT; ++j) bt[j] = lds_operand(base + (256 + wt + 16 * j + col) * kRingK + swz);
-#pragma unroll
-    for (int i = 0; i < FW; ++i) aw[i] = lds_operand(base + (ww + 16 * i + col) * kRingK + swz);
+  };
+  // Products of the stage whose fragments are in aw / bt, reading stage
+  // `next` into aw / bt_next. After the last stage `next` repeats a stage
+  // whose loads have all landed, and what is read goes unused.
+  auto step = [&](const mfma_in8 (&bt)[FT], mfma_in8 (&bt_next)[FT], int next) {
+    const elem_t* nb = ring + (next % kStages) * kRingStage + (ww + col) * kRingK + swz;
+    read_tokens(next, bt_next);
 #pragma unroll
     for (int i = 0; i < FW; ++i) {
 #pragma unroll
       for (int j = 0; j < FT; ++j) acc[i][j] = mfma16x16x32(aw[i], bt[j], acc[i][j]);
+      aw[i] = lds_operand(nb + 16 * i * kRingK);
     }
+    // keep that order: the token reads, then per W fragment its products and
+    // its replacement's read
+    __builtin_amdgcn_sched_group_barrier(0x100, FT, 0);
+#pragma unroll
+    for (int i = 0; i < FW; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, FT, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+  // Before reading stage `next`: this wave's loads of it have landed (at most
+  // the loads of the stages issued after it remain) and its earlier fragment
+  // reads have returned; then the block meets and the freed buffer is refilled.
+  auto advance = [&](int next) {
+    if (next + kStages - 2 < stages) {
+      wait_stage_landed<4 * (kStages - 2)>();
+    } else {
+      wait_stage_landed<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    if (next + kStages - 1 < stages) issue(next + kStages - 1);
+  };
+  for (int s = 0; s < kStages - 1 && s < stages; ++s) issue(s);
+  advance(0);
+  read_tokens(0, bt_a);
+  {
+    const elem_t* base = ring + (ww + col) * kRingK + swz;
+#pragma unroll
+    for (int i = 0; i < FW; ++i) aw[i] = lds_operand(base + 16 * i * kRingK);
+  }
+  for (int s = 0; s < stages; ++s) {
+    if (s + 1 < stages) advance(s + 1);
+    step(bt_a, bt_b, min(s + 1, stages - 1));
+#pragma unroll
+    for (int j = 0; j < FT; ++j) bt_a[j] = bt_b[j];
   }
 
   float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
@@ -554,9 +597,18 @@ __device__ __forceinline__ int value_slot(int k) {
 // two-way bank conflicted and the operand reads are conflict free.
 __device__ __forceinline__ int value_swizzle(int d) { return ((d >> 3) ^ (d >> 1)) & 7; }
 
+// Key rows are head_dim elements with 16-byte chunk c at position
+// c ^ key_swizzle(key), so the fragment reads of 16 consecutive keys are free
+// of bank conflicts (measured on MI355X for 128-byte rows; 256-byte rows
+// spread 16 rows over all 16 chunk positions).
+template <int kHeadDim>
+__device__ __forceinline__ int key_swizzle(int key) {
+  return kHeadDim == 64 ? (key & 7) : (key & 15);
+}
+
 template <int kHeadDim>
 struct FlashShared {
-  static constexpr int kKeyPitch = kHeadDim + 8;
+  static constexpr int kKeyPitch = kHeadDim;
   elem_t keys[2][kFlashKeys * kKeyPitch];
   elem_t values_t[2][kHeadDim * kFlashKeys];
 };
@@ -621,7 +673,7 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
       const int chunk = c * kFlashThreads + threadIdx.x;
       const int key = chunk / (kHeadDim / 8);
       const int d0 = (chunk % (kHeadDim / 8)) * 8;
-      store16(&sh.keys[buf][key * kKeyPitch + d0], kreg[c]);
+      store16(&sh.keys[buf][key * kKeyPitch + (((d0 >> 3) ^ key_swizzle<kHeadDim>(key)) << 3)], kreg[c]);
       if (!with_values) continue;
       const int slot = value_slot(key);
 #pragma unroll
@@ -643,7 +695,8 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
       for (int rf = 0; rf < kRF; ++rf) s[rf][kf] = mfma_acc4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < kSteps; ++ks) {
-        const mfma_in8 a = lds_operand(&sh.keys[buf][(kf * 16 + col) * kKeyPitch + ks * 32 + 8 * grp]);
+        const mfma_in8 a = lds_operand(
+            &sh.keys[buf][(kf * 16 + col) * kKeyPitch + (((ks * 4 + grp) ^ key_swizzle<kHeadDim>(col)) << 3)]);
 #pragma unroll
         for (int rf = 0; rf < kRF; ++rf) s[rf][kf] = mfma16x16x32(a, qf[rf][ks], s[rf][kf]);
       }

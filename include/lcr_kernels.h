@@ -156,6 +156,15 @@ int lcr_gemm_ws(void* Y, int y_fp32, const void* X, const void* W, int T, int N,
  * current device (0: no split). */
 size_t lcr_gemm_workspace_bytes(int T, int N, int K);
 
+/* act[t][f] = rne(silu(g) * u) with g, u the 16-bit-rounded outputs of the
+ * fused gate/up projection W_gate_up[2 ffn][K] (gate rows first, as the
+ * reference fuses them, src/model.cu:165-172): the gate/up GEMM of
+ * src/model.cu:441 and launch_swiglu_strided (src/kernels.cuh:40) in one
+ * kernel, bit-identical to the pair. ffn % 16 == 0; workspace as for
+ * lcr_gemm_ws with N = 2 ffn. */
+int lcr_gemm_swiglu_ws(void* act, const void* X, const void* W_gate_up, int T, int ffn, int K,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Causal GQA attention for a prefill chunk: the two strided-batched GEMMs and
  * the softmax of src/model.cu:509-560 (K13 gather + G6 + K10 + G7 + K7) in
  * one flash-style pass reading the cache through the view.

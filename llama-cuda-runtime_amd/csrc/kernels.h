@@ -124,6 +124,11 @@ inline void launch_gemm(void* Y, bool y_fp32, const elem_t* X, const elem_t* W, 
   check_kernel_status(lcr_gemm_ws(Y, y_fp32 ? 1 : 0, X, W, T, N, K, workspace, workspace_bytes, stream));
 }
 
+inline void launch_gemm_swiglu(elem_t* act, const elem_t* X, const elem_t* W_gate_up, int T, int ffn,
+                               int K, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  check_kernel_status(lcr_gemm_swiglu_ws(act, X, W_gate_up, T, ffn, K, workspace, workspace_bytes, stream));
+}
+
 inline void launch_prefill_attention(elem_t* out, const elem_t* q_heads, const KvCacheView& view,
                                      int num_heads, int heads_per_kv, int tokens,
                                      int start_position, float scale, bool paged,

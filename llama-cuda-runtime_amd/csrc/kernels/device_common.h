@@ -97,6 +97,9 @@ __host__ __device__ __forceinline__ float lcr_expf(float in) {
   return in != in ? in : (in_range ? y : special);
 }
 
+// silu(v) = v / (1 + exp(-v)) with the shared exp, the activation of SwiGLU.
+__host__ __device__ __forceinline__ float lcr_silu(float v) { return v / (1.0f + lcr_expf(-v)); }
+
 __host__ __device__ __forceinline__ void lcr_sincosf(float angle, float* s_out, float* c_out) {
   const double x = static_cast<double>(angle);
   const double k = __builtin_rint(x * 6.36619772367581382433e-01);

@@ -26,7 +26,7 @@ constexpr int kMaxGroupedHeads = 4;
 // and more) attention runs one block per (kv head, split) for the whole group.
 constexpr int kGroupedMinSplits = 16;
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + lcr_expf(-v)); }
+__device__ __forceinline__ float silu(float v) { return lcr_silu(v); }
 
 // RMSNorm of the residual sum v into LDS as elements:
 //   normed = rne((f(rne(v)) * scale) * f(w)),  scale from sum(v^2).

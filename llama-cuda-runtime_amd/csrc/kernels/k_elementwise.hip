@@ -25,7 +25,7 @@ int grid_for(int64_t work_items) {
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(blocks, 8192)));
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + lcr_expf(-v)); }
+__device__ __forceinline__ float silu(float v) { return lcr_silu(v); }
 
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void embedding_kernel(elem_t* __restrict__ out,

@@ -103,13 +103,32 @@ constexpr int kGemmPitch = kStageK;
 // over K into `splits` slices of k_chunk elements. A split launch writes
 // fp32 partial products, slice s to partial + s * T * N, and a second kernel
 // sums the slices in slice order.
+//
+// Gated launches (ffn > 0) compute SwiGLU of the fused gate/up projection,
+// whose weight holds the ffn gate rows then the ffn up rows: logical row p
+// reads weight row weight_row(p), so that each 32 logical rows hold 16 gate
+// rows then the 16 up rows of the same features. A wave's fragments 2m and
+// 2m + 1 then pair gate and up values of the same outputs, and the epilogue
+// writes act = rne(silu(rne(gate)) * rne(up)), the same roundings as a GEMM
+// to 16-bit followed by the SwiGLU kernel.
 struct GemmGrid {
   int tiles_t;
   int tiles_w;
   int splits;
   int k_chunk;
   float* partial;  // nullptr: no split, write Y
+  int ffn;         // > 0: gated (Y is act[T][ffn], N == 2 * ffn)
 };
+
+__device__ __forceinline__ int weight_row(int p, int ffn) {
+  return ffn == 0 ? p : (((p >> 5) << 4) | (p & 15)) + ((p & 16) ? ffn : 0);
+}
+
+__device__ __forceinline__ float swiglu_rounded(float gate, float up) {
+  const float g = elem_bits_to_float(float_to_elem_bits(gate));
+  const float u = elem_bits_to_float(float_to_elem_bits(up));
+  return elem_bits_to_float(float_to_elem_bits(lcr_silu(g) * u));
+}
 
 struct GemmWork {
   int w0, t0, k_first, k_len, split;
@@ -135,7 +154,28 @@ __device__ __forceinline__ bool gemm_work(const GemmGrid& g, int BW, int BT, int
 // acc[i][j][v] is output (token t0 + tw + 16j + col, feature w0 + ww + 16i + 4grp + v).
 template <int FW, int FT, bool kFp32Out>
 __device__ __forceinline__ void store_gemm_tile(const mfma_acc4 (&acc)[FW][FT], void* Y, float* partial,
-                                                int T, int N, int t_base, int w_base, int col, int grp) {
+                                                int T, int N, int t_base, int w_base, int col, int grp,
+                                                int ffn) {
+  if (ffn > 0 && partial == nullptr) {
+    // fragments 2m (gate) and 2m + 1 (up): features (w_base + 32m) / 2 + 4grp + v
+#pragma unroll
+    for (int j = 0; j < FT; ++j) {
+      const int t = t_base + j * 16 + col;
+      if (t >= T) continue;
+#pragma unroll
+      for (int m = 0; m < FW / 2; ++m) {
+        const int f = (w_base + 32 * m) / 2 + 4 * grp;
+        if (f >= ffn) continue;
+        uint2 packed;
+        packed.x = pack_elems(swiglu_rounded(acc[2 * m][j][0], acc[2 * m + 1][j][0]),
+                              swiglu_rounded(acc[2 * m][j][1], acc[2 * m + 1][j][1]));
+        packed.y = pack_elems(swiglu_rounded(acc[2 * m][j][2], acc[2 * m + 1][j][2]),
+                              swiglu_rounded(acc[2 * m][j][3], acc[2 * m + 1][j][3]));
+        *reinterpret_cast<uint2*>(static_cast<elem_t*>(Y) + static_cast<size_t>(t) * ffn + f) = packed;
+      }
+    }
+    return;
+  }
   const bool whole_words = (N & 3) == 0;
 #pragma unroll
   for (int j = 0; j < FT; ++j) {
@@ -210,7 +250,7 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
   for (int c = 0; c < kPerW; ++c) {
     const int row = w0 + kRowsPerPass * c + trow;
     live |= (row < N ? 1u : 0u) << c;
-    wsrc[c] = W + static_cast<size_t>(min(row, N - 1)) * K + work.k_first;
+    wsrc[c] = W + static_cast<size_t>(weight_row(min(row, N - 1), grid.ffn)) * K + work.k_first;
   }
 #pragma unroll
   for (int c = 0; c < kPerT; ++c) {
@@ -285,7 +325,7 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
   }
 
   float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
-  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp);
+  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp, grid.ffn);
 }
 
 // The large-tile GEMM with a ring of kStages LDS stages of 32 K each, filled
@@ -353,7 +393,7 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
   for (int i = 0; i < 4; ++i) {
     const int row = 16 * (8 * i + wave) + (lane >> 2);
     const int chunk = (lane & 3) ^ ((row >> 1) & 3);
-    src[i] = (row < 256 ? W + static_cast<size_t>(min(w0 + row, N - 1)) * K
+    src[i] = (row < 256 ? W + static_cast<size_t>(weight_row(min(w0 + row, N - 1), grid.ffn)) * K
                         : X + static_cast<size_t>(min(t0 + row - 256, T - 1)) * K) + work.k_first + 8 * chunk;
   }
   const uint32_t ring_base = lds_address_of(ring) + static_cast<uint32_t>(wave * 16 * kRingK * 2);
@@ -432,10 +472,36 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
   }
 
   float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
-  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp);
+  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp, grid.ffn);
 }
 
 constexpr int kRingStages = 4;
+
+// act[t][f] = SwiGLU of the summed gate and up partial products (logical
+// columns 32 (f / 16) + f % 16 and that + 16), for gated split launches.
+__global__ __launch_bounds__(256) void gemm_reduce_swiglu_kernel(elem_t* __restrict__ act,
+                                                                 const float* __restrict__ partial, int splits,
+                                                                 int T, int ffn) {
+  const size_t i = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) * 4;  // act element, f % 4 == 0
+  if (i >= static_cast<size_t>(T) * ffn) return;
+  const int t = static_cast<int>(i / ffn);
+  const int f = static_cast<int>(i % ffn);
+  const size_t n = 2 * static_cast<size_t>(ffn);
+  const size_t count = static_cast<size_t>(T) * n;
+  const size_t g_at = static_cast<size_t>(t) * n + ((f >> 4) << 5) + (f & 15);
+  float4 g = *reinterpret_cast<const float4*>(partial + g_at);
+  float4 u = *reinterpret_cast<const float4*>(partial + g_at + 16);
+  for (int s = 1; s < splits; ++s) {
+    const float4 gs = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(s) * count + g_at);
+    const float4 us = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(s) * count + g_at + 16);
+    g.x += gs.x; g.y += gs.y; g.z += gs.z; g.w += gs.w;
+    u.x += us.x; u.y += us.y; u.z += us.z; u.w += us.w;
+  }
+  uint2 packed;
+  packed.x = pack_elems(swiglu_rounded(g.x, u.x), swiglu_rounded(g.y, u.y));
+  packed.y = pack_elems(swiglu_rounded(g.z, u.z), swiglu_rounded(g.w, u.w));
+  *reinterpret_cast<uint2*>(act + i) = packed;
+}
 
 // Y = sum over slices of the fp32 partial products, in slice order.
 template <bool kFp32Out>
@@ -551,10 +617,10 @@ void launch_gemm_ring(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, 
 }
 
 void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K, void* workspace,
-              size_t workspace_bytes, hipStream_t s) {
+              size_t workspace_bytes, int ffn, hipStream_t s) {
   const GemmPlan plan = plan_gemm(T, N, K, device_compute_units(), workspace != nullptr ? workspace_bytes : 0);
   GemmGrid grid{(T + plan.bt - 1) / plan.bt, (N + plan.bw - 1) / plan.bw, plan.splits, plan.k_chunk,
-                plan.splits > 1 ? static_cast<float*>(workspace) : nullptr};
+                plan.splits > 1 ? static_cast<float*>(workspace) : nullptr, ffn};
   switch (plan.shape) {
     case GemmShape::kRing256x256:
       launch_gemm_ring(Y, fp32_out, X, W, T, N, K, grid, s);
@@ -569,7 +635,11 @@ void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
       launch_gemm_tiles<128, 128, 2, 2>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
   }
-  if (plan.splits > 1) {
+  if (plan.splits > 1 && ffn > 0) {
+    const size_t count = static_cast<size_t>(T) * ffn;
+    gemm_reduce_swiglu_kernel<<<static_cast<unsigned>((count + 1023) / 1024), 256, 0, s>>>(
+        static_cast<elem_t*>(Y), grid.partial, plan.splits, T, ffn);
+  } else if (plan.splits > 1) {
     const size_t count = static_cast<size_t>(T) * N;
     const unsigned blocks = static_cast<unsigned>((count + 1023) / 1024);
     if (fp32_out) {
@@ -937,7 +1007,7 @@ extern "C" int lcr_gemm(void* Y, int y_fp32, const void* X, const void* W, int T
                         void* stream) {
   const int status = gemm_checks(Y, X, W, T, N, K);
   if (status != LCR_OK || T == 0 || N == 0) return status;
-  run_gemm(Y, y_fp32 != 0, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W), T, N, K, nullptr, 0,
+  run_gemm(Y, y_fp32 != 0, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W), T, N, K, nullptr, 0, 0,
            static_cast<hipStream_t>(stream));
   CAPI_LAUNCHED();
   return LCR_OK;
@@ -956,7 +1026,22 @@ extern "C" int lcr_gemm_ws(void* Y, int y_fp32, const void* X, const void* W, in
                                                                                << " bytes has no pointer");
   CAPI_CHECK((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "gemm workspace must be 16-byte aligned");
   run_gemm(Y, y_fp32 != 0, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W), T, N, K, workspace,
-           workspace_bytes, static_cast<hipStream_t>(stream));
+           workspace_bytes, 0, static_cast<hipStream_t>(stream));
+  CAPI_LAUNCHED();
+  return LCR_OK;
+}
+
+extern "C" int lcr_gemm_swiglu_ws(void* act, const void* X, const void* W_gate_up, int T, int ffn, int K,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  CAPI_CHECK(ffn >= 0, "gemm_swiglu needs a non-negative ffn width");
+  CAPI_CHECK(ffn % 16 == 0, "gemm_swiglu needs ffn to be a multiple of 16, got " << ffn);
+  const int status = gemm_checks(act, X, W_gate_up, T, 2 * ffn, K);
+  if (status != LCR_OK || T == 0 || ffn == 0) return status;
+  CAPI_CHECK(workspace != nullptr || workspace_bytes == 0, "gemm workspace of " << workspace_bytes
+                                                                               << " bytes has no pointer");
+  CAPI_CHECK((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "gemm workspace must be 16-byte aligned");
+  run_gemm(act, false, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W_gate_up), T, 2 * ffn, K,
+           workspace, workspace_bytes, ffn, static_cast<hipStream_t>(stream));
   CAPI_LAUNCHED();
   return LCR_OK;
 }

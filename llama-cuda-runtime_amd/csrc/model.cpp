@@ -615,18 +615,24 @@ void Model::run_layers(int tokens, int start_position) {
       launch_add_residual_rmsnorm(normed_, x_, proj_out_, w.post_attention_norm, tokens, hidden,
                                   config_.rms_norm_eps, stream_);
     }
-    {
-      ProfileScope scope(&profiler_, "gate/up", stream_);
-      if (tokens == 1) {
-        launch_gemv(gate_up_, false, w.gate_up_proj, normed_, 2 * ffn, hidden, stream_);
-      } else {
-        launch_gemm(gate_up_, false, normed_, w.gate_up_proj, tokens, 2 * ffn, hidden,
-                    gemm_workspace_, gemm_workspace_size_, stream_);
+    if (tokens > 1 && ffn % 16 == 0) {
+      ProfileScope scope(&profiler_, "gate/up+swiglu", stream_);
+      launch_gemm_swiglu(act_, normed_, w.gate_up_proj, tokens, ffn, hidden, gemm_workspace_,
+                         gemm_workspace_size_, stream_);
+    } else {
+      {
+        ProfileScope scope(&profiler_, "gate/up", stream_);
+        if (tokens == 1) {
+          launch_gemv(gate_up_, false, w.gate_up_proj, normed_, 2 * ffn, hidden, stream_);
+        } else {
+          launch_gemm(gate_up_, false, normed_, w.gate_up_proj, tokens, 2 * ffn, hidden,
+                      gemm_workspace_, gemm_workspace_size_, stream_);
+        }
       }
-    }
-    {
-      ProfileScope scope(&profiler_, "swiglu", stream_);
-      launch_swiglu_strided(act_, gate_up_, gate_up_ + ffn, tokens, ffn, 2 * ffn, stream_);
+      {
+        ProfileScope scope(&profiler_, "swiglu", stream_);
+        launch_swiglu_strided(act_, gate_up_, gate_up_ + ffn, tokens, ffn, 2 * ffn, stream_);
+      }
     }
     {
       ProfileScope scope(&profiler_, "down", stream_);

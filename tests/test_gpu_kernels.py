@@ -397,6 +397,30 @@ def test_gemm_workspace_plans(gpu):
     assert lib.lcr_gemm_workspace_bytes(0, 2048, 2048) == 0
 
 
+@pytest.mark.parametrize("T,F,K", [(2048, 8192, 2048), (512, 8192, 2048), (37, 8192, 2048), (300, 1024, 520),
+                                   (130, 48, 64)])
+def test_gemm_swiglu_matches_gemm_then_swiglu(gpu, T, F, K):
+    """The fused gate/up projection + SwiGLU gives the bits of the GEMM to
+    16-bit followed by the SwiGLU kernel (the roundings are the same and the
+    GEMM sums each output over K in the same order), with the workspace's
+    split plan and without a workspace."""
+    lib = gpu
+    r = rng(T + F + K)
+    Xd = dev(random_elems(r, (T, K)))
+    Wd = dev(random_elems(r, (2 * F, K), 0.05))
+    ws_bytes = lib.lcr_gemm_workspace_bytes(T, 2 * F, K)
+    ws = zeros_dev(max(ws_bytes, 16) // 4, np.float32)
+    for wsp, wsb in ((p(ws), ws_bytes), (None, 0)):
+        gate_up = zeros_dev(T * 2 * F)
+        ok(lib, lib.lcr_gemm_ws(p(gate_up), 0, p(Xd), p(Wd), T, 2 * F, K, wsp, wsb, NULL), "gemm_ws")
+        want = zeros_dev(T * F)
+        ok(lib, lib.lcr_swiglu_strided(p(want), p(gate_up), ctypes.c_void_p(gate_up.ptr + 2 * F), T, F, 2 * F, NULL),
+           "swiglu_strided")
+        got = zeros_dev(T * F)
+        ok(lib, lib.lcr_gemm_swiglu_ws(p(got), p(Xd), p(Wd), T, F, K, wsp, wsb, NULL), "gemm_swiglu_ws")
+        expect_bits_equal(host(got), host(want), f"gemm+swiglu {T}x{F}x{K} workspace {wsb}")
+
+
 PREFILL_CASES = [
     # (num_heads, kv_heads, head_dim, tokens, start, paged)
     (32, 8, 64, 7, 0, False),

@@ -8,6 +8,8 @@ compiler that merges a multiply with the following f32 -> f16 rounding into a
 mixed-precision fma with a +0 addend fails the cancellation case.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -121,3 +123,31 @@ def test_small_model_fp16_all_paths(gpu, lcr, tmp_path):
             tok = oracle.argmax(want)
         m.close()
         ref.close()
+
+
+@pytest.mark.parametrize("T,N,K", [(300, 2048, 2048), (1000, 16384, 2048), (64, 2048, 8192)])
+def test_gemm_fp16(gpu, lcr, T, N, K):
+    """The fp16 MFMA GEMM (all tile shapes, with and without a K split)
+    against a float64 product, and its fused SwiGLU form against the GEMM
+    followed by the SwiGLU kernel, bit for bit."""
+    lib = lcr.load_library("fp16")
+    r = rng(T + N + K)
+    X = random_elems(r, (T, K), kind=FP16)
+    W = random_elems(r, (N, K), 0.02, kind=FP16)
+    Xd, Wd = dev(X), dev(W)
+    exp = oracle.elems_to_f32(X, FP16).astype(np.float64) @ oracle.elems_to_f32(W, FP16).astype(np.float64).T
+    ws_bytes = lib.lcr_gemm_workspace_bytes(T, N, K)
+    ws = zeros_dev(max(ws_bytes, 16) // 4, np.float32)
+    Y = zeros_dev(T * N, np.float32)
+    ok(lib, lib.lcr_gemm_ws(p(Y), 1, p(Xd), p(Wd), T, N, K, p(ws), ws_bytes, None), "gemm_ws fp16")
+    got = host(Y, np.float32).reshape(T, N).astype(np.float64)
+    assert np.abs(got - exp).max() <= 1e-4 * np.abs(exp).max()
+    F = N // 2
+    gate_up = zeros_dev(T * N)
+    ok(lib, lib.lcr_gemm_ws(p(gate_up), 0, p(Xd), p(Wd), T, N, K, p(ws), ws_bytes, None), "gemm_ws fp16 out")
+    want = zeros_dev(T * F)
+    ok(lib, lib.lcr_swiglu_strided(p(want), p(gate_up), ctypes.c_void_p(gate_up.ptr + 2 * F), T, F, N, None),
+       "swiglu_strided fp16")
+    fused = zeros_dev(T * F)
+    ok(lib, lib.lcr_gemm_swiglu_ws(p(fused), p(Xd), p(Wd), T, F, K, p(ws), ws_bytes, None), "gemm_swiglu fp16")
+    expect_bits_equal(host(fused), host(want), "fp16 gemm+swiglu")

@@ -205,6 +205,10 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=256)
     ap.add_argument("--counters", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 3 / config 4 measurements")
+    ap.add_argument("--prefill", type=int, default=0, metavar="T",
+                    help="only run the config 4 prefill of T tokens and print its JSON (for profiling)")
+    ap.add_argument("--long-context", type=int, default=0, metavar="CTX",
+                    help="only run the config 3 decode at context CTX and print its JSON (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -226,6 +230,12 @@ def main() -> int:
     prompt = lcr.synthetic_tokens(args.prompt, config["vocab_size"], seed=lcr.PROMPT_SEED)
     if args.counters:
         return counters_run(lcr, model_dir, prompt, args.max_seq)
+    if args.prefill > 0:
+        print(json.dumps({"prefill_config4": prefill_run(lcr, model_dir, config, args.prefill)}))
+        return 0
+    if args.long_context > 0:
+        print(json.dumps({"long_context": long_context(lcr, model_dir, config, args.long_context)}))
+        return 0
     t0 = time.perf_counter()
     model = lcr.Model(model_dir, max_seq=args.max_seq)
     load_s = time.perf_counter() - t0

@@ -5,7 +5,8 @@
 //   out[i]        = lo * cos(a) - hi * sin(a)
 //   out[i + half] = hi * cos(a) + lo * sin(a)
 // computed as separate multiplies and a subtract/add (no fusion), with
-// sin/cos from lcr_sincosf. The query kernel writes the head-major
+// sin/cos from lcr_sincosf, evaluated once per (token, i) and shared by every
+// head of the token. The query kernel writes the head-major
 // [num_heads][tokens][head_dim] layout; the key kernel writes K (rotated) and V
 // (copied) straight into the cache at KvCacheView::offset.
 #include <algorithm>
@@ -17,52 +18,75 @@
 namespace lcr {
 namespace {
 
-__device__ __forceinline__ void rotate_pair(float lo, float hi, float position, float freq,
-                                            float* out_lo, float* out_hi) {
-  float s, c;
-  lcr_sincosf(position * freq, &s, &c);
-  *out_lo = lo * c - hi * s;
-  *out_hi = hi * c + lo * s;
+constexpr int kRopeThreads = 256;
+constexpr int kMaxRopeHalf = 256;  // head_dim up to 512
+
+// One block per token: the head_dim/2 angles of the token's position are
+// evaluated once into LDS (cos, sin), then every head's pairs are rotated.
+__device__ __forceinline__ void token_angles(float2* cs, const float* inv_freq, int position, int half) {
+  for (int i = threadIdx.x; i < half; i += kRopeThreads) {
+    float s, c;
+    lcr_sincosf(static_cast<float>(position) * inv_freq[i], &s, &c);
+    cs[i] = make_float2(c, s);
+  }
+  __syncthreads();
 }
 
-__global__ void rope_q_kernel(elem_t* __restrict__ q_heads, const elem_t* __restrict__ q_proj,
-                              const float* __restrict__ inv_freq, int tokens, int start_position,
-                              int head_dim, int src_row_stride) {
+__device__ __forceinline__ void rotate(float lo, float hi, float2 cs, float* out_lo, float* out_hi) {
+  *out_lo = lo * cs.x - hi * cs.y;
+  *out_hi = hi * cs.x + lo * cs.y;
+}
+
+__global__ __launch_bounds__(kRopeThreads) void rope_q_kernel(elem_t* __restrict__ q_heads,
+                                                             const elem_t* __restrict__ q_proj,
+                                                             const float* __restrict__ inv_freq,
+                                                             int tokens, int start_position, int num_heads,
+                                                             int head_dim, int src_row_stride) {
+  __shared__ float2 cs[kMaxRopeHalf];
   const int t = blockIdx.x;
-  const int h = blockIdx.y;
   const int half = head_dim / 2;
-  const float position = static_cast<float>(start_position + t);
-  const int64_t src = static_cast<int64_t>(t) * src_row_stride + static_cast<int64_t>(h) * head_dim;
-  const int64_t dst = (static_cast<int64_t>(h) * tokens + t) * head_dim;
-  for (int i = threadIdx.x; i < half; i += blockDim.x) {
+  token_angles(cs, inv_freq, start_position + t, half);
+  const int64_t src = static_cast<int64_t>(t) * src_row_stride;
+  for (int idx = threadIdx.x; idx < num_heads * half; idx += kRopeThreads) {
+    const int h = idx / half;
+    const int i = idx - h * half;
+    const int64_t s = src + static_cast<int64_t>(h) * head_dim + i;
+    const int64_t dst = (static_cast<int64_t>(h) * tokens + t) * head_dim + i;
     float a, b;
-    rotate_pair(elem_to_float(q_proj[src + i]), elem_to_float(q_proj[src + i + half]), position,
-                inv_freq[i], &a, &b);
-    q_heads[dst + i] = float_to_elem(a);
-    q_heads[dst + i + half] = float_to_elem(b);
+    rotate(elem_to_float(q_proj[s]), elem_to_float(q_proj[s + half]), cs[i], &a, &b);
+    q_heads[dst] = float_to_elem(a);
+    q_heads[dst + half] = float_to_elem(b);
   }
 }
 
 template <bool kPaged>
-__global__ void rope_write_kv_kernel(KvCacheView view, const elem_t* __restrict__ k_proj,
-                                     const elem_t* __restrict__ v_proj,
-                                     const float* __restrict__ inv_freq, int start_position,
-                                     int src_row_stride) {
+__global__ __launch_bounds__(kRopeThreads) void rope_write_kv_kernel(KvCacheView view,
+                                                                    const elem_t* __restrict__ k_proj,
+                                                                    const elem_t* __restrict__ v_proj,
+                                                                    const float* __restrict__ inv_freq,
+                                                                    int start_position, int src_row_stride) {
+  __shared__ float2 cs[kMaxRopeHalf];
   const int t = blockIdx.x;
-  const int h = blockIdx.y;
   const int head_dim = view.head_dim;
   const int half = head_dim / 2;
   const int position = start_position + t;
-  const int64_t src = static_cast<int64_t>(t) * src_row_stride + static_cast<int64_t>(h) * head_dim;
-  const size_t dst = view.offset<kPaged>(h, position);
-  for (int i = threadIdx.x; i < half; i += blockDim.x) {
+  token_angles(cs, inv_freq, position, half);
+  const int64_t src = static_cast<int64_t>(t) * src_row_stride;
+  for (int idx = threadIdx.x; idx < view.num_kv_heads * half; idx += kRopeThreads) {
+    const int h = idx / half;
+    const int i = idx - h * half;
+    const int64_t s = src + static_cast<int64_t>(h) * head_dim + i;
+    const size_t dst = view.offset<kPaged>(h, position) + i;
     float a, b;
-    rotate_pair(elem_to_float(k_proj[src + i]), elem_to_float(k_proj[src + i + half]),
-                static_cast<float>(position), inv_freq[i], &a, &b);
-    view.keys[dst + i] = float_to_elem(a);
-    view.keys[dst + i + half] = float_to_elem(b);
+    rotate(elem_to_float(k_proj[s]), elem_to_float(k_proj[s + half]), cs[i], &a, &b);
+    view.keys[dst] = float_to_elem(a);
+    view.keys[dst + half] = float_to_elem(b);
   }
-  for (int i = threadIdx.x; i < head_dim; i += blockDim.x) view.values[dst + i] = v_proj[src + i];
+  for (int idx = threadIdx.x; idx < view.num_kv_heads * head_dim; idx += kRopeThreads) {
+    const int h = idx / head_dim;
+    const int i = idx - h * head_dim;
+    view.values[view.offset<kPaged>(h, position) + i] = v_proj[src + static_cast<int64_t>(h) * head_dim + i];
+  }
 }
 
 }  // namespace
@@ -77,11 +101,10 @@ extern "C" int lcr_rope_q(void* q_heads, const void* q_proj, const float* inv_fr
   if (tokens == 0 || num_heads == 0) return LCR_OK;
   CAPI_CHECK(head_dim > 0 && head_dim % 2 == 0,
              "head_dim must be positive and even for RoPE, got " << head_dim);
-  const dim3 grid(static_cast<unsigned>(tokens), static_cast<unsigned>(num_heads));
-  const int block = std::min(256, ((head_dim / 2 + 63) / 64) * 64);
-  rope_q_kernel<<<grid, block, 0, static_cast<hipStream_t>(stream)>>>(
+  CAPI_CHECK(head_dim / 2 <= kMaxRopeHalf, "rope_q supports head_dim up to " << 2 * kMaxRopeHalf);
+  rope_q_kernel<<<static_cast<unsigned>(tokens), kRopeThreads, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<elem_t*>(q_heads), static_cast<const elem_t*>(q_proj), inv_freq, tokens,
-      start_position, head_dim, src_row_stride);
+      start_position, num_heads, head_dim, src_row_stride);
   CAPI_LAUNCHED();
   return LCR_OK;
 }
@@ -96,8 +119,10 @@ extern "C" int lcr_rope_write_kv(const lcr_kv_view* view, const void* k_proj, co
   CAPI_CHECK(v.head_dim > 0 && v.head_dim % 2 == 0,
              "head_dim must be positive and even for RoPE, got " << v.head_dim);
   CAPI_CHECK(!paged || v.page_table != nullptr, "a paged cache view needs a page table");
-  const dim3 grid(static_cast<unsigned>(tokens), static_cast<unsigned>(v.num_kv_heads));
-  const int block = std::min(256, ((v.head_dim + 63) / 64) * 64);
+  CAPI_CHECK(v.head_dim / 2 <= kMaxRopeHalf, "rope_write_kv supports head_dim up to " << 2 * kMaxRopeHalf);
+  if (v.num_kv_heads == 0) return LCR_OK;
+  const unsigned grid = static_cast<unsigned>(tokens);
+  const int block = kRopeThreads;
   auto s = static_cast<hipStream_t>(stream);
   auto* k = static_cast<const elem_t*>(k_proj);
   auto* vv = static_cast<const elem_t*>(v_proj);

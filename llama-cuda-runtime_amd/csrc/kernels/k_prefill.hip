@@ -654,8 +654,13 @@ void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
 // Prefill attention (MFMA, flash-style)
 // ---------------------------------------------------------------------------
 
-constexpr int kFlashThreads = 256;  // four waves: the query heads of one kv head
-constexpr int kFlashKeys = 64;      // keys per staged tile
+// Eight waves: the four query heads of one kv head, each over two key groups
+// (the even and the odd 64-key tiles), so a block walks its keys in half the
+// steps; the two groups merge their statistics and their outputs at fixed
+// points, group 0 first.
+constexpr int kFlashThreads = 512;
+constexpr int kFlashKeys = 64;      // keys per tile; two tiles are staged per step
+constexpr int kKeyGroups = 2;
 
 // Slot of key k (0..63) of a tile in the transposed value rows: the order in
 // which a wave's S^T accumulators hand keys to the P operand. MFMA k-slot
@@ -676,11 +681,12 @@ __device__ __forceinline__ int key_swizzle(int key) {
   return kHeadDim == 64 ? (key & 7) : (key & 15);
 }
 
-template <int kHeadDim>
+template <int kHeadDim, int kRows>
 struct FlashShared {
   static constexpr int kKeyPitch = kHeadDim;
-  elem_t keys[2][kFlashKeys * kKeyPitch];
-  elem_t values_t[2][kHeadDim * kFlashKeys];
+  elem_t keys[2][kKeyGroups * kFlashKeys * kKeyPitch];           // two tiles per buffer
+  elem_t values_t[2][kKeyGroups][kHeadDim * kFlashKeys];
+  float stats[kFlashThreads / 64][kRows][2];                       // per wave: row max, row sum
 };
 
 template <bool kPaged, int kHeadDim, int kRF>
@@ -690,11 +696,13 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
   constexpr int kRows = 16 * kRF;                         // query positions per block
   constexpr int kSteps = kHeadDim / 32;                   // MFMA k-steps over head_dim
   constexpr int kDFrags = kHeadDim / 16;                  // output fragments over head_dim
-  constexpr int kChunks = kFlashKeys * kHeadDim / 8;      // 16-byte chunks per K (or V) tile
+  constexpr int kPairKeys = kKeyGroups * kFlashKeys;      // keys staged per step
+  constexpr int kChunks = kPairKeys * kHeadDim / 8;       // 16-byte chunks of K (or V) per step
   constexpr int kPer = kChunks / kFlashThreads;
-  constexpr int kKeyPitch = FlashShared<kHeadDim>::kKeyPitch;
-  static_assert(kChunks % kFlashThreads == 0, "tile must split evenly over the block");
-  __shared__ __attribute__((aligned(16))) FlashShared<kHeadDim> sh;
+  constexpr int kKeyPitch = FlashShared<kHeadDim, kRows>::kKeyPitch;
+  static_assert(kChunks % kFlashThreads == 0, "a step must split evenly over the block");
+  static_assert(kKeyGroups * 4 == kFlashThreads / 64, "one wave per (head, key group)");
+  __shared__ __attribute__((aligned(16))) FlashShared<kHeadDim, kRows> sh;
 
   const int r0 = static_cast<int>(gridDim.x - 1u - blockIdx.x) * kRows;  // longest rows first
   const int kv = blockIdx.y;
@@ -702,13 +710,15 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
   const int lane = lane_id();
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int g = blockIdx.z * 4 + wave;
+  const int kg = wave >> 2;  // key group: tiles kg, kg + 2, ...
+  const int g = blockIdx.z * 4 + (wave & 3);
   const bool active = g < group;
   const int head = kv * group + (active ? g : 0);
 
   const int last_key = start_position + tokens - 1;
   const int block_keys = start_position + min(r0 + kRows, tokens);
   const int tiles = (block_keys + kFlashKeys - 1) / kFlashKeys;
+  const int steps = (tiles + kKeyGroups - 1) / kKeyGroups;
 
   // Q fragments, the N side of S^T: row r0 + 16rf + col, dims 32ks + 8grp .. +7.
   mfma_in8 qf[kRF][kSteps];
@@ -725,14 +735,15 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
     }
   }
 
+  // Step `step` stages tiles 2 step and 2 step + 1: keys 128 step .. +127.
   vec16 kreg[kPer], vreg[kPer];
-  auto fetch = [&](int tile, bool with_values) {
+  auto fetch = [&](int step, bool with_values) {
 #pragma unroll
     for (int c = 0; c < kPer; ++c) {
       const int chunk = c * kFlashThreads + threadIdx.x;
       const int key = chunk / (kHeadDim / 8);
       const int d0 = (chunk % (kHeadDim / 8)) * 8;
-      const size_t at = view.offset<kPaged>(kv, min(tile * kFlashKeys + key, last_key)) + d0;
+      const size_t at = view.offset<kPaged>(kv, min(step * kPairKeys + key, last_key)) + d0;
       kreg[c] = load16(view.keys + at);
       if (with_values) vreg[c] = load16(view.values + at);
     }
@@ -745,20 +756,22 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
       const int d0 = (chunk % (kHeadDim / 8)) * 8;
       store16(&sh.keys[buf][key * kKeyPitch + (((d0 >> 3) ^ key_swizzle<kHeadDim>(key)) << 3)], kreg[c]);
       if (!with_values) continue;
-      const int slot = value_slot(key);
+      const int slot = value_slot(key & (kFlashKeys - 1));
+      elem_t* vt = sh.values_t[buf][key / kFlashKeys];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int d = d0 + j;
         const uint16_t bits = static_cast<uint16_t>(vreg[c].w[j >> 1] >> (16 * (j & 1)));
-        sh.values_t[buf][d * kFlashKeys + ((((slot >> 3) ^ value_swizzle(d)) << 3) | (slot & 7))] =
-            elem_t{bits};
+        vt[d * kFlashKeys + ((((slot >> 3) ^ value_swizzle(d)) << 3) | (slot & 7))] = elem_t{bits};
       }
     }
   };
-  // Scores of one staged tile in base-2 units (scale * log2(e) * q . k),
-  // transposed: s[rf][kf][v] is row 16rf + col against key 16kf + 4grp + v;
-  // keys past a row's position are -inf.
+  // Scores of this wave's tile of a staged step in base-2 units
+  // (scale * log2(e) * q . k), transposed: s[rf][kf][v] is row 16rf + col
+  // against key 16kf + 4grp + v of tile `tile`; keys past a row's position
+  // are -inf.
   auto scores = [&](int buf, int tile, mfma_acc4 (&s)[kRF][4]) {
+    const elem_t* kb = &sh.keys[buf][kg * kFlashKeys * kKeyPitch];
 #pragma unroll
     for (int kf = 0; kf < 4; ++kf) {
 #pragma unroll
@@ -766,7 +779,7 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
 #pragma unroll
       for (int ks = 0; ks < kSteps; ++ks) {
         const mfma_in8 a = lds_operand(
-            &sh.keys[buf][(kf * 16 + col) * kKeyPitch + (((ks * 4 + grp) ^ key_swizzle<kHeadDim>(col)) << 3)]);
+            kb + (kf * 16 + col) * kKeyPitch + (((ks * 4 + grp) ^ key_swizzle<kHeadDim>(col)) << 3));
 #pragma unroll
         for (int rf = 0; rf < kRF; ++rf) s[rf][kf] = mfma16x16x32(a, qf[rf][ks], s[rf][kf]);
       }
@@ -795,8 +808,8 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
     }
   };
 
-  // Pass 1: row max M and sum L = sum exp(s - M), keys only. The sum is kept
-  // per lane against a running max and rescaled when the max grows.
+  // Pass 1: per key group, row max m and sum l of exp(s - m), keys only; the
+  // sum is kept per lane against a running max and rescaled when it grows.
   float m[kRF], l[kRF];
 #pragma unroll
   for (int rf = 0; rf < kRF; ++rf) {
@@ -806,10 +819,11 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
   fetch(0, false);
   deposit(0, false);
   __syncthreads();
-  for (int tile = 0; tile < tiles; ++tile) {
-    const int buf = tile & 1;
-    if (tile + 1 < tiles) fetch(tile + 1, false);
-    if (active) {
+  for (int step = 0; step < steps; ++step) {
+    const int buf = step & 1;
+    if (step + 1 < steps) fetch(step + 1, false);
+    const int tile = kKeyGroups * step + kg;
+    if (active && tile < tiles) {
       mfma_acc4 s[kRF][4];
       scores(buf, tile, s);
 #pragma unroll
@@ -823,30 +837,54 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
         mt = fmaxf(mt, xor_lane<16>(mt));
         mt = fmaxf(mt, xor_lane<32>(mt));
         const float m_new = fmaxf(m[rf], mt);
+        // Until a row has seen a visible key in this group (group 1's first
+        // tiles can be fully masked for the early rows) its max is -inf; the
+        // exponentials are then taken against 0, all of them are 0, and l
+        // stays 0.
+        const float base = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
         float sum = 0.0f;
 #pragma unroll
         for (int kf = 0; kf < 4; ++kf) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) sum += __builtin_amdgcn_exp2f(s[rf][kf][v] - m_new);
+          for (int v = 0; v < 4; ++v) sum += __builtin_amdgcn_exp2f(s[rf][kf][v] - base);
         }
-        l[rf] = __builtin_fmaf(l[rf], __builtin_amdgcn_exp2f(m[rf] - m_new), sum);
+        l[rf] = m[rf] == m_new ? l[rf] + sum : __builtin_fmaf(l[rf], __builtin_amdgcn_exp2f(m[rf] - base), sum);
         m[rf] = m_new;
       }
     }
-    if (tile + 1 < tiles) deposit(buf ^ 1, false);
+    if (step + 1 < steps) deposit(buf ^ 1, false);
     __syncthreads();
   }
-  float inv[kRF];
+  // Merge the two key groups, group 0 first: M = max(m0, m1),
+  // L = l0 exp(m0 - M) + l1 exp(m1 - M). Group 0 holds key 0, visible to every
+  // row, so M is finite; a group with no visible key has m = -inf and
+  // contributes 0.
 #pragma unroll
   for (int rf = 0; rf < kRF; ++rf) {
     float total = l[rf];
     total += xor_lane<16>(total);
     total += xor_lane<32>(total);
-    inv[rf] = 1.0f / total;
+    if (grp == 0) {
+      sh.stats[wave][rf * 16 + col][0] = m[rf];
+      sh.stats[wave][rf * 16 + col][1] = total;
+    }
+  }
+  __syncthreads();
+  float inv[kRF];
+#pragma unroll
+  for (int rf = 0; rf < kRF; ++rf) {
+    const int h = wave & 3;
+    const float m0 = sh.stats[h][rf * 16 + col][0], l0 = sh.stats[h][rf * 16 + col][1];
+    const float m1 = sh.stats[h + 4][rf * 16 + col][0], l1 = sh.stats[h + 4][rf * 16 + col][1];
+    const float M = fmaxf(m0, m1);
+    const float L = __builtin_fmaf(l1, __builtin_amdgcn_exp2f(m1 - M), l0 * __builtin_amdgcn_exp2f(m0 - M));
+    m[rf] = M;
+    inv[rf] = 1.0f / L;
   }
 
   // Pass 2: p = exp(s - M) * (1/L) rounded to the element type, where the
-  // reference rounds its probability buffer, then O^T += V^T . P^T in fp32.
+  // reference rounds its probability buffer, then O^T += V^T . P^T in fp32 per
+  // key group; the groups' outputs add at the end, group 0 first.
   mfma_acc4 o[kRF][kDFrags];
 #pragma unroll
   for (int rf = 0; rf < kRF; ++rf) {
@@ -856,12 +894,14 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
   fetch(0, true);
   deposit(0, true);
   __syncthreads();
-  for (int tile = 0; tile < tiles; ++tile) {
-    const int buf = tile & 1;
-    if (tile + 1 < tiles) fetch(tile + 1, true);
-    if (active) {
+  for (int step = 0; step < steps; ++step) {
+    const int buf = step & 1;
+    if (step + 1 < steps) fetch(step + 1, true);
+    const int tile = kKeyGroups * step + kg;
+    if (active && tile < tiles) {
       mfma_acc4 s[kRF][4];
       scores(buf, tile, s);
+      const elem_t* vt = sh.values_t[buf][kg];
 #pragma unroll
       for (int rf = 0; rf < kRF; ++rf) {
         uint32_t pk[4][2];
@@ -874,24 +914,38 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
           pk[kf][1] = pack_rounded(pr[2], pr[3]);
         }
 #pragma unroll
-        for (int step = 0; step < 2; ++step) {
-          const vec16 pw{{pk[2 * step][0], pk[2 * step][1], pk[2 * step + 1][0], pk[2 * step + 1][1]}};
+        for (int half = 0; half < 2; ++half) {
+          const vec16 pw{{pk[2 * half][0], pk[2 * half][1], pk[2 * half + 1][0], pk[2 * half + 1][1]}};
           const mfma_in8 b = as_operand(pw);
 #pragma unroll
           for (int df = 0; df < kDFrags; ++df) {
             const int d = df * 16 + col;
-            const mfma_in8 a = lds_operand(
-                &sh.values_t[buf][d * kFlashKeys + (((step * 4 + grp) ^ value_swizzle(d)) << 3)]);
+            const mfma_in8 a = lds_operand(&vt[d * kFlashKeys + (((half * 4 + grp) ^ value_swizzle(d)) << 3)]);
             o[rf][df] = mfma16x16x32(a, b, o[rf][df]);
           }
         }
       }
     }
-    if (tile + 1 < tiles) deposit(buf ^ 1, true);
+    if (step + 1 < steps) deposit(buf ^ 1, true);
     __syncthreads();
   }
 
-  if (!active) return;
+  // Group 1 hands its partial output to group 0 through the (now free) key
+  // buffers; group 0 adds it to its own and stores.
+  float* handoff = reinterpret_cast<float*>(&sh.keys[0][0]);
+  static_assert(sizeof(sh.keys) >= 4 * kRF * kDFrags * 4 * 64 * sizeof(float), "handoff must fit");
+  if (kg == 1) {
+#pragma unroll
+    for (int rf = 0; rf < kRF; ++rf) {
+#pragma unroll
+      for (int df = 0; df < kDFrags; ++df) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) handoff[((((wave & 3) * kRF + rf) * kDFrags + df) * 4 + v) * 64 + lane] = o[rf][df][v];
+      }
+    }
+  }
+  __syncthreads();
+  if (!active || kg == 1) return;
   // o[rf][df][v] = O[row 16rf + col][dim 16df + 4grp + v]
 #pragma unroll
   for (int rf = 0; rf < kRF; ++rf) {
@@ -901,9 +955,12 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
                   static_cast<size_t>(head) * kHeadDim + 4 * grp;
 #pragma unroll
     for (int df = 0; df < kDFrags; ++df) {
+      float r[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) r[v] = o[rf][df][v] + handoff[((((wave & 3) * kRF + rf) * kDFrags + df) * 4 + v) * 64 + lane];
       uint2 packed;
-      packed.x = pack_elems(o[rf][df][0], o[rf][df][1]);
-      packed.y = pack_elems(o[rf][df][2], o[rf][df][3]);
+      packed.x = pack_elems(r[0], r[1]);
+      packed.y = pack_elems(r[2], r[3]);
       *reinterpret_cast<uint2*>(dst + df * 16) = packed;
     }
   }
@@ -974,17 +1031,11 @@ void launch_flash(elem_t* o, const elem_t* q, const KvCacheView& v, int num_head
                   int tokens, int start_position, float scale, hipStream_t s) {
   const float scale_log2e = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   const unsigned zs = static_cast<unsigned>((group + 3) / 4);
-  // Two row fragments per wave when that still gives two blocks per compute unit.
-  const long long wide_blocks = static_cast<long long>((tokens + 31) / 32) * v.num_kv_heads * zs;
-  if (wide_blocks >= 2LL * device_compute_units()) {
-    const dim3 grid(static_cast<unsigned>((tokens + 31) / 32), static_cast<unsigned>(v.num_kv_heads), zs);
-    flash_prefill_kernel<kPaged, kHeadDim, 2><<<grid, kFlashThreads, 0, s>>>(
-        o, q, v, num_heads, group, tokens, start_position, scale_log2e);
-  } else {
-    const dim3 grid(static_cast<unsigned>((tokens + 15) / 16), static_cast<unsigned>(v.num_kv_heads), zs);
-    flash_prefill_kernel<kPaged, kHeadDim, 1><<<grid, kFlashThreads, 0, s>>>(
-        o, q, v, num_heads, group, tokens, start_position, scale_log2e);
-  }
+  // One row fragment (16 positions) per wave: more, lighter blocks (two per
+  // compute unit) measured faster than two fragments per wave at every T.
+  const dim3 grid(static_cast<unsigned>((tokens + 15) / 16), static_cast<unsigned>(v.num_kv_heads), zs);
+  flash_prefill_kernel<kPaged, kHeadDim, 1><<<grid, kFlashThreads, 0, s>>>(o, q, v, num_heads, group, tokens,
+                                                                          start_position, scale_log2e);
 }
 
 }  // namespace

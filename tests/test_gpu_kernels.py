@@ -47,7 +47,11 @@ def test_embedding_lookup(gpu, orc):
     expect_bits_equal(host(out2), table2[ids].ravel(), "embedding odd")
 
 
-@pytest.mark.parametrize("tokens,dim", [(5, 2048), (3, 1000), (1, 8), (2, 20000)])
+# 16-byte path with 1, 2 and 4 chunks per thread (2048, 4096, 3000, 8192), the
+# element paths (1000 and 999: not a multiple of 8; 20000: past the 16-byte
+# path, staged in LDS; 12296: past the LDS row limit)
+@pytest.mark.parametrize("tokens,dim", [(5, 2048), (3, 1000), (1, 8), (2, 20000), (3, 4096), (2, 3000),
+                                        (2, 8192), (2, 12296)])
 def test_rmsnorm(gpu, orc, tokens, dim):
     lib = gpu
     r = rng(tokens * 7919 + dim)
@@ -60,7 +64,8 @@ def test_rmsnorm(gpu, orc, tokens, dim):
     expect_bits_equal(host(out), expected, f"rmsnorm {tokens}x{dim}")
 
 
-@pytest.mark.parametrize("tokens,dim", [(5, 2048), (4, 999), (2, 20000)])
+@pytest.mark.parametrize("tokens,dim", [(5, 2048), (4, 999), (2, 20000), (3, 4096), (2, 8192), (2, 3000),
+                                        (2, 12296)])
 def test_add_residual_rmsnorm(gpu, orc, tokens, dim):
     lib = gpu
     r = rng(dim)

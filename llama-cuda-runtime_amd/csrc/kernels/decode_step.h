@@ -63,6 +63,7 @@ struct DecodeStepArgs {
   unsigned long long* argmax_partials;  // [lm_head blocks]
   bool paged;
   int splits;
+  int compute_units;         // of the device: sizes the output head's grid
 };
 
 // True when the fused kernels are compiled for this geometry.
@@ -88,6 +89,6 @@ void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
 // leave it out only to time the head alone).
 void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t stream, bool with_argmax = true);
 
-int lm_head_blocks(int vocab);
+int lm_head_blocks(int vocab, int compute_units);
 
 }  // namespace lcr

@@ -350,6 +350,7 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.argmax_partials = argmax_partials_;
   a.paged = options_.kv_layout == KvLayout::kPaged;
   a.splits = splits;
+  a.compute_units = multiprocessors_;
   return a;
 }
 

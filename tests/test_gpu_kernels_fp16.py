@@ -151,3 +151,24 @@ def test_gemm_fp16(gpu, lcr, T, N, K):
     fused = zeros_dev(T * F)
     ok(lib, lib.lcr_gemm_swiglu_ws(p(fused), p(Xd), p(Wd), T, F, K, p(ws), ws_bytes, None), "gemm_swiglu fp16")
     expect_bits_equal(host(fused), host(want), "fp16 gemm+swiglu")
+
+
+def test_small_model_fp16_mfma_prefill(gpu, lcr, tmp_path):
+    """The fp16 build's MFMA prefill (GEMMs, fused SwiGLU, two-pass attention)
+    against the oracle's fp16 chunked prefill: logits within 2e-2 of the
+    largest, and the oracle's first token within that bound of our best logit
+    (this random-init model has near-ties, so the two may pick different
+    tokens of equal score within rounding). The decode path is compared bit
+    for bit elsewhere."""
+    cfg = lcr.llama_config(num_hidden_layers=2, vocab_size=4096)
+    lcr.write_synthetic_checkpoint(tmp_path, cfg, seed=9, fp16=True)
+    prompt = lcr.synthetic_tokens(200, 4096, seed=13)
+    m = lcr.Model(tmp_path, variant="fp16", max_seq=256)
+    got = m.logits(m.prefill(prompt))
+    ref = oracle.OracleModel(tmp_path, kind=FP16, max_seq=256)
+    want = ref.prefill(prompt)
+    bound = 2e-2 * max(1.0, float(np.abs(want).max()))
+    assert float(np.abs(got - want).max()) <= bound
+    assert float(got.max() - got[oracle.argmax(want)]) <= bound
+    m.close()
+    ref.close()

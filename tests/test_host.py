@@ -112,3 +112,21 @@ def test_golden_fixture_is_consistent():
     assert len(g["decode_path"]["logits_sha256"]) == 65
     assert g["decode_path"]["greedy_tokens"][0] == g["decode_path"]["first_top5_ids"][0]
     assert g["chunked_prefill"]["first_argmax"] == g["chunked_prefill"]["greedy_tokens"][0]
+
+
+def test_gemm_split_plans(lcr):
+    """The prefill GEMM's split-K plan (host logic; without a device it plans
+    for 256 compute units): no split once the output tiles fill the device;
+    otherwise a power-of-two number of slices, at most 16, each at least 256
+    of K, with one fp32 partial product of the output per slice."""
+    lib = lcr.load_library("bf16")
+    assert lib.lcr_gemm_workspace_bytes(2048, 16384, 2048) == 0
+    assert lib.lcr_gemm_workspace_bytes(4096, 3072, 2048) == 0
+    assert lib.lcr_gemm_workspace_bytes(0, 2048, 2048) == 0
+    assert lib.lcr_gemm_workspace_bytes(16, 2048, 12) == 0  # K not a multiple of 8
+    for T, N, K in [(512, 2048, 8192), (37, 2048, 8192), (512, 3072, 2048), (128, 2048, 2048)]:
+        b = lib.lcr_gemm_workspace_bytes(T, N, K)
+        assert b > 0, (T, N, K)
+        splits, rem = divmod(b, T * N * 4)
+        assert rem == 0 and splits in (2, 4, 8, 16), (T, N, K, b)
+        assert K // splits >= 256

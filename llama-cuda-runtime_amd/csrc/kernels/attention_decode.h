@@ -47,6 +47,8 @@
 //     L and sum accumulated in split order, out = rne(sum * (1 / L)).
 #pragma once
 
+#include <type_traits>
+
 #include "../kv_cache.h"
 #include "device_common.h"
 
@@ -68,7 +70,12 @@ __host__ __device__ __forceinline__ void softmax_combine(float* m, float* l, flo
   *m = merged;
 }
 
-template <int kHeadDim, int kHeads>
+// Positions whose cache addresses a block of the paged layout keeps in LDS
+// (16 KiB): a split longer than this is walked in windows of that many
+// positions (64 tiles, so every wave keeps its tiles and their order).
+constexpr int kAttnPositionTable = 4096;
+
+template <bool kPaged, int kHeadDim, int kHeads>
 struct AttnShared {
   float probs[kAttnWaves][64 * kHeads];
   float wave_m[kAttnWaves][kHeads];
@@ -76,6 +83,9 @@ struct AttnShared {
   float wave_acc[kAttnWaves][kHeads][kHeadDim];
   float scale[kHeads][kAttnWaves];  // c_w of step 7
   float merged_m[kHeads];           // M of step 7
+  // Paged layout: the 16-byte-chunk index of position begin + i of the
+  // block's range (chunk 0 of that position's key and value rows).
+  uint32_t chunks[kPaged ? kAttnPositionTable : 1];
 };
 
 // Step 3's reduce-scatter: at offset O the lane keeps the half of its N values
@@ -104,17 +114,30 @@ __device__ __forceinline__ float sum_over_groups(float v) {
   return v;
 }
 
+template <bool B>
+using attn_flag = std::integral_constant<bool, B>;
+
 // One block: query heads head0 .. head0 + kHeads - 1 (all reading kv head
 // `kv_head`) over split `split` of `splits` (split < splits). One head per
 // block gives short contexts the most blocks; a whole GQA group per block
 // loads each key/value once for all its heads, which is what long contexts,
 // bound by the cache bytes, need. `q` holds num_heads * kHeadDim elements
 // (head h at h * kHeadDim). Writes out (splits == 1) or partials[head][split].
+//
+// Addressing. A lane's key and value chunks of a position share one 16-byte
+// index (32 bits: a layer view spans at most 64 GiB), computed once per tile
+// for both. In the paged layout the block first stores the index of every
+// position of its range (or of the current window of it) in LDS, one
+// page-table read and division per position, all issued together, so no tile
+// waits on a page-table load: loads return in issue order, and a table load
+// issued after a tile's keys would hold the next tile's requests until those
+// keys were in. Tiles whose 64 positions are all in range skip the masking
+// selects.
 template <bool kPaged, int kHeadDim, int kHeads>
 __device__ __forceinline__ void decode_attention_block(
-    AttnShared<kHeadDim, kHeads>& sh, elem_t* __restrict__ out, float* __restrict__ partials,
-    const elem_t* __restrict__ q, const KvCacheView& view, int kv_head, int head0, int split,
-    int splits, int seq_len, float scale) {
+    AttnShared<kPaged, kHeadDim, kHeads>& sh, elem_t* __restrict__ out,
+    float* __restrict__ partials, const elem_t* __restrict__ q, const KvCacheView& view,
+    int kv_head, int head0, int split, int splits, int seq_len, float scale) {
   constexpr int P = kHeadDim / 8;   // chunks per position
   constexpr int Q = 64 / P;         // positions per load instruction
   constexpr int G = kHeads;
@@ -127,6 +150,15 @@ __device__ __forceinline__ void decode_attention_block(
   const int begin = split * chunk;
   const int end = min(seq_len, begin + chunk);
   const int length = max(0, end - begin);
+  // Positions [begin + window, begin + window + window_len) are addressed
+  // through the table.
+  auto fill_table = [&](int window) {
+    const int window_len = min(kAttnPositionTable, length - window);
+    for (int i = static_cast<int>(threadIdx.x); i < window_len; i += kAttnThreads) {
+      sh.chunks[i] = static_cast<uint32_t>(view.offset<true>(kv_head, begin + window + i) / 8);
+    }
+  };
+  if constexpr (kPaged) fill_table(0);
 
   float qv[G][8];
 #pragma unroll
@@ -145,37 +177,49 @@ __device__ __forceinline__ void decode_attention_block(
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
   }
+  if constexpr (kPaged) __syncthreads();
 
-  // Requests the P chunks this lane holds of tile `tile`. Every load is
-  // issued (positions past the range are clamped to the last valid one), so
-  // each tile is the same fixed number of loads and the wait for a tile never
-  // covers the one requested after it.
-  auto load_tile = [&](int tile, vec16 (&kr)[P], vec16 (&vr)[P]) {
-    const int tile_begin = begin + tile * kAttnTile;
+  // 16-byte index of this lane's chunk of the P positions it holds in tile
+  // `tile` (positions past the range are clamped to the last valid one, so
+  // every tile issues the same loads); `window` is the table's first position.
+  const uint32_t head_chunk = kPaged ? 0u : static_cast<uint32_t>(
+      (static_cast<size_t>(kv_head) * static_cast<size_t>(view.head_stride)) / 8);
+  auto tile_chunks = [&](int tile, int window, uint32_t (&o)[P]) {
+    const int tile_begin = tile * kAttnTile;
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const int pos = min(tile_begin + i * Q + a, end - 1);
-      const size_t off = view.offset<kPaged>(kv_head, pos) + 8 * j;
-      kr[i] = load16(view.keys + off);
-      vr[i] = load16(view.values + off);
+      const int idx = min(tile_begin + i * Q + a, length - 1);
+      uint32_t c;
+      if constexpr (kPaged) {
+        c = sh.chunks[idx - window];
+      } else {
+        c = head_chunk + static_cast<uint32_t>(begin + idx) * P;
+      }
+      o[i] = c + static_cast<uint32_t>(j);
     }
+  };
+  auto load_chunks = [&](const elem_t* base, const uint32_t (&o)[P], vec16 (&r)[P]) {
+#pragma unroll
+    for (int i = 0; i < P; ++i) r[i] = load16(base + 8 * static_cast<size_t>(o[i]));
   };
 
   // Steps 2-4 for one tile: scores, the online softmax update, and the
-  // probabilities into LDS; returns nothing, leaves r[] for step 5.
+  // probabilities into LDS; leaves r[] for step 5.
   float r[G];
-  auto score_tile = [&](int tile, const vec16 (&kr)[P]) {
-    const int count = min(kAttnTile, end - (begin + tile * kAttnTile));
+  auto score_tile = [&](int count, const vec16 (&kr)[P], auto full) {
+    constexpr bool kFull = decltype(full)::value;
     // Step 2: partial dots (positions past the range contribute zeros), value
     // index i * G + g.
     float vals[P * G];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const bool keep = i * Q + a < count;
+      const bool keep = kFull || i * Q + a < count;
       float kf[8];
       unpack8(kr[i], kf);
+      if constexpr (!kFull) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = keep ? kf[e] : 0.0f;
+        for (int e = 0; e < 8; ++e) kf[e] = keep ? kf[e] : 0.0f;
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float d = 0.0f;
@@ -190,7 +234,7 @@ __device__ __forceinline__ void decode_attention_block(
     // Step 4.
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float s = own < count ? vals[g] : kSoftmaxIdentity;
+      const float s = (kFull || own < count) ? vals[g] : kSoftmaxIdentity;
       const float mnew = fmaxf(m[g], wave_max(s));
       r[g] = lcr_expf(m[g] - mnew);
       const float p = lcr_expf(s - mnew);
@@ -204,8 +248,8 @@ __device__ __forceinline__ void decode_attention_block(
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
   // Step 5 for one tile.
-  auto value_tile = [&](int tile, const vec16 (&vr)[P]) {
-    const int count = min(kAttnTile, end - (begin + tile * kAttnTile));
+  auto value_tile = [&](int count, const vec16 (&vr)[P], auto full) {
+    constexpr bool kFull = decltype(full)::value;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
@@ -214,11 +258,13 @@ __device__ __forceinline__ void decode_attention_block(
     const float* pr = &sh.probs[wave][a * P * G];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const bool keep = i * Q + a < count;
+      const bool keep = kFull || i * Q + a < count;
       float vf[8];
       unpack8(vr[i], vf);
+      if constexpr (!kFull) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vf[e] = keep ? vf[e] : 0.0f;
+        for (int e = 0; e < 8; ++e) vf[e] = keep ? vf[e] : 0.0f;
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float pi = pr[i * G + g];
@@ -231,108 +277,143 @@ __device__ __forceinline__ void decode_attention_block(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
-  auto load_keys = [&](int tile, vec16 (&kr)[P]) {
-    const int tile_begin = begin + tile * kAttnTile;
+  // The single-head tile, steps 2-5 in one pass (the same arithmetic as
+  // score_tile + value_tile, in the instruction order that runs fastest for
+  // the latency-bound short-context case).
+  auto process_tile = [&](int count, const vec16 (&kr)[P], const vec16 (&vr)[P], auto full) {
+    constexpr bool kFull = decltype(full)::value;
+    float vals[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const int pos = min(tile_begin + i * Q + a, end - 1);
-      kr[i] = load16(view.keys + view.offset<kPaged>(kv_head, pos) + 8 * j);
+      const bool keep = kFull || i * Q + a < count;
+      float kf[8];
+      unpack8(kr[i], kf);
+      float d = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = __builtin_fmaf(qv[0][e], keep ? kf[e] : 0.0f, d);
+      vals[i] = d;
     }
-  };
-  auto load_values = [&](int tile, vec16 (&vr)[P]) {
-    const int tile_begin = begin + tile * kAttnTile;
+    reduce_scatter<P / 2, P>(vals, lane);
+    const int own = j * Q + a;
+    const float s = (kFull || own < count) ? vals[0] : kSoftmaxIdentity;
+    const float mnew = fmaxf(m[0], wave_max(s));
+    const float rr = lcr_expf(m[0] - mnew);
+    const float p = lcr_expf(s - mnew);
+    l_lane[0] = __builtin_fmaf(l_lane[0], rr, p);
+    m[0] = mnew;
+    sh.probs[wave][lane] = p;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[0][e] = acc[0][e] * rr;
+    const float* pr = &sh.probs[wave][a * P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const int pos = min(tile_begin + i * Q + a, end - 1);
-      vr[i] = load16(view.values + view.offset<kPaged>(kv_head, pos) + 8 * j);
+      const bool keep = kFull || i * Q + a < count;
+      float vf[8];
+      unpack8(vr[i], vf);
+      const float pi = pr[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[0][e] = __builtin_fmaf(pi, keep ? vf[e] : 0.0f, acc[0][e]);
     }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
+  auto tile_count = [&](int tile) { return min(kAttnTile, length - tile * kAttnTile); };
 
-  // Tiles wave, wave + 8, ... . One head per block: two register sets, the
-  // next tile's loads in flight while the current one is processed. A group
-  // per block needs its registers for the heads, so it keeps one set and
-  // refills the keys as soon as the scores are taken and the values as soon
-  // as they are used.
-  if (wave * kAttnTile < length) {
-    if constexpr (G == 1) {
-      // The single-head tile, steps 2-5 in one pass (the same arithmetic as
-      // score_tile + value_tile, in the instruction order that runs fastest
-      // for the latency-bound short-context case).
-      auto process_tile = [&](int tile, const vec16 (&kr)[P], const vec16 (&vr)[P]) {
-        const int count = min(kAttnTile, end - (begin + tile * kAttnTile));
-        float vals[P];
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-          const bool keep = i * Q + a < count;
-          float kf[8];
-          unpack8(kr[i], kf);
-          float d = 0.0f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) d = __builtin_fmaf(qv[0][e], keep ? kf[e] : 0.0f, d);
-          vals[i] = d;
+  // Tiles wave, wave + 8, ... of the window [first_tile, last_tile). One head
+  // per block with head_dim <= 64: two register sets, the next tile's loads in
+  // flight while the current one is processed. A group per block needs its
+  // registers for the heads (and head_dim 128 needs them for its tile), so it
+  // keeps one set and refills the keys as soon as the scores are taken and
+  // the values as soon as they are used.
+  auto run_tiles = [&](int first_tile, int last_tile, int window) {
+    if (first_tile + wave >= last_tile) return;
+    if constexpr (G == 1 && P <= 8) {
+      auto process = [&](int tile, const vec16 (&kr)[P], const vec16 (&vr)[P]) {
+        const int count = tile_count(tile);
+        if (count == kAttnTile) {
+          process_tile(count, kr, vr, attn_flag<true>{});
+        } else {
+          process_tile(count, kr, vr, attn_flag<false>{});
         }
-        reduce_scatter<P / 2, P>(vals, lane);
-        const int own = j * Q + a;
-        const float s = own < count ? vals[0] : kSoftmaxIdentity;
-        const float mnew = fmaxf(m[0], wave_max(s));
-        const float rr = lcr_expf(m[0] - mnew);
-        const float p = lcr_expf(s - mnew);
-        l_lane[0] = __builtin_fmaf(l_lane[0], rr, p);
-        m[0] = mnew;
-        sh.probs[wave][lane] = p;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[0][e] = acc[0][e] * rr;
-        const float* pr = &sh.probs[wave][a * P];
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-          const bool keep = i * Q + a < count;
-          float vf[8];
-          unpack8(vr[i], vf);
-          const float pi = pr[i];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[0][e] = __builtin_fmaf(pi, keep ? vf[e] : 0.0f, acc[0][e]);
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       };
       vec16 ka[P], va[P], kb[P], vb[P];
-      int tile = wave;
-      load_tile(tile, ka, va);
+      uint32_t o[P];
+      int tile = first_tile + wave;
+      tile_chunks(tile, window, o);
+      load_chunks(view.keys, o, ka);
+      load_chunks(view.values, o, va);
       while (true) {
         const int t1 = tile + kAttnWaves;
-        const bool more1 = t1 * kAttnTile < length;
-        if (more1) load_tile(t1, kb, vb);
-        process_tile(tile, ka, va);
+        const bool more1 = t1 < last_tile;
+        if (more1) {
+          tile_chunks(t1, window, o);
+          load_chunks(view.keys, o, kb);
+          load_chunks(view.values, o, vb);
+        }
+        process(tile, ka, va);
         if (!more1) break;
         const int t2 = t1 + kAttnWaves;
-        const bool more2 = t2 * kAttnTile < length;
-        if (more2) load_tile(t2, ka, va);
-        process_tile(t1, kb, vb);
+        const bool more2 = t2 < last_tile;
+        if (more2) {
+          tile_chunks(t2, window, o);
+          load_chunks(view.keys, o, ka);
+          load_chunks(view.values, o, va);
+        }
+        process(t1, kb, vb);
         if (!more2) break;
         tile = t2;
       }
     } else {
       vec16 kr[P], vr[P];
-      int tile = wave;
-      load_keys(tile, kr);
-      load_values(tile, vr);
+      uint32_t o[P];
+      int tile = first_tile + wave;
+      tile_chunks(tile, window, o);
+      load_chunks(view.keys, o, kr);
+      load_chunks(view.values, o, vr);
       while (true) {
         const int next = tile + kAttnWaves;
-        const bool more = next * kAttnTile < length;
-        score_tile(tile, kr);
-        if (more) load_keys(next, kr);
-        value_tile(tile, vr);
+        const bool more = next < last_tile;
+        const int count = tile_count(tile);
+        const bool full = count == kAttnTile;
+        if (full) {
+          score_tile(count, kr, attn_flag<true>{});
+        } else {
+          score_tile(count, kr, attn_flag<false>{});
+        }
+        if (more) {
+          tile_chunks(next, window, o);
+          load_chunks(view.keys, o, kr);
+        }
+        if (full) {
+          value_tile(count, vr, attn_flag<true>{});
+        } else {
+          value_tile(count, vr, attn_flag<false>{});
+        }
         if (!more) break;
-        load_values(next, vr);
+        load_chunks(view.values, o, vr);
         tile = next;
       }
     }
+  };
+  const int tiles = (length + kAttnTile - 1) / kAttnTile;
+  if constexpr (kPaged) {
+    constexpr int kWindowTiles = kAttnPositionTable / kAttnTile;
+    for (int first = 0; first < tiles; first += kWindowTiles) {
+      if (first > 0) {
+        __syncthreads();  // every wave is done with the previous window's table
+        fill_table(first * kAttnTile);
+        __syncthreads();
+      }
+      run_tiles(first, min(tiles, first + kWindowTiles), first * kAttnTile);
+    }
+  } else {
+    run_tiles(0, tiles, 0);
   }
 
   // Step 6.
@@ -400,6 +481,7 @@ __device__ __forceinline__ void decode_attention_block(
 constexpr int kMergeThreads = 256;
 constexpr int kMaxHeadDim = 128;
 constexpr int kMergeLdsFloats = kMaxSplits * (kPartialHeader + kMaxHeadDim) + kMaxSplits;
+static_assert(kMaxSplits <= 64, "the merge takes the maximum over the splits in one wave");
 
 __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
                                                      const float* __restrict__ partials, int head,
@@ -410,14 +492,18 @@ __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
   for (int i = threadIdx.x; i < n; i += blockDim.x) lds[i] = base[i];
   __syncthreads();
   float* c = lds + kMaxSplits * (kPartialHeader + kMaxHeadDim);
-  if (static_cast<int>(threadIdx.x) < splits) {
-    float tm = lds[0];
-    for (int s = 1; s < splits; ++s) tm = fmaxf(tm, lds[s * stride]);
-    c[threadIdx.x] = lcr_expf(lds[threadIdx.x * stride] - tm);
+  if (threadIdx.x < 64) {
+    // The maximum over the splits by one wave (splits <= 64; a maximum does
+    // not depend on the order it is taken in).
+    const int s = threadIdx.x;
+    const float ms = s < splits ? lds[s * stride] : kSoftmaxIdentity;
+    const float tm = wave_max(ms);
+    if (s < splits) c[s] = lcr_expf(ms - tm);
   }
   __syncthreads();
   for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
     float tl = 0.0f, sum = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < splits; ++s) {
       tl = __builtin_fmaf(lds[s * stride + 1], c[s], tl);
       sum = __builtin_fmaf(c[s], lds[s * stride + kPartialHeader + d], sum);

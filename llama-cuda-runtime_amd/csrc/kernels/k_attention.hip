@@ -23,7 +23,7 @@ template <bool kPaged, int kHeadDim, int kGroup>
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
     elem_t* __restrict__ out, float* __restrict__ partials, const elem_t* __restrict__ q,
     KvCacheView view, int seq_len, float scale, int splits) {
-  __shared__ AttnShared<kHeadDim, 1> sh;
+  __shared__ AttnShared<kPaged, kHeadDim, 1> sh;
   decode_attention_block<kPaged, kHeadDim, 1>(sh, out, partials, q, view, blockIdx.x / kGroup,
                                            blockIdx.x, blockIdx.y, splits, seq_len, scale);
 }

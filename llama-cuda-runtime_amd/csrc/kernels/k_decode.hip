@@ -19,6 +19,8 @@ constexpr int kLmHeadMaxBlocks = 1024;
 constexpr int kLmHeadRows = 2;  // rows per wave per group
 constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
 constexpr int kDownWaves = 1;   // waves (rows) per down block
+constexpr int kQkvRowsPerWave = 2;   // rows per qkv wave
+constexpr int kGateUpActsPerWave = 1;  // activations (gate + up row pairs) per gate_up wave
 // Largest GQA group one attention block serves (register budget: the group's
 // q, scores and accumulators next to two key/value tiles per lane).
 constexpr int kMaxGroupedHeads = 4;
@@ -113,28 +115,34 @@ __device__ __forceinline__ void load_resid_chunk(const float* resid, int chunk, 
 // 1. QKV projection + RoPE + KV append
 // ---------------------------------------------------------------------------
 
+// A block serves 2 * kQkvRowsPerWave rotation pairs (i, i + head_dim / 2) of
+// one head: waves 0 and 1 take the first rows of the pairs, waves 2 and 3 the
+// second ones, kQkvRowsPerWave rows each.
 template <int NCH, int HD, bool kPaged>
 __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, LayerDevicePtrs w,
                                                             KvCacheView view, int layer) {
   constexpr int H = NCH * 512;
   constexpr int HALF = HD / 2;
-  constexpr int BLOCKS_PER_HEAD = HALF / 4;
+  constexpr int RW = kQkvRowsPerWave;
+  constexpr int PAIRS = 2 * RW;  // rotation pairs per block
+  constexpr int BLOCKS_PER_HEAD = HALF / PAIRS;
+  static_assert(HALF % PAIRS == 0, "head_dim / 2 must be a multiple of the pairs per block");
   __shared__ __attribute__((aligned(16))) elem_t xs[H];
   __shared__ float scratch[9];
-  __shared__ float rowv[8];
+  __shared__ float rowv[2 * PAIRS];
 
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   const int head = blockIdx.x / BLOCKS_PER_HEAD;
-  const int i0 = (blockIdx.x % BLOCKS_PER_HEAD) * 4;
-  const int r0 = i0 + (wave & 1) * 2 + ((wave >> 1) ? HALF : 0);  // row within the head
+  const int i0 = (blockIdx.x % BLOCKS_PER_HEAD) * PAIRS;
+  const int r0 = i0 + (wave & 1) * RW + ((wave >> 1) ? HALF : 0);  // row within the head
 
   // Everything the prologue and epilogue read is requested before the weight
   // tile, so its latency hides under the stream: the position, the rotation
   // (cos, sin) of this position from the precomputed table, and the norm
   // inputs.
   const int pos = *a.position;
-  const float2 rot = a.rope_table[static_cast<size_t>(pos) * HALF + i0 + (threadIdx.x & 3)];
+  const float2 rot = a.rope_table[static_cast<size_t>(pos) * HALF + i0 + (threadIdx.x % PAIRS)];
   NormInput<NCH> nin;
   if (layer == 0) {
     const elem_t* erow = a.embedding + static_cast<size_t>(*a.token) * H;
@@ -145,10 +153,11 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
                    w.input_norm);
   }
 
-  GemvTile<2, NCH> tile;
+  GemvTile<RW, NCH> tile;
   {
-    const elem_t* rows[2] = {w.qkv + static_cast<size_t>(head * HD + r0) * H,
-                             w.qkv + static_cast<size_t>(head * HD + r0 + 1) * H};
+    const elem_t* rows[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) rows[r] = w.qkv + static_cast<size_t>(head * HD + r0 + r) * H;
     tile.load(rows, lane);
   }
 
@@ -156,19 +165,19 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
 
   vec16 xv[NCH];
   load_x_lds<NCH>(xv, xs, lane);
-  float out[2];
+  float out[RW];
   tile.dot(out, xv);
   if (lane == 0) {
-    rowv[wave * 2 + 0] = elem_to_float(float_to_elem(out[0]));
-    rowv[wave * 2 + 1] = elem_to_float(float_to_elem(out[1]));
+#pragma unroll
+    for (int r = 0; r < RW; ++r) rowv[wave * RW + r] = elem_to_float(float_to_elem(out[r]));
   }
   __syncthreads();
 
-  if (threadIdx.x < 4) {
+  if (static_cast<int>(threadIdx.x) < PAIRS) {
     const int k = threadIdx.x;
     const int i = i0 + k;
     const float lo = rowv[k];
-    const float hi = rowv[4 + k];
+    const float hi = rowv[PAIRS + k];
     if (head < a.num_heads + a.num_kv_heads) {
       const float ra = lo * rot.x - hi * rot.y;
       const float rb = hi * rot.x + lo * rot.y;
@@ -223,7 +232,7 @@ template <bool kPaged, int HD, int G, int kHeads>
 __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStepArgs a,
                                                                       KvCacheView view,
                                                                       float scale) {
-  __shared__ AttnShared<HD, kHeads> sh;
+  __shared__ AttnShared<kPaged, HD, kHeads> sh;
   const int seq_len = *a.position + 1;
   const int splits = min(a.splits, seq_len);
   int unit, g = 0;
@@ -292,24 +301,33 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(DecodeStepArgs a, Lay
   constexpr int H = NCH * 512;
   __shared__ __attribute__((aligned(16))) elem_t xs[H];
   __shared__ float scratch[9];
+  constexpr int A = kGateUpActsPerWave;
   const int lane = lane_id();
-  const int i = blockIdx.x * kWaves + (threadIdx.x >> 6);  // activation index of this wave
+  // First activation index of this wave.
+  const int i = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * A;
   NormInput<NCH> nin;
   norm_load<NCH>(nin, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
                  w.post_norm);
-  GemvTile<2, NCH> tile;
-  const elem_t* rows[2] = {w.gate_up + static_cast<size_t>(i) * H,
-                           w.gate_up + static_cast<size_t>(a.ffn + i) * H};
+  GemvTile<2 * A, NCH> tile;
+  const elem_t* rows[2 * A];
+#pragma unroll
+  for (int k = 0; k < A; ++k) {
+    rows[2 * k] = w.gate_up + static_cast<size_t>(i + k) * H;
+    rows[2 * k + 1] = w.gate_up + static_cast<size_t>(a.ffn + i + k) * H;
+  }
   tile.load(rows, lane);
   norm_finish<NCH>(xs, nin, a.eps, scratch, nullptr);
   vec16 xv[NCH];
   load_x_lds<NCH>(xv, xs, lane);
-  float out[2];
+  float out[2 * A];
   tile.dot(out, xv);
   if (lane == 0) {
-    const float g = elem_to_float(float_to_elem(out[0]));
-    const float u = elem_to_float(float_to_elem(out[1]));
-    a.act[i] = float_to_elem(silu(g) * u);
+#pragma unroll
+    for (int k = 0; k < A; ++k) {
+      const float g = elem_to_float(float_to_elem(out[2 * k]));
+      const float u = elem_to_float(float_to_elem(out[2 * k + 1]));
+      a.act[i + k] = float_to_elem(silu(g) * u);
+    }
   }
 }
 
@@ -409,7 +427,7 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
                          int layer, hipStream_t s, unsigned mask) {
   if (mask & kDecodeQkv) {
     const int qkv_rows = (a.num_heads + 2 * a.num_kv_heads) * HD;
-    qkv_rope_kernel<NCH, HD, kPaged><<<qkv_rows / 8, kThreads, 0, s>>>(a, w, view, layer);
+    qkv_rope_kernel<NCH, HD, kPaged><<<qkv_rows / (4 * kQkvRowsPerWave), kThreads, 0, s>>>(a, w, view, layer);
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeAttention) {
@@ -432,7 +450,7 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeGateUp) {
-    gate_up_kernel<NCH><<<a.ffn / kWaves, kThreads, 0, s>>>(a, w);
+    gate_up_kernel<NCH><<<a.ffn / (kWaves * kGateUpActsPerWave), kThreads, 0, s>>>(a, w);
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeDown) {

@@ -21,19 +21,23 @@ constexpr int kNormThreads = 256;
 
 // Adds the per-thread partial sums of a 256-thread block in the fixed tree.
 // Every thread must call it; every thread gets the total. `scratch` holds at
-// least 9 floats of LDS.
-__device__ __forceinline__ float block_norm_total(float s, float* scratch) {
+// least 8 floats of LDS. The second butterfly runs over the 8 group totals
+// p0..p7 with zeros in lanes 8..31, where offsets 16 and 8 add nothing, so
+// every thread evaluates its offsets 4, 2, 1 directly:
+// ((p0 + p4) + (p2 + p6)) + ((p1 + p5) + (p3 + p7)).
+// This form leaves `scratch` in use: the caller passes a barrier before it
+// writes `scratch` again.
+__device__ __forceinline__ float block_norm_total_once(float s, float* scratch) {
   const int t = static_cast<int>(threadIdx.x);
   s = half_wave_sum(s);
   if ((t & 31) == 0) scratch[t >> 5] = s;
   __syncthreads();
-  if (t < 32) {
-    float v = (t < 8) ? scratch[t] : 0.0f;
-    v = half_wave_sum(v);
-    if (t == 0) scratch[8] = v;
-  }
-  __syncthreads();
-  const float total = scratch[8];
+  return ((scratch[0] + scratch[4]) + (scratch[2] + scratch[6])) +
+         ((scratch[1] + scratch[5]) + (scratch[3] + scratch[7]));
+}
+
+__device__ __forceinline__ float block_norm_total(float s, float* scratch) {
+  const float total = block_norm_total_once(s, scratch);
   __syncthreads();
   return total;
 }

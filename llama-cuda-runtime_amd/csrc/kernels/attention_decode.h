@@ -325,21 +325,29 @@ __device__ __forceinline__ void decode_attention_block(
   };
   auto tile_count = [&](int tile) { return min(kAttnTile, length - tile * kAttnTile); };
 
-  // Tiles wave, wave + 8, ... of the window [first_tile, last_tile). One head
-  // per block with head_dim <= 64: two register sets, the next tile's loads in
-  // flight while the current one is processed. A group per block needs its
-  // registers for the heads (and head_dim 128 needs them for its tile), so it
-  // keeps one set and refills the keys as soon as the scores are taken and
-  // the values as soon as they are used.
+  // Tiles wave, wave + 8, ... of the window [first_tile, last_tile). Up to
+  // two heads per block with head_dim <= 64: two register sets, the next
+  // tile's loads in flight while the current one is processed. Four heads
+  // per block need their registers for the heads (and head_dim 128 needs
+  // them for its tile), so they keep one set and refill the keys as soon as
+  // the scores are taken and the values as soon as they are used.
   auto run_tiles = [&](int first_tile, int last_tile, int window) {
     if (first_tile + wave >= last_tile) return;
-    if constexpr (G == 1 && P <= 8) {
+    if constexpr (G <= 2 && P <= 8) {
       auto process = [&](int tile, const vec16 (&kr)[P], const vec16 (&vr)[P]) {
         const int count = tile_count(tile);
-        if (count == kAttnTile) {
-          process_tile(count, kr, vr, attn_flag<true>{});
+        if constexpr (G == 1) {
+          if (count == kAttnTile) {
+            process_tile(count, kr, vr, attn_flag<true>{});
+          } else {
+            process_tile(count, kr, vr, attn_flag<false>{});
+          }
+        } else if (count == kAttnTile) {
+          score_tile(count, kr, attn_flag<true>{});
+          value_tile(count, vr, attn_flag<true>{});
         } else {
-          process_tile(count, kr, vr, attn_flag<false>{});
+          score_tile(count, kr, attn_flag<false>{});
+          value_tile(count, vr, attn_flag<false>{});
         }
       };
       vec16 ka[P], va[P], kb[P], vb[P];

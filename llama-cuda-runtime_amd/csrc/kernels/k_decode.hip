@@ -21,11 +21,15 @@ constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
 constexpr int kDownWaves = 1;   // waves (rows) per down block
 constexpr int kQkvRowsPerWave = 2;   // rows per qkv wave
 constexpr int kGateUpActsPerWave = 1;  // activations (gate + up row pairs) per gate_up wave
-// Largest GQA group one attention block serves (register budget: the group's
-// q, scores and accumulators next to two key/value tiles per lane).
-constexpr int kMaxGroupedHeads = 4;
+// Query heads per block in the long-context attention launch (with fewer
+// than G, the heads of one kv head are spread over G / kLongContextHeads
+// blocks on one XCD, which share its keys and values in L2). The whole group
+// of four measured fastest at 32768 positions: 27.0 us at 32 splits, against
+// 28.3 us for two heads per block at their best count (16 splits), although
+// two heads leave the registers for two key/value tiles in flight per wave.
+constexpr int kLongContextHeads = 4;
 // From this many splits on (the model's policy gives them to contexts of 16384
-// and more) attention runs one block per (kv head, split) for the whole group.
+// and more) attention runs kLongContextHeads query heads per block.
 constexpr int kGroupedMinSplits = 16;
 
 __device__ __forceinline__ float silu(float v) { return lcr_silu(v); }
@@ -199,16 +203,17 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
 }
 
 // ---------------------------------------------------------------------------
-// 2. Attention (split-K; the last block of a kv head merges the splits)
+// 2. Attention (split-K; a second kernel merges the splits)
 // ---------------------------------------------------------------------------
 
-// One block per (query head, split): four times the blocks of a per-kv-head
-// grid, each with a quarter of the arithmetic, which is what a short context
-// needs (the kernel is latency-bound there). The blocks of one (kv head, split)
-// are numbered so they land on the same XCD (consecutive block ids go round
-// robin over the 8 XCDs), where they share the key/value lines in that XCD's
-// L2. The results equal the per-kv-head grid's bit for bit: no arithmetic
-// mixes heads.
+// Block b of a grid with `group` blocks per (kv head, split) unit: up to 16K
+// positions one block per (query head, split), four times the blocks of a
+// per-kv-head grid with a quarter of the arithmetic each, which is what the
+// latency-bound shorter contexts need; beyond, one block per pair of query
+// heads. The blocks of one unit are numbered so they land on the same XCD
+// (consecutive block ids go round robin over the 8 XCDs), where they share
+// the key/value lines in that XCD's L2. The results equal a per-kv-head
+// grid's bit for bit: no arithmetic mixes heads.
 __device__ __forceinline__ void attention_block_coords(int b, int units, int group, int* unit,
                                                        int* g) {
   constexpr int kXcds = 8;
@@ -226,19 +231,19 @@ __device__ __forceinline__ void attention_block_coords(int b, int units, int gro
   }
 }
 
-// kHeads = 1: one block per (query head, split), numbered so the blocks of a
-// kv head share an XCD. kHeads = G: one block per (kv head, split) for the
-// whole group.
+// kHeads query heads per block (1 or kLongContextHeads), G / kHeads blocks
+// per (kv head, split), numbered so the blocks of a kv head share an XCD.
 template <bool kPaged, int HD, int G, int kHeads>
 __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStepArgs a,
                                                                       KvCacheView view,
                                                                       float scale) {
   __shared__ AttnShared<kPaged, HD, kHeads> sh;
+  constexpr int kBlocksPerGroup = G / kHeads;
   const int seq_len = *a.position + 1;
   const int splits = min(a.splits, seq_len);
   int unit, g = 0;
-  if (kHeads == 1) {
-    attention_block_coords(blockIdx.x, a.num_kv_heads * a.splits, G, &unit, &g);
+  if (kBlocksPerGroup > 1) {
+    attention_block_coords(blockIdx.x, a.num_kv_heads * a.splits, kBlocksPerGroup, &unit, &g);
   } else {
     unit = blockIdx.x;
   }
@@ -248,7 +253,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStep
   // blocks have no range and must not touch the partials of other heads.
   if (split >= splits) return;
   decode_attention_block<kPaged, HD, kHeads>(sh, a.attn, a.partials, a.q, view, kv_head,
-                                             kv_head * G + g, split, splits, seq_len, scale);
+                                             kv_head * G + g * kHeads, split, splits, seq_len, scale);
 }
 
 // Split merge (splits > 1 only), one kMergeThreads-thread block per query head.
@@ -440,9 +445,10 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
   }
   if (mask & kDecodeAttention) {
     const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
-    if (a.splits >= kGroupedMinSplits && G <= kMaxGroupedHeads) {
-      attention_step_kernel<kPaged, HD, G, (G <= kMaxGroupedHeads ? G : 1)>
-          <<<a.num_kv_heads * a.splits, kAttnThreads, 0, s>>>(a, view, scale);
+    constexpr int kHeads = G <= kLongContextHeads ? G : (G % kLongContextHeads == 0 ? kLongContextHeads : 1);
+    if (a.splits >= kGroupedMinSplits && kHeads > 1) {
+      attention_step_kernel<kPaged, HD, G, kHeads>
+          <<<a.num_kv_heads * a.splits * (G / kHeads), kAttnThreads, 0, s>>>(a, view, scale);
     } else {
       attention_step_kernel<kPaged, HD, G, 1>
           <<<a.num_kv_heads * a.splits * G, kAttnThreads, 0, s>>>(a, view, scale);

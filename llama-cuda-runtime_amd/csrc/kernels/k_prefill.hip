@@ -368,11 +368,18 @@ __device__ __forceinline__ void wait_stage_landed() {
   __builtin_amdgcn_s_waitcnt((kCount & 15) | ((kCount >> 4) << 14) | (7 << 4));
 }
 
-template <int kStages, bool kFp32Out>
-__global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, const elem_t* __restrict__ X,
-                                                        const elem_t* __restrict__ W, int T, int N, int K,
-                                                        GemmGrid grid) {
-  constexpr int FW = 8, FT = 4;  // wave tile 128 W rows x 64 tokens
+// kWaves = 8: wave tiles of 128 W rows x 64 tokens (two waves per SIMD).
+// kWaves = 4: wave tiles of 128 x 128 (one wave per SIMD, its 256 fp32
+// accumulators in the accumulation registers), so a stage's products read
+// 64 KB of fragments from LDS instead of 96 KB.
+template <int kStages, int kWaves, bool kFp32Out>
+__global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict__ Y, const elem_t* __restrict__ X,
+                                                                const elem_t* __restrict__ W, int T, int N, int K,
+                                                                GemmGrid grid) {
+  static_assert(kWaves == 4 || kWaves == 8, "4 or 8 waves per block");
+  constexpr int FW = 8;                      // W fragments of 16 rows per wave
+  constexpr int FT = kWaves == 8 ? 4 : 8;    // token fragments of 16 tokens per wave
+  constexpr int kLoads = 32 / kWaves;        // 1 KB loads per wave per stage
   __shared__ __attribute__((aligned(1024))) elem_t ring[kStages * kRingStage];
 
   GemmWork work;
@@ -383,15 +390,15 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int ww = (wave >> 2) * 128;
-  const int wt = (wave & 3) * 64;
+  const int ww = (kWaves == 8 ? (wave >> 2) : (wave >> 1)) * 128;
+  const int wt = (kWaves == 8 ? (wave & 3) : (wave & 1)) * (16 * FT);
 
-  // Load i (0..3) of a wave fills 1 KB block 8i + wave of the stage: rows
+  // Load i of a wave fills 1 KB block kWaves * i + wave of the stage: rows
   // 16 block .. +15, four lanes per row.
-  const elem_t* src[4];
+  const elem_t* src[kLoads];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * (8 * i + wave) + (lane >> 2);
+  for (int i = 0; i < kLoads; ++i) {
+    const int row = 16 * (kWaves * i + wave) + (lane >> 2);
     const int chunk = (lane & 3) ^ ((row >> 1) & 3);
     src[i] = (row < 256 ? W + static_cast<size_t>(weight_row(min(w0 + row, N - 1), grid.ffn)) * K
                         : X + static_cast<size_t>(min(t0 + row - 256, T - 1)) * K) + work.k_first + 8 * chunk;
@@ -400,7 +407,9 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
   auto issue = [&](int s) {
     const uint32_t base = ring_base + static_cast<uint32_t>((s % kStages) * kRingStage * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) load_to_lds16(src[i] + s * kRingK, base + static_cast<uint32_t>(i * 8 * 16 * kRingK * 2));
+    for (int i = 0; i < kLoads; ++i) {
+      load_to_lds16(src[i] + s * kRingK, base + static_cast<uint32_t>(i * kWaves * 16 * kRingK * 2));
+    }
   };
 
   mfma_acc4 acc[FW][FT];
@@ -414,9 +423,9 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
   // The next stage's fragments are read during the current stage's products,
   // so LDS reads overlap matrix work: its token fragments into the second of
   // two sets, and each W fragment into the registers of the current one as
-  // soon as that one's four products are issued. After the barrier that
-  // precedes reading stage s + 1, every wave's reads of stage s have
-  // returned, and stage s's buffer takes stage s + kStages.
+  // soon as that one's products are issued. After the barrier that precedes
+  // reading stage s + 1, every wave's reads of stage s have returned, and
+  // stage s's buffer takes stage s + kStages.
   mfma_in8 aw[FW], bt_a[FT], bt_b[FT];
   auto read_tokens = [&](int s, mfma_in8 (&bt)[FT]) {
     const elem_t* base = ring + (s % kStages) * kRingStage;
@@ -449,7 +458,7 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
   // reads have returned; then the block meets and the freed buffer is refilled.
   auto advance = [&](int next) {
     if (next + kStages - 2 < stages) {
-      wait_stage_landed<4 * (kStages - 2)>();
+      wait_stage_landed<kLoads * (kStages - 2)>();
     } else {
       wait_stage_landed<0>();
     }
@@ -476,6 +485,10 @@ __global__ __launch_bounds__(512) void gemm_ring_kernel(void* __restrict__ Y, co
 }
 
 constexpr int kRingStages = 4;
+// Waves per ring block. Eight (two per SIMD) measured faster than four with
+// 128 x 128 wave tiles: 143 against 176 us for T = 2048, N = 16384, K = 2048;
+// one wave per SIMD leaves the LDS and barrier latencies uncovered.
+constexpr int kRingWaves = 8;
 
 // act[t][f] = SwiGLU of the summed gate and up partial products (logical
 // columns 32 (f / 16) + f % 16 and that + 16), for gated split launches.
@@ -610,9 +623,9 @@ void launch_gemm_ring(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, 
   const int units = grid.tiles_t * grid.tiles_w * grid.splits;
   const unsigned blocks = static_cast<unsigned>(((units + 7) / 8) * 8);
   if (fp32_out) {
-    gemm_ring_kernel<kRingStages, true><<<blocks, 512, 0, s>>>(Y, X, W, T, N, K, grid);
+    gemm_ring_kernel<kRingStages, kRingWaves, true><<<blocks, 64 * kRingWaves, 0, s>>>(Y, X, W, T, N, K, grid);
   } else {
-    gemm_ring_kernel<kRingStages, false><<<blocks, 512, 0, s>>>(Y, X, W, T, N, K, grid);
+    gemm_ring_kernel<kRingStages, kRingWaves, false><<<blocks, 64 * kRingWaves, 0, s>>>(Y, X, W, T, N, K, grid);
   }
 }
 

@@ -152,10 +152,27 @@ __device__ __forceinline__ void decode_attention_block(
   const int length = max(0, end - begin);
   // Positions [begin + window, begin + window + window_len) are addressed
   // through the table.
+  // One thread per page of the window: a single page-table read, then the
+  // index of each of the page's positions in the window.
   auto fill_table = [&](int window) {
     const int window_len = min(kAttnPositionTable, length - window);
-    for (int i = static_cast<int>(threadIdx.x); i < window_len; i += kAttnThreads) {
-      sh.chunks[i] = static_cast<uint32_t>(view.offset<true>(kv_head, begin + window + i) / 8);
+    if (window_len <= 0) return;  // an empty split reads no page-table entry
+    const int first = begin + window;                      // first position of the window
+    const int first_page = first / view.page_size;
+    const int pages = (first + window_len - 1) / view.page_size - first_page + 1;
+    const uint32_t head_chunk8 = static_cast<uint32_t>(
+        (static_cast<size_t>(kv_head) * static_cast<size_t>(view.head_stride)) / 8);
+    for (int pi = static_cast<int>(threadIdx.x); pi < pages; pi += kAttnThreads) {
+      const int page = first_page + pi;
+      const uint32_t base = static_cast<uint32_t>(
+          (static_cast<size_t>(view.page_table[page]) * static_cast<size_t>(view.page_stride)) / 8) +
+          head_chunk8;
+      const int lo = max(page * view.page_size, first);
+      const int hi = min((page + 1) * view.page_size, first + window_len);
+      for (int pos = lo; pos < hi; ++pos) {
+        sh.chunks[pos - first] =
+            base + static_cast<uint32_t>(pos - page * view.page_size) * static_cast<uint32_t>(P);
+      }
     }
   };
   if constexpr (kPaged) fill_table(0);
@@ -404,6 +421,9 @@ __device__ __forceinline__ void decode_attention_block(
           value_tile(count, vr, attn_flag<false>{});
         }
         if (!more) break;
+        // head_dim 128 recomputes the indices rather than keeping 16 of them
+        // live across the value products
+        if constexpr (P > 8) tile_chunks(next, window, o);
         load_chunks(view.values, o, vr);
         tile = next;
       }
@@ -482,7 +502,7 @@ __device__ __forceinline__ void decode_attention_block(
 }
 
 // Merge of the split partials of one query head (step 8), by a block of
-// kMergeThreads threads. The partials are first copied into LDS with every
+// exactly kMergeThreads threads. The partials are first copied into LDS with every
 // thread loading (they come from other XCDs' writes, so each load is a trip to
 // the memory side; issued together they cost one such trip, not one per
 // split), then folded from LDS in split order.
@@ -497,7 +517,20 @@ __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
   const int stride = kPartialHeader + head_dim;
   const float* base = partials + static_cast<size_t>(head) * splits * stride;
   const int n = splits * stride;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) lds[i] = base[i];
+  // Every load is issued before the first LDS store: a loop of load-then-
+  // store would wait out one memory round trip per iteration.
+  constexpr int kPer = (kMaxSplits * (kPartialHeader + kMaxHeadDim) + kMergeThreads - 1) / kMergeThreads;
+  float staged[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = static_cast<int>(threadIdx.x) + k * kMergeThreads;
+    staged[k] = i < n ? base[i] : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = static_cast<int>(threadIdx.x) + k * kMergeThreads;
+    if (i < n) lds[i] = staged[k];
+  }
   __syncthreads();
   float* c = lds + kMaxSplits * (kPartialHeader + kMaxHeadDim);
   if (threadIdx.x < 64) {

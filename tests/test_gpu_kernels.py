@@ -216,6 +216,20 @@ ATTENTION_CASES = [
 
 @pytest.mark.parametrize("heads,kv,hd,positions,splits,paged", ATTENTION_CASES)
 def test_decode_attention(gpu, lcr, orc, heads, kv, hd, positions, splits, paged):
+    check_decode_attention(gpu, lcr, orc, heads, kv, hd, positions, splits, paged, 16)
+
+
+# The paged kernel keeps each position's cache address in LDS, for at most
+# 4096 positions at a time: one split longer than that is walked in windows
+# (9000 positions: 4096 + 4096 + 808; 4097: a window of one position). Page
+# sizes other than 16 cut pages across tiles and windows differently.
+@pytest.mark.parametrize("positions,splits,page_size", [
+    (9000, 1, 16), (4097, 1, 16), (8192, 1, 16), (1000, 3, 1), (1000, 3, 7), (3000, 2, 64)])
+def test_decode_attention_page_windows(gpu, lcr, orc, positions, splits, page_size):
+    check_decode_attention(gpu, lcr, orc, 32, 8, 64, positions, splits, True, page_size)
+
+
+def check_decode_attention(gpu, lcr, orc, heads, kv, hd, positions, splits, paged, page_size):
     lib = gpu
     r = rng(positions * 31 + splits)
     kv_dim = kv * hd
@@ -225,9 +239,9 @@ def test_decode_attention(gpu, lcr, orc, heads, kv, hd, positions, splits, paged
     table = None
     if paged:
         # a shuffled block table, as the long-context configuration uses
-        pages = -(-(positions + 8) // 16)
+        pages = -(-(positions + 8) // page_size)
         table = r.permutation(pages).astype(np.int32)
-    cache = Cache(kv, hd, positions + 8, paged, 16, table)
+    cache = Cache(kv, hd, positions + 8, paged, page_size, table)
     fill_cache(lib, lcr, cache, keys, values, positions)
     # The identity rotation must have landed every vector bit-exactly.
     hv = cache.host_view()

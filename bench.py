@@ -61,14 +61,14 @@ def load_package():
     return mod
 
 
-def checkpoint_dir(lcr, config, seed) -> Path:
+def checkpoint_dir(lcr, config, seed, fp16: bool = False) -> Path:
     base = Path(os.environ.get("LCR_SYNTH_DIR", tempfile.gettempdir()))
-    d = base / f"lcr_synth_llama32_1b_bf16_{seed}"
+    d = base / f"lcr_synth_llama32_1b_{'fp16' if fp16 else 'bf16'}_{seed}"
     st = d / "model.safetensors"
     stamp = d / "STAMP"
-    want = json.dumps({"config": config, "seed": seed})
+    want = json.dumps({"config": config, "seed": seed, "fp16": fp16})
     if not (st.exists() and stamp.exists() and stamp.read_text() == want):
-        lcr.write_synthetic_checkpoint(d, config, seed=seed)
+        lcr.write_synthetic_checkpoint(d, config, seed=seed, fp16=fp16)
         stamp.write_text(want)
     return d
 
@@ -175,6 +175,52 @@ def prefill_run(lcr, model_dir: Path, config: dict, T: int) -> dict:
             "mfma_frac": tflops / BF16_DENSE_PEAK_TFLOPS}
 
 
+SAMPLING_T, SAMPLING_TOP_K, SAMPLING_TOP_P = 0.8, 40, 0.95
+SAMPLING_UNIFORM_SEED = 20260904
+
+
+def sampling_run(lcr, config: dict, prompt_len: int = 512, steps: int = 256) -> dict:
+    """the fp16 build, a paged cache of 16-token
+    pages, a seeded 512-token prompt (MFMA prefill), then `steps` tokens
+    sampled at temperature 0.8, top-k 40, top-p 0.95 with one Philox uniform
+    per token, through the reference's host loop of decode() + sample() per
+    token (src/main.cu:442-466). Timed on the host clock, with the per-token
+    device-to-host copy of the sampled id inside; one untimed pass first."""
+    cfg16 = lcr.llama_config(torch_dtype="float16")
+    d = checkpoint_dir(lcr, cfg16, lcr.WEIGHT_SEED, fp16=True)
+    prompt = lcr.synthetic_tokens(prompt_len, config["vocab_size"], seed=lcr.PROMPT_SEED, variant="fp16")
+    uniforms = lcr.philox_uniforms(SAMPLING_UNIFORM_SEED, steps)
+    m = lcr.Model(d, variant="fp16", max_seq=prompt_len + steps + 1, paged=1, page_size=16)
+
+    def run():
+        ptr = m.prefill(prompt)
+        prefill_ms = m.stats().last_prefill_ms
+        ids = []
+        lcr.synchronize("fp16")
+        t0 = time.perf_counter()
+        for step in range(steps):
+            tok = m.sample(ptr, SAMPLING_T, SAMPLING_TOP_K, SAMPLING_TOP_P, uniforms[step])
+            ids.append(tok)
+            if step + 1 < steps:
+                ptr = m.decode(tok)
+        seconds = time.perf_counter() - t0
+        return ids, seconds, prefill_ms
+
+    run()
+    m.reset()
+    ids, seconds, prefill_ms = run()
+    st = m.stats()
+    m.close()
+    mean_len = prompt_len + steps / 2.0
+    bytes_per_token = st.weight_bytes_per_token + mean_len * st.kv_bytes_per_position
+    ms = seconds * 1000.0 / steps
+    return {"prompt_tokens": prompt_len, "sampled_tokens": steps, "temperature": SAMPLING_T,
+            "top_k": SAMPLING_TOP_K, "top_p": SAMPLING_TOP_P, "prefill_ms": prefill_ms,
+            "ms_per_token": ms, "tok_s": 1000.0 / ms,
+            "token_gbs": bytes_per_token / (ms / 1000.0) / 1e9,
+            "distinct_ids": len(set(ids)), "first_ids": [int(x) for x in ids[:8]]}
+
+
 def counters_run(lcr, model_dir: Path, prompt, max_seq: int) -> int:
     """Eager work for a rocprofv3 --pmc pass: every fused decode kernel is a
     separate dispatch, plus a 256 MiB device-to-device copy whose counter
@@ -204,11 +250,13 @@ def main() -> int:
     ap.add_argument("--kernel-launches", type=int, default=64)
     ap.add_argument("--cpu-steps", type=int, default=256)
     ap.add_argument("--counters", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the config 3 / config 4 measurements")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config 3 / 4 / 5 measurements")
     ap.add_argument("--prefill", type=int, default=0, metavar="T",
                     help="only run the config 4 prefill of T tokens and print its JSON (for profiling)")
     ap.add_argument("--long-context", type=int, default=0, metavar="CTX",
                     help="only run the config 3 decode at context CTX and print its JSON (for profiling)")
+    ap.add_argument("--sampling", action="store_true",
+                    help="only run the config 5 fp16 stochastic-sampling loop and print its JSON")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -235,6 +283,9 @@ def main() -> int:
         return 0
     if args.long_context > 0:
         print(json.dumps({"long_context": long_context(lcr, model_dir, config, args.long_context)}))
+        return 0
+    if args.sampling:
+        print(json.dumps({"sampling_config5": sampling_run(lcr, config)}))
         return 0
     t0 = time.perf_counter()
     model = lcr.Model(model_dir, max_seq=args.max_seq)
@@ -290,6 +341,7 @@ def main() -> int:
     if not args.no_extra:
         extra["long_context"] = [long_context(lcr, model_dir, config, ctx) for ctx in (8192, 32768)]
         extra["prefill_config4"] = [prefill_run(lcr, model_dir, config, t) for t in (512, 2048)]
+        extra["sampling_config5"] = sampling_run(lcr, config)
 
     cpu = None
     if not args.no_cpu_baseline:

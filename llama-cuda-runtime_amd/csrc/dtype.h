@@ -49,12 +49,20 @@ __host__ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
-// fp16 conversions are written with integer operations, as the bf16 ones
-// are. With the hardware conversions the compiler merges a multiply and the
-// following f32 -> f16 rounding into one mixed-precision fma with a +0 addend,
-// which turns a -0 product into +0; here every product is rounded to f32 first
-// and the conversion cannot be merged, so device, host and oracle agree.
+// The f32 -> f16 rounding is written with integer operations, as the bf16
+// one is. With the hardware conversion the compiler merges a multiply and the
+// following rounding into one mixed-precision fma with a +0 addend, which
+// turns a -0 product into +0; here every product is rounded to f32 first and
+// the conversion cannot be merged, so device, host and oracle agree.
+// Widening f16 -> f32 is exact, so device code uses the hardware conversion
+// (which the compiler may merge into a mixed-precision fma, also exact): the
+// same value as the integer form below for every input but a signalling NaN,
+// which the hardware returns quieted. Every fp16 weight of a decode step is
+// widened once, so this is the fp16 GEMVs' inner loop.
 __host__ __device__ __forceinline__ float half_bits_to_float(uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b & 0xffffu)));
+#endif
   const uint32_t sign = (b & 0x8000u) << 16;
   const uint32_t exp = (b >> 10) & 0x1fu;
   const uint32_t man = b & 0x3ffu;

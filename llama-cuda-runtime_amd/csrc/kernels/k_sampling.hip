@@ -50,6 +50,17 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
   return va > vb || (va == vb && ia < ib);
 }
 
+// Loads per thread in flight in the passes over the logits (element i of a
+// batch is base + i * kSampleThreads, so each thread keeps its order).
+constexpr int kSampleBatch = 8;
+constexpr int kSampleWaves = kSampleThreads / 64;
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restrict__ out_id,
                                                                 const float* __restrict__ logits,
                                                                 int vocab, float inv_temperature,
@@ -58,15 +69,26 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
   __shared__ float lds32[32];
   __shared__ unsigned long long lds_u64[16];
   __shared__ int histogram[kHistogramBins];
-  __shared__ int counts[kSampleThreads];
+  __shared__ int wave_counts[kSampleWaves];
   __shared__ int shared_cutoff;
   __shared__ float values[kMaxCandidates];
   __shared__ int indices[kMaxCandidates];
   const int t = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = t >> 6;
 
   // 1. Maximum logit (exact in any order).
   float local_max = -FLT_MAX;
-  for (int i = t; i < vocab; i += kSampleThreads) local_max = fmaxf(local_max, logits[i]);
+  for (int base = t; base < vocab; base += kSampleBatch * kSampleThreads) {
+    float v[kSampleBatch];
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) {
+      const int i = base + k * kSampleThreads;
+      v[k] = i < vocab ? logits[i] : -FLT_MAX;
+    }
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) local_max = fmaxf(local_max, v[k]);
+  }
   {
     // Reuse the u64 block max on the order key of the float (ties irrelevant).
     unsigned long long key = static_cast<unsigned long long>(order_key(local_max)) << 32;
@@ -76,65 +98,122 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
   }
   const float max_logit = local_max;
 
-  // 2. Exponential sum over the whole vocabulary, and the histogram.
+  // 2. Exponential sum over the whole vocabulary, and the histogram. Most
+  // logits fall in the last (clamped) bin: that bin is counted in registers
+  // and added once per wave, the others with LDS atomics.
   for (int b = t; b < kHistogramBins; b += kSampleThreads) histogram[b] = 0;
   __syncthreads();
   float local_sum = 0.0f;
-  for (int i = t; i < vocab; i += kSampleThreads) {
-    const float scaled = (logits[i] - max_logit) * inv_temperature;
-    local_sum += lcr_expf(scaled);
-    const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
-    if (bin >= 0) atomicAdd(&histogram[bin], 1);
-  }
-  const float total_sum = block_sum_1024(local_sum, lds32);
-
-  // 3. Cutoff bin.
-  if (t == 0) {
-    int running = 0;
-    int cutoff = 0;
-    for (int b = 0; b < kHistogramBins; ++b) {
-      if (running + histogram[b] > kMaxCandidates) break;
-      running += histogram[b];
-      cutoff = b + 1;
+  int last_bin = 0;
+  for (int base = t; base < vocab; base += kSampleBatch * kSampleThreads) {
+    float v[kSampleBatch];
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) {
+      const int i = base + k * kSampleThreads;
+      v[k] = i < vocab ? logits[i] : 0.0f;
     }
-    shared_cutoff = max(cutoff, 1);
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) {
+      if (base + k * kSampleThreads < vocab) {
+        const float scaled = (v[k] - max_logit) * inv_temperature;
+        local_sum += lcr_expf(scaled);
+        const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
+        if (bin == kHistogramBins - 1) {
+          ++last_bin;
+        } else if (bin >= 0) {
+          atomicAdd(&histogram[bin], 1);
+        }
+      }
+    }
+  }
+  last_bin = wave_sum_int(last_bin);
+  if (lane == 0) atomicAdd(&histogram[kHistogramBins - 1], last_bin);
+  const float total_sum = block_sum_1024(local_sum, lds32);  // its barriers order the atomics
+
+  // 3. Cutoff bin: the number of leading bins whose running count stays
+  // <= kMaxCandidates (at least 1). Wave 0, four bins per lane, in bin order.
+  if (wave == 0) {
+    static_assert(kHistogramBins == 4 * 64, "four bins per lane");
+    int c[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c[k] = histogram[4 * lane + k];
+    const int mine = c[0] + c[1] + c[2] + c[3];
+    int before = mine;  // inclusive scan of the lane totals
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int other = __shfl_up(before, o, 64);
+      if (lane >= o) before += other;
+    }
+    before -= mine;
+    int fits = 0;
+    int running = before;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      running += c[k];
+      fits += running <= kMaxCandidates ? 1 : 0;
+    }
+    fits = wave_sum_int(fits);
+    if (lane == 0) shared_cutoff = max(fits, 1);
   }
   __syncthreads();
   const int cutoff_bin = shared_cutoff;
 
-  // 4. Ordered compaction: thread t scans the contiguous index range
-  // [t*per, (t+1)*per), counts, takes an exclusive prefix over threads, writes.
-  const int per = (vocab + kSampleThreads - 1) / kSampleThreads;
-  const int lo = min(vocab, t * per);
-  const int hi = min(vocab, lo + per);
-  auto is_candidate = [&](int i, float* scaled_out) {
-    const float scaled = (logits[i] - max_logit) * inv_temperature;
+  // 4. Ordered compaction. Wave w owns the index range [w * seg, (w + 1) * seg)
+  // and walks it 64 consecutive logits per step (coalesced): it counts its
+  // candidates, takes the exclusive prefix over the waves, then writes them
+  // in index order (a lane's slot is the candidates of the lanes below it).
+  auto is_candidate = [&](float logit, float* scaled_out) {
+    const float scaled = (logit - max_logit) * inv_temperature;
     const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
     *scaled_out = scaled;
     return bin < cutoff_bin;
   };
+  const int seg = ((vocab + kSampleWaves - 1) / kSampleWaves + 63) / 64 * 64;
+  const int lo = min(vocab, wave * seg);
+  const int hi = min(vocab, lo + seg);
   int mine = 0;
-  for (int i = lo; i < hi; ++i) {
-    float scaled;
-    if (is_candidate(i, &scaled)) ++mine;
+  for (int base = lo; base < hi; base += 64 * kSampleBatch) {
+    float v[kSampleBatch];
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) {
+      const int i = base + 64 * k + lane;
+      v[k] = i < hi ? logits[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) {
+      float scaled;
+      const bool take = base + 64 * k + lane < hi && is_candidate(v[k], &scaled);
+      mine += __popcll(__ballot(take));
+    }
   }
-  counts[t] = mine;
+  if (lane == 0) wave_counts[wave] = mine;
   __syncthreads();
-  // Inclusive scan (Hillis-Steele) over the 1024 counts.
-  for (int o = 1; o < kSampleThreads; o <<= 1) {
-    const int add = t >= o ? counts[t - o] : 0;
-    __syncthreads();
-    counts[t] += add;
-    __syncthreads();
+  int total_found = 0;
+  int slot = 0;
+  for (int w = 0; w < kSampleWaves; ++w) {
+    if (w == wave) slot = total_found;
+    total_found += wave_counts[w];
   }
-  const int total_found = counts[kSampleThreads - 1];
-  int slot = counts[t] - mine;
-  for (int i = lo; i < hi && slot < kMaxCandidates; ++i) {
-    float scaled;
-    if (is_candidate(i, &scaled)) {
-      values[slot] = scaled;
-      indices[slot] = i;
-      ++slot;
+  for (int base = lo; base < hi && slot < kMaxCandidates; base += 64 * kSampleBatch) {
+    float v[kSampleBatch];
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) {
+      const int i = base + 64 * k + lane;
+      v[k] = i < hi ? logits[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kSampleBatch; ++k) {
+      const int i = base + 64 * k + lane;
+      float scaled = 0.0f;
+      const bool take = i < hi && is_candidate(v[k], &scaled);
+      const unsigned long long mask = __ballot(take);
+      const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+      if (take && slot + below < kMaxCandidates) {
+        values[slot + below] = scaled;
+        indices[slot + below] = i;
+      }
+      slot += __popcll(mask);
     }
   }
   const int found = min(total_found, kMaxCandidates);

@@ -522,6 +522,27 @@ def test_sampling_matches_oracle(gpu, orc, lcr):
             assert got == exp, f"trial {trial} T={T} k={k} p={pp} u={u}: gpu {got} oracle {exp}"
 
 
+def test_sampling_edges_match_oracle(gpu, orc, lcr):
+    """Vocabularies that do not fill the sampler's per-wave ranges, and a
+    first histogram bin holding more than 1024 candidates (the cutoff is then
+    one bin and the candidates are the first 1024 in index order)."""
+    lib = gpu
+    r = rng(91)
+    uniforms = lcr.philox_uniforms(7, 32)
+    cases = []
+    for vocab in (1, 63, 64, 65, 1000, 1025, 4097):
+        cases.append(r.normal(0, 1.2, size=vocab).astype(np.float32))
+    crowded = r.normal(-30, 1, size=128256).astype(np.float32)
+    crowded[r.choice(128256, 5000, replace=False)] = np.float32(4.0) - r.random(5000).astype(np.float32) * 0.01
+    cases.append(crowded)
+    for n, logits in enumerate(cases):
+        for (T, k, pp) in [(0.8, 40, 0.95), (1.0, 0, 0.9), (1.0, 0, 1.0), (2.0, 3, 1.0)]:
+            u = uniforms[n % 32]
+            got = gpu_sample(lib, logits, T, k, pp, u)
+            exp = oracle.sample(logits, T, k, pp, u)
+            assert got == exp, f"vocab {logits.size} T={T} k={k} p={pp} u={u}: gpu {got} oracle {exp}"
+
+
 def test_argmax_ties_and_edges(gpu, orc):
     lib = gpu
     r = rng(3)

@@ -51,11 +51,23 @@ __global__ __launch_bounds__(kSoftmaxThreads) void causal_softmax_kernel(
 
   float m = kSoftmaxIdentity;
   float l = 0.0f;
-  for (int k = t; k < limit; k += kSoftmaxThreads) {
-    const float s = scores[base + k];
-    const float merged = fmaxf(m, s);
-    l = __builtin_fmaf(l, lcr_expf(m - merged), lcr_expf(s - merged));
-    m = merged;
+  // Keys t, t + 256, ... in that order, four loads in flight at a time.
+  constexpr int kBatch = 4;
+  for (int k0 = t; k0 < limit; k0 += kBatch * kSoftmaxThreads) {
+    float s[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int k = k0 + b * kSoftmaxThreads;
+      s[b] = k < limit ? scores[base + k] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (k0 + b * kSoftmaxThreads < limit) {
+        const float merged = fmaxf(m, s[b]);
+        l = __builtin_fmaf(l, lcr_expf(m - merged), lcr_expf(s[b] - merged));
+        m = merged;
+      }
+    }
   }
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) {
@@ -78,9 +90,18 @@ __global__ __launch_bounds__(kSoftmaxThreads) void causal_softmax_kernel(
   __syncthreads();
   const float row_max = row_stats[0];
   const float inv = 1.0f / row_stats[1];
-  for (int k = t; k < keys; k += kSoftmaxThreads) {
-    const float p = k < limit ? lcr_expf(scores[base + k] - row_max) * inv : 0.0f;
-    probs[base + k] = float_to_elem(p);
+  for (int k0 = t; k0 < keys; k0 += kBatch * kSoftmaxThreads) {
+    float s[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int k = k0 + b * kSoftmaxThreads;
+      s[b] = k < limit ? scores[base + k] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int k = k0 + b * kSoftmaxThreads;
+      if (k < keys) probs[base + k] = float_to_elem(k < limit ? lcr_expf(s[b] - row_max) * inv : 0.0f);
+    }
   }
 }
 

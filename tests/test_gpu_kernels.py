@@ -371,6 +371,8 @@ GEMM_CASES = [
     # 256 x 256 tiles: the LDS ring at K = 2048 with ragged tokens, K shorter
     # than the ring (64, 32), and a K that is not a multiple of 32
     (1000, 16384, 2048), (512, 65536, 64), (512, 65536, 32), (1024, 16384, 520),
+    # 256 x 128 ring tiles (a few hundred tokens): whole, ragged tokens, split K
+    (512, 16384, 2048), (520, 3072, 2048), (384, 2048, 8192),
 ]
 
 

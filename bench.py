@@ -25,7 +25,13 @@ The JSON line also carries:
   cpu_baseline  the CPU oracle (oracle/, the restatement of the reference's
                 decode step) on this box's host cores: the same prompt is
                 prefilled untimed, then a bounded number of greedy decode steps
-                (decode + argmax) over the same context range is timed.
+                (decode + argmax) over the same context range is timed;
+  oracle_greedy_parity
+                the GPU's greedy sequence, with the prompt prefilled through the
+                decode path as the oracle's is, against the oracle's sequence
+                from that CPU run (the timed run's MFMA prefill is within
+                tolerance of the oracle, not bit-exact, so its continuation can
+                part from the oracle's at a near-tie).
 
 --counters runs a short eager (un-captured) decode plus one device copy of
 256 MiB and prints a line: the program to put under rocprofv3 --pmc, where the
@@ -94,10 +100,12 @@ def cpu_baseline(model_dir: Path, prompt, steps: int, max_seq: int):
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     ref = oracle.OracleModel(model_dir, max_seq=max_seq)
     tok = oracle.argmax(ref.prefill(prompt, use_decode_path=True))  # untimed: fills the KV cache
+    tokens = [tok]
     t0 = time.perf_counter()
     done = 0
     while done < steps:
         tok = oracle.argmax(ref.decode(tok))
+        tokens.append(tok)
         done += 1
         if time.perf_counter() - t0 > CPU_BASELINE_SECONDS:
             break  # bounded sample on a slow host
@@ -115,7 +123,23 @@ def cpu_baseline(model_dir: Path, prompt, steps: int, max_seq: int):
                   f"rows, {threads} threads)",
         "ms_per_token": 1000.0 * dt / steps,
         "seconds": dt,
+        "_tokens": tokens,  # the greedy sequence, compared with the GPU's below (not printed)
     }
+
+
+def greedy_parity(lcr, model_dir: Path, prompt, steps: int, max_seq: int, oracle_tokens) -> dict:
+    """The GPU's greedy sequence with the prompt prefilled through the decode
+    path (bit-exact against the oracle, like the decode steps themselves)
+    against the oracle's sequence from the CPU baseline run."""
+    m = lcr.Model(model_dir, max_seq=max_seq, prefill_via_decode=1)
+    first = m.sample(m.prefill(prompt), 0.0)
+    ids, _ = m.generate_greedy(first, steps)
+    m.close()
+    gpu = [int(first)] + [int(x) for x in ids]
+    n = min(len(gpu), len(oracle_tokens))
+    diverge = next((i for i in range(n) if gpu[i] != oracle_tokens[i]), None)
+    return {"greedy_tokens_compared": n, "identical": diverge is None, "first_divergence": diverge,
+            "prefill": "decode path on the GPU and in the CPU oracle"}
 
 
 def prefill_flops(config: dict, T: int) -> float:
@@ -344,8 +368,11 @@ def main() -> int:
         extra["sampling_config5"] = sampling_run(lcr, config)
 
     cpu = None
+    parity = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(model_dir, prompt, args.cpu_steps, args.max_seq)
+        parity = greedy_parity(lcr, model_dir, prompt, len(cpu["_tokens"]) - 1, args.max_seq,
+                               cpu.pop("_tokens"))
 
     result = {
         "metric": "decode tok/s + HBM GB/s (% of peak), Llama-3.2-1B-arch bf16 batch 1",
@@ -394,6 +421,7 @@ def main() -> int:
         "kernels": kernels,
         **extra,
         "cpu_baseline": cpu,
+        "oracle_greedy_parity": parity,
         "generated_first_ids": [int(x) for x in ids[:8]],
         "setup_s": {"checkpoint": gen_s, "load": load_s},
         "reference_frac_of_peak": REFERENCE_PEAK_FRAC,

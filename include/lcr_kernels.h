@@ -165,6 +165,26 @@ size_t lcr_gemm_workspace_bytes(int T, int N, int K);
 int lcr_gemm_swiglu_ws(void* act, const void* X, const void* W_gate_up, int T, int ffn, int K,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* table[p * (head_dim / 2) + i] = (cos a, sin a) for a = float(p) * inv_freq[i]
+ * and p < positions: the per-position angles lcr_rope_q and lcr_rope_write_kv
+ * evaluate (src/kernels/rope.cu:33-87), the same values, tabulated once. The
+ * table is positions * head_dim / 2 pairs of floats. */
+int lcr_rope_table(float* table, const float* inv_freq, int positions, int head_dim, void* stream);
+
+/* The fused q/k/v projection of src/model.cu:393 followed by launch_rope_q and
+ * launch_rope_write_kv (src/model.cu:396-406, src/kernels.cuh:62-72) in one
+ * pass, bit-identical to lcr_gemm_ws into a [T][N] buffer and those two
+ * kernels reading it: each output is rounded to the element type, queries
+ * are rotated into q_heads [num_heads][T][head_dim], keys rotated and values
+ * copied into the cache through the view at positions start_position + t.
+ * W_qkv holds the num_heads query heads, then the view's num_kv_heads key and
+ * value heads, head_dim rows each (N = (num_heads + 2 num_kv_heads) head_dim).
+ * rope_table comes from lcr_rope_table and covers positions up to
+ * start_position + T. head_dim is 64 or 128; workspace as for lcr_gemm_ws. */
+int lcr_gemm_qkv_rope_ws(void* q_heads, const lcr_kv_view* view, const void* X, const void* W_qkv,
+                         const float* rope_table, int T, int num_heads, int K, int start_position,
+                         int paged, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Causal GQA attention for a prefill chunk: the two strided-batched GEMMs and
  * the softmax of src/model.cu:509-560 (K13 gather + G6 + K10 + G7 + K7) in
  * one flash-style pass reading the cache through the view.

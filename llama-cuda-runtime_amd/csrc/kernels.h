@@ -129,6 +129,15 @@ inline void launch_gemm_swiglu(elem_t* act, const elem_t* X, const elem_t* W_gat
   check_kernel_status(lcr_gemm_swiglu_ws(act, X, W_gate_up, T, ffn, K, workspace, workspace_bytes, stream));
 }
 
+inline void launch_gemm_qkv_rope(elem_t* q_heads, const KvCacheView& view, const elem_t* X, const elem_t* W_qkv,
+                                 const float2* rope_table, int T, int num_heads, int K, int start_position,
+                                 bool paged, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const lcr_kv_view v = view.to_c();
+  check_kernel_status(lcr_gemm_qkv_rope_ws(q_heads, &v, X, W_qkv, reinterpret_cast<const float*>(rope_table), T,
+                                           num_heads, K, start_position, paged ? 1 : 0, workspace,
+                                           workspace_bytes, stream));
+}
+
 inline void launch_prefill_attention(elem_t* out, const elem_t* q_heads, const KvCacheView& view,
                                      int num_heads, int heads_per_kv, int tokens,
                                      int start_position, float scale, bool paged,

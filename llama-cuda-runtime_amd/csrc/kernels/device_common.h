@@ -66,6 +66,12 @@ __device__ __forceinline__ uint32_t pack_elems(float lo, float hi) {
          (static_cast<uint32_t>(float_to_elem_bits(hi)) << 16);
 }
 
+// Half-split RoPE of one pair by the angle's (cos, sin): (lo c - hi s,
+// hi c + lo s), separate products and a subtract / add.
+__device__ __forceinline__ float2 rope_rotate(float lo, float hi, float2 cs) {
+  return make_float2(lo * cs.x - hi * cs.y, hi * cs.x + lo * cs.y);
+}
+
 // Eight elements of a 16-byte chunk, widened to float, in memory order.
 __device__ __forceinline__ void unpack8(const vec16& v, float* out) {
 #pragma unroll

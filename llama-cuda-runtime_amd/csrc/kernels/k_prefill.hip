@@ -111,6 +111,26 @@ constexpr int kGemmPitch = kStageK;
 // 2m + 1 then pair gate and up values of the same outputs, and the epilogue
 // writes act = rne(silu(rne(gate)) * rne(up)), the same roundings as a GEMM
 // to 16-bit followed by the SwiGLU kernel.
+//
+// Projection launches with RoPE (rope.table != nullptr) write nothing to Y:
+// the q/k/v projection's output rows are num_heads query heads, then the
+// cache's key heads and value heads, head_dim rows each. Each output is
+// rounded to the element type, as a 16-bit GEMM output would be; queries are
+// then rotated into q_heads [num_heads][T][head_dim], keys rotated and values
+// copied into the cache at position start_position + t, with the arithmetic
+// of the separate RoPE kernels reading a 16-bit output. The unsplit epilogue
+// pairs element i of a head with i + head_dim / 2 inside one lane (fragments
+// m and m + head_dim / 32 of a 64- or 128-row head block), so a wave's rows
+// must hold whole heads; split launches rotate in the reduction.
+struct GemmRope {
+  const float2* table;  // (cos, sin) of position p, pair i at p * head_dim / 2 + i
+  elem_t* q_heads;
+  KvCacheView view;
+  int start_position;
+  int q_dim;  // num_heads * head_dim: the rows before it are queries
+  int paged;
+};
+
 struct GemmGrid {
   int tiles_t;
   int tiles_w;
@@ -118,6 +138,7 @@ struct GemmGrid {
   int k_chunk;
   float* partial;  // nullptr: no split, write Y
   int ffn;         // > 0: gated (Y is act[T][ffn], N == 2 * ffn)
+  GemmRope rope;
 };
 
 __device__ __forceinline__ int weight_row(int p, int ffn) {
@@ -128,6 +149,93 @@ __device__ __forceinline__ float swiglu_rounded(float gate, float up) {
   const float g = elem_bits_to_float(float_to_elem_bits(gate));
   const float u = elem_bits_to_float(float_to_elem_bits(up));
   return elem_bits_to_float(float_to_elem_bits(lcr_silu(g) * u));
+}
+
+__device__ __forceinline__ float round_to_elem(float x) { return elem_bits_to_float(float_to_elem_bits(x)); }
+
+// Four pairs (i .. i + 3 with i + half .. i + half + 3) of output row t of the
+// head whose first projection row is row0, already rounded to the element
+// type: rotated into q_heads or the keys, or copied into the values.
+template <bool kPaged>
+__device__ __forceinline__ void emit_rope_quad(const GemmRope& r, int T, int t, int row0, int i, int head_dim,
+                                               const float (&lo)[4], const float (&hi)[4]) {
+  const int half = head_dim >> 1;
+  const int position = r.start_position + t;
+  const int kv_dim = r.view.num_kv_heads * head_dim;
+  float a[4], b[4];
+  elem_t* dst;
+  if (row0 < r.q_dim + kv_dim) {
+    const float4* cs = reinterpret_cast<const float4*>(r.table + static_cast<size_t>(position) * half + i);
+    const float4 c01 = cs[0], c23 = cs[1];
+    const float2 c[4] = {{c01.x, c01.y}, {c01.z, c01.w}, {c23.x, c23.y}, {c23.z, c23.w}};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float2 rot = rope_rotate(lo[v], hi[v], c[v]);
+      a[v] = rot.x;
+      b[v] = rot.y;
+    }
+    dst = row0 < r.q_dim
+              ? r.q_heads + (static_cast<size_t>(row0 / head_dim) * T + t) * head_dim + i
+              : r.view.keys + r.view.offset<kPaged>((row0 - r.q_dim) / head_dim, position) + i;
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      a[v] = lo[v];
+      b[v] = hi[v];
+    }
+    dst = r.view.values + r.view.offset<kPaged>((row0 - r.q_dim - kv_dim) / head_dim, position) + i;
+  }
+  *reinterpret_cast<uint2*>(dst) = uint2{pack_elems(a[0], a[1]), pack_elems(a[2], a[3])};
+  *reinterpret_cast<uint2*>(dst + half) = uint2{pack_elems(b[0], b[1]), pack_elems(b[2], b[3])};
+}
+
+// The unsplit RoPE epilogue for heads of 32 kHalfFrags rows: fragment m of a
+// head block holds pairs 16 m + 4 grp + v, its partner fragment m + kHalfFrags
+// the matching high halves.
+template <int FW, int FT, int kHalfFrags, bool kPaged>
+__device__ __forceinline__ void store_rope_tile(const mfma_acc4 (&acc)[FW][FT], const GemmRope& r, int T, int N,
+                                                int t_base, int w_base, int col, int grp) {
+  constexpr int kHeadDim = 32 * kHalfFrags;
+  static_assert(FW % (2 * kHalfFrags) == 0, "a wave's rows hold whole heads");
+#pragma unroll
+  for (int j = 0; j < FT; ++j) {
+    const int t = t_base + j * 16 + col;
+    if (t >= T) continue;
+#pragma unroll
+    for (int hb = 0; hb < FW / (2 * kHalfFrags); ++hb) {
+      const int row0 = w_base + hb * kHeadDim;
+      if (row0 >= N) continue;
+#pragma unroll
+      for (int m = 0; m < kHalfFrags; ++m) {
+        const int f = 2 * kHalfFrags * hb + m;
+        float lo[4], hi[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          lo[v] = round_to_elem(acc[f][j][v]);
+          hi[v] = round_to_elem(acc[f + kHalfFrags][j][v]);
+        }
+        emit_rope_quad<kPaged>(r, T, t, row0, 16 * m + 4 * grp, kHeadDim, lo, hi);
+      }
+    }
+  }
+}
+
+template <int FW, int FT>
+__device__ __forceinline__ void store_rope_heads(const mfma_acc4 (&acc)[FW][FT], const GemmRope& r, int T, int N,
+                                                 int t_base, int w_base, int col, int grp) {
+  if (r.view.head_dim == 64) {
+    if (r.paged) {
+      store_rope_tile<FW, FT, 2, true>(acc, r, T, N, t_base, w_base, col, grp);
+    } else {
+      store_rope_tile<FW, FT, 2, false>(acc, r, T, N, t_base, w_base, col, grp);
+    }
+  } else if constexpr (FW % 8 == 0) {
+    if (r.paged) {
+      store_rope_tile<FW, FT, 4, true>(acc, r, T, N, t_base, w_base, col, grp);
+    } else {
+      store_rope_tile<FW, FT, 4, false>(acc, r, T, N, t_base, w_base, col, grp);
+    }
+  }
 }
 
 struct GemmWork {
@@ -155,7 +263,14 @@ __device__ __forceinline__ bool gemm_work(const GemmGrid& g, int BW, int BT, int
 template <int FW, int FT, bool kFp32Out>
 __device__ __forceinline__ void store_gemm_tile(const mfma_acc4 (&acc)[FW][FT], void* Y, float* partial,
                                                 int T, int N, int t_base, int w_base, int col, int grp,
-                                                int ffn) {
+                                                const GemmGrid& grid) {
+  const int ffn = grid.ffn;
+  if constexpr (!kFp32Out) {
+    if (grid.rope.table != nullptr && partial == nullptr) {
+      store_rope_heads<FW, FT>(acc, grid.rope, T, N, t_base, w_base, col, grp);
+      return;
+    }
+  }
   if (ffn > 0 && partial == nullptr) {
     // fragments 2m (gate) and 2m + 1 (up): features (w_base + 32m) / 2 + 4grp + v
 #pragma unroll
@@ -325,7 +440,7 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
   }
 
   float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
-  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp, grid.ffn);
+  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp, grid);
 }
 
 // The large-tile GEMM with a ring of kStages LDS stages of 32 K each, filled
@@ -490,7 +605,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   }
 
   float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
-  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp, grid.ffn);
+  store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp, grid);
 }
 
 constexpr int kRingStages = 4;
@@ -527,6 +642,37 @@ __global__ __launch_bounds__(256) void gemm_reduce_swiglu_kernel(elem_t* __restr
   packed.x = pack_elems(swiglu_rounded(g.x, u.x), swiglu_rounded(g.y, u.y));
   packed.y = pack_elems(swiglu_rounded(g.z, u.z), swiglu_rounded(g.w, u.w));
   *reinterpret_cast<uint2*>(act + i) = packed;
+}
+
+// Split projection launches with RoPE: one thread per (token, head, four
+// pairs) sums the slices of its four low and four high outputs in slice
+// order, then rounds, rotates and writes them as the unsplit epilogue does.
+template <bool kPaged>
+__global__ __launch_bounds__(256) void gemm_reduce_rope_kernel(const float* __restrict__ partial, int splits,
+                                                               int T, int N, GemmRope r) {
+  const int head_dim = r.view.head_dim;
+  const int half = head_dim >> 1;
+  const int quads = half >> 2;
+  const int heads = N / head_dim;
+  const size_t u = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (u >= static_cast<size_t>(T) * heads * quads) return;
+  const int q = static_cast<int>(u % quads);
+  const size_t rest = u / quads;
+  const int h = static_cast<int>(rest % heads);
+  const int t = static_cast<int>(rest / heads);
+  const size_t count = static_cast<size_t>(T) * N;
+  const size_t at = static_cast<size_t>(t) * N + static_cast<size_t>(h) * head_dim + 4 * q;
+  float4 lo = *reinterpret_cast<const float4*>(partial + at);
+  float4 hi = *reinterpret_cast<const float4*>(partial + at + half);
+  for (int s = 1; s < splits; ++s) {
+    const float4 ls = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(s) * count + at);
+    const float4 hs = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(s) * count + at + half);
+    lo.x += ls.x; lo.y += ls.y; lo.z += ls.z; lo.w += ls.w;
+    hi.x += hs.x; hi.y += hs.y; hi.z += hs.z; hi.w += hs.w;
+  }
+  const float l[4] = {round_to_elem(lo.x), round_to_elem(lo.y), round_to_elem(lo.z), round_to_elem(lo.w)};
+  const float hh[4] = {round_to_elem(hi.x), round_to_elem(hi.y), round_to_elem(hi.z), round_to_elem(hi.w)};
+  emit_rope_quad<kPaged>(r, T, t, h * head_dim, 4 * q, head_dim, l, hh);
 }
 
 // Y = sum over slices of the fp32 partial products, in slice order.
@@ -580,8 +726,10 @@ struct GemmPlan {
 // measured fraction of a compute unit's MFMA peak. Splitting K is considered
 // only when the tiles alone leave compute units idle, and costs the fp32
 // partials' round trip through memory plus a launch. Each slice keeps at
-// least 256 K and is a whole number of the shape's K stages.
-GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes) {
+// least 256 K and is a whole number of the shape's K stages. With
+// wide_waves, an unsplit plan uses only shapes whose waves own 128 W rows
+// (the RoPE epilogue for 128-row heads).
+GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wide_waves = false) {
   struct Option {
     GemmShape shape;
     int bw, bt, stage_k;
@@ -605,6 +753,7 @@ GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes) {
       const int k_chunk = ((K + splits - 1) / splits + o.stage_k - 1) / o.stage_k * o.stage_k;
       if (splits > 1 && k_chunk < 256) break;
       const int used = (K + k_chunk - 1) / k_chunk;
+      if (wide_waves && used == 1 && o.bt != 256) continue;
       const size_t bytes = used > 1 ? static_cast<size_t>(used) * T * N * sizeof(float) : 0;
       if (bytes > workspace_bytes) break;
       const long long rounds = (tiles * used + cus - 1) / cus;
@@ -645,10 +794,13 @@ void launch_gemm_ring(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, 
 }
 
 void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K, void* workspace,
-              size_t workspace_bytes, int ffn, hipStream_t s) {
-  const GemmPlan plan = plan_gemm(T, N, K, device_compute_units(), workspace != nullptr ? workspace_bytes : 0);
+              size_t workspace_bytes, int ffn, hipStream_t s, const GemmRope* rope = nullptr) {
+  const bool wide_waves = rope != nullptr && rope->view.head_dim == 128;
+  const GemmPlan plan =
+      plan_gemm(T, N, K, device_compute_units(), workspace != nullptr ? workspace_bytes : 0, wide_waves);
   GemmGrid grid{(T + plan.bt - 1) / plan.bt, (N + plan.bw - 1) / plan.bw, plan.splits, plan.k_chunk,
-                plan.splits > 1 ? static_cast<float*>(workspace) : nullptr, ffn};
+                plan.splits > 1 ? static_cast<float*>(workspace) : nullptr, ffn,
+                rope != nullptr ? *rope : GemmRope{}};
   switch (plan.shape) {
     case GemmShape::kRing256x256:
       launch_gemm_ring<256, kRingWaves, kRingStages>(Y, fp32_out, X, W, T, N, K, grid, s);
@@ -666,7 +818,15 @@ void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
       launch_gemm_tiles<128, 128, 2, 2>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
   }
-  if (plan.splits > 1 && ffn > 0) {
+  if (plan.splits > 1 && rope != nullptr) {
+    const size_t threads = static_cast<size_t>(T) * (N / rope->view.head_dim) * (rope->view.head_dim / 8);
+    const unsigned blocks = static_cast<unsigned>((threads + 255) / 256);
+    if (rope->paged) {
+      gemm_reduce_rope_kernel<true><<<blocks, 256, 0, s>>>(grid.partial, plan.splits, T, N, *rope);
+    } else {
+      gemm_reduce_rope_kernel<false><<<blocks, 256, 0, s>>>(grid.partial, plan.splits, T, N, *rope);
+    }
+  } else if (plan.splits > 1 && ffn > 0) {
     const size_t count = static_cast<size_t>(T) * ffn;
     gemm_reduce_swiglu_kernel<<<static_cast<unsigned>((count + 1023) / 1024), 256, 0, s>>>(
         static_cast<elem_t*>(Y), grid.partial, plan.splits, T, ffn);
@@ -1124,6 +1284,46 @@ extern "C" int lcr_gemm_swiglu_ws(void* act, const void* X, const void* W_gate_u
   CAPI_CHECK((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "gemm workspace must be 16-byte aligned");
   run_gemm(act, false, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W_gate_up), T, 2 * ffn, K,
            workspace, workspace_bytes, ffn, static_cast<hipStream_t>(stream));
+  CAPI_LAUNCHED();
+  return LCR_OK;
+}
+
+extern "C" int lcr_gemm_qkv_rope_ws(void* q_heads, const lcr_kv_view* view, const void* X, const void* W_qkv,
+                                    const float* rope_table, int T, int num_heads, int K, int start_position,
+                                    int paged, void* workspace, size_t workspace_bytes, void* stream) {
+  CAPI_CHECK(view != nullptr, "gemm_qkv_rope needs a cache view");
+  CAPI_CHECK(num_heads >= 0 && view->num_kv_heads >= 0 && start_position >= 0,
+             "gemm_qkv_rope needs non-negative head counts and start position");
+  const int head_dim = view->head_dim;
+  CAPI_CHECK(head_dim == 64 || head_dim == 128, "gemm_qkv_rope supports head_dim 64 or 128, got " << head_dim);
+  const long long n = static_cast<long long>(num_heads + 2 * view->num_kv_heads) * head_dim;
+  CAPI_CHECK(n <= INT32_MAX, "gemm_qkv_rope output width " << n << " is too large");
+  const int N = static_cast<int>(n);
+  const int status = gemm_checks(q_heads, X, W_qkv, T, N, K);
+  if (status != LCR_OK || T == 0 || N == 0) return status;
+  CAPI_CHECK(rope_table != nullptr && (reinterpret_cast<uintptr_t>(rope_table) & 15u) == 0,
+             "gemm_qkv_rope needs a 16-byte aligned RoPE table");
+  CAPI_CHECK(view->num_kv_heads == 0 ||
+                 (view->keys != nullptr && view->values != nullptr &&
+                  (reinterpret_cast<uintptr_t>(view->keys) & 7u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(view->values) & 7u) == 0),
+             "gemm_qkv_rope needs 8-byte aligned cache keys and values");
+  CAPI_CHECK(view->page_stride % 4 == 0 && view->head_stride % 4 == 0,
+             "gemm_qkv_rope needs cache strides in whole 8-byte groups");
+  CAPI_CHECK(!paged || view->page_table != nullptr, "a paged cache view needs a page table");
+  CAPI_CHECK(!paged || view->page_size > 0, "a paged cache view needs a positive page size");
+  CAPI_CHECK(workspace != nullptr || workspace_bytes == 0, "gemm workspace of " << workspace_bytes
+                                                                               << " bytes has no pointer");
+  CAPI_CHECK((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "gemm workspace must be 16-byte aligned");
+  GemmRope rope{};
+  rope.table = reinterpret_cast<const float2*>(rope_table);
+  rope.q_heads = static_cast<elem_t*>(q_heads);
+  rope.view = KvCacheView::from_c(*view);
+  rope.start_position = start_position;
+  rope.q_dim = num_heads * head_dim;
+  rope.paged = paged != 0 ? 1 : 0;
+  run_gemm(nullptr, false, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W_qkv), T, N, K, workspace,
+           workspace_bytes, 0, static_cast<hipStream_t>(stream), &rope);
   CAPI_LAUNCHED();
   return LCR_OK;
 }

@@ -14,6 +14,7 @@
 #include "../capi_util.h"
 #include "../kv_cache.h"
 #include "device_common.h"
+#include "fill.h"
 
 namespace lcr {
 namespace {
@@ -33,8 +34,9 @@ __device__ __forceinline__ void token_angles(float2* cs, const float* inv_freq, 
 }
 
 __device__ __forceinline__ void rotate(float lo, float hi, float2 cs, float* out_lo, float* out_hi) {
-  *out_lo = lo * cs.x - hi * cs.y;
-  *out_hi = hi * cs.x + lo * cs.y;
+  const float2 r = rope_rotate(lo, hi, cs);
+  *out_lo = r.x;
+  *out_hi = r.y;
 }
 
 __global__ __launch_bounds__(kRopeThreads) void rope_q_kernel(elem_t* __restrict__ q_heads,
@@ -133,4 +135,18 @@ extern "C" int lcr_rope_write_kv(const lcr_kv_view* view, const void* k_proj, co
   }
   CAPI_LAUNCHED();
   return LCR_OK;
+}
+
+extern "C" int lcr_rope_table(float* table, const float* inv_freq, int positions, int head_dim, void* stream) {
+  CAPI_CHECK(positions >= 0, "rope_table needs a non-negative position count");
+  CAPI_CHECK(head_dim > 0 && head_dim % 2 == 0,
+             "head_dim must be positive and even for RoPE, got " << head_dim);
+  if (positions == 0) return LCR_OK;
+  CAPI_CHECK(table != nullptr && inv_freq != nullptr, "rope_table needs a table and inverse frequencies");
+  CAPI_CHECK((reinterpret_cast<uintptr_t>(table) & 7u) == 0, "rope_table needs an 8-byte aligned table");
+  return capi::guarded([&] {
+    build_rope_table(reinterpret_cast<float2*>(table), inv_freq, positions, head_dim / 2,
+                     static_cast<hipStream_t>(stream));
+    return LCR_OK;
+  });
 }

@@ -54,7 +54,10 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
                                  config_.num_heads, config_.num_kv_heads, config_.head_dim) &&
            config_.vocab_size > 0;
 
-  if (fused_) {
+  // The table serves the fused decode step and the prefill q/k/v projection
+  // with RoPE in its epilogue.
+  qkv_rope_ = config_.head_dim == 64 || config_.head_dim == 128;
+  if (fused_ || qkv_rope_) {
     const int half = config_.head_dim / 2;
     HIP_CHECK(hipMalloc(&rope_table_, static_cast<size_t>(options_.max_seq) * half * sizeof(float2)));
     build_rope_table(rope_table_, inv_freq_, options_.max_seq, half, stream_);
@@ -577,17 +580,21 @@ void Model::run_layers(int tokens, int start_position) {
       launch_rmsnorm(normed_, x_, w.input_norm, tokens, hidden, config_.rms_norm_eps, stream_);
     }
     input_norm_done_ = false;
-    {
-      ProfileScope scope(&profiler_, "qkv_proj", stream_);
-      if (tokens == 1) {
-        launch_gemv(qkv_, false, w.qkv_proj, normed_, qkv_stride, hidden, stream_);
-      } else {
-        launch_gemm(qkv_, false, normed_, w.qkv_proj, tokens, qkv_stride, hidden, gemm_workspace_,
-                    gemm_workspace_size_, stream_);
-      }
-    }
     const KvCacheView view = kv_cache_->view(layer);
-    {
+    if (tokens > 1 && qkv_rope_) {
+      ProfileScope scope(&profiler_, "qkv_proj + rope + kv write", stream_);
+      launch_gemm_qkv_rope(q_heads_, view, normed_, w.qkv_proj, rope_table_, tokens, config_.num_heads, hidden,
+                           start_position, paged, gemm_workspace_, gemm_workspace_size_, stream_);
+    } else {
+      {
+        ProfileScope scope(&profiler_, "qkv_proj", stream_);
+        if (tokens == 1) {
+          launch_gemv(qkv_, false, w.qkv_proj, normed_, qkv_stride, hidden, stream_);
+        } else {
+          launch_gemm(qkv_, false, normed_, w.qkv_proj, tokens, qkv_stride, hidden, gemm_workspace_,
+                      gemm_workspace_size_, stream_);
+        }
+      }
       ProfileScope scope(&profiler_, "rope + kv write", stream_);
       launch_rope_q(q_heads_, qkv_, inv_freq_, tokens, start_position, config_.num_heads,
                     config_.head_dim, qkv_stride, stream_);

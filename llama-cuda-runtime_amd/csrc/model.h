@@ -150,7 +150,8 @@ class Model {
   const elem_t* lm_head_ = nullptr;
   std::vector<LayerWeights> layers_;
   float* inv_freq_ = nullptr;
-  float2* rope_table_ = nullptr;  // fused step: [max_seq][head_dim / 2] (cos, sin)
+  float2* rope_table_ = nullptr;  // fused step, prefill q/k/v: [max_seq][head_dim / 2] (cos, sin)
+  bool qkv_rope_ = false;         // prefill chunks rotate in the q/k/v projection's epilogue
 
   DeviceArena arena_;
   std::unique_ptr<KvCache> kv_cache_;

@@ -442,6 +442,89 @@ def test_gemm_swiglu_matches_gemm_then_swiglu(gpu, T, F, K):
         expect_bits_equal(host(got), host(want), f"gemm+swiglu {T}x{F}x{K} workspace {wsb}")
 
 
+def test_rope_table_matches_oracle(gpu, orc):
+    """lcr_rope_table holds the (cos, sin) the RoPE kernels evaluate per
+    token: the oracle's sincos of float(p) * inv_freq[i], bit for bit."""
+    lib = gpu
+    hd, positions = 128, 5000
+    freq = rope_table(hd)
+    table = zeros_dev(positions * hd, np.float32)
+    ok(lib, lib.lcr_rope_table(p(table), p(dev(freq)), positions, hd, NULL), "rope_table")
+    got = host(table, np.float32).reshape(positions, hd // 2, 2)
+    L = orc.load()
+    s, c = ctypes.c_float(), ctypes.c_float()
+    for pos in (0, 1, 2, 17, 255, 1024, 4093, 4999):
+        for i in range(hd // 2):
+            L.orc_sincosf(float(np.float32(pos) * freq[i]), ctypes.byref(s), ctypes.byref(c))
+            want = np.array([c.value, s.value], dtype=np.float32)
+            expect_bits_equal(got[pos, i].view(np.uint32), want.view(np.uint32), f"rope table p={pos} i={i}")
+
+
+QKV_ROPE_CASES = [
+    # (T, num_heads, kv_heads, head_dim, K, start, paged): the Llama-3.2-1B
+    # projection at 2048 tokens (unsplit 256 x 128 ring tiles) and at 512
+    # (K split, rotated in the reduction), a chunk continuing at a later
+    # position, ragged token counts, N = 640 (a tile past the last head), one
+    # token, and 128-wide heads (256 x 256 tiles when unsplit)
+    (2048, 32, 8, 64, 2048, 0, False),
+    (512, 32, 8, 64, 2048, 100, True),
+    (37, 8, 2, 64, 512, 5, False),
+    (100, 6, 2, 64, 256, 1000, True),
+    (1, 4, 2, 64, 256, 3, False),
+    (300, 16, 4, 128, 1024, 7, True),
+    (130, 8, 8, 128, 512, 0, False),
+]
+
+
+@pytest.mark.parametrize("T,nh,kv,hd,K,start,paged", QKV_ROPE_CASES)
+def test_gemm_qkv_rope_matches_unfused(gpu, lcr, T, nh, kv, hd, K, start, paged):
+    """The q/k/v projection with RoPE in its epilogue gives the bits of
+    lcr_gemm_ws to 16-bit followed by lcr_rope_q and lcr_rope_write_kv: the
+    queries and the whole key and value caches (positions outside the chunk
+    stay untouched), with the workspace's split plan and without a workspace.
+    128-wide heads restrict an unsplit plan to 256 x 256 tiles, so with a
+    workspace their plan can split K differently from the plain GEMM's; that
+    pair is compared to the GEMM's 16-bit tolerance, the others bit for bit."""
+    lib = gpu
+    r = rng(T * 31 + nh * 7 + hd + start)
+    N = (nh + 2 * kv) * hd
+    q_dim, kv_dim = nh * hd, kv * hd
+    Xd = dev(random_elems(r, (T, K)))
+    Wd = dev(random_elems(r, (N, K), 0.05))
+    freq_d = dev(rope_table(hd))
+    positions = start + T
+    table = zeros_dev(positions * hd, np.float32)
+    ok(lib, lib.lcr_rope_table(p(table), p(freq_d), positions, hd, NULL), "rope_table")
+    ws_bytes = lib.lcr_gemm_workspace_bytes(T, N, K)
+    ws = zeros_dev(max(ws_bytes, 16) // 4, np.float32)
+    max_seq = -(-positions // 16) * 16
+    pages = r.permutation(max_seq // 16) if paged else None
+    for wsp, wsb in ((p(ws), ws_bytes), (None, 0)):
+        what = f"qkv+rope T={T} heads={nh}/{kv} hd={hd} K={K} start={start} paged={paged} workspace={wsb}"
+        want_cache = Cache(kv, hd, max_seq, paged, 16, pages)
+        got_cache = Cache(kv, hd, max_seq, paged, 16, pages)
+        qkv = zeros_dev(T * N)
+        ok(lib, lib.lcr_gemm_ws(p(qkv), 0, p(Xd), p(Wd), T, N, K, wsp, wsb, NULL), "gemm_ws")
+        q_want = zeros_dev(nh * T * hd)
+        ok(lib, lib.lcr_rope_q(p(q_want), p(qkv), p(freq_d), T, start, nh, hd, N, NULL), "rope_q")
+        vw = want_cache.view(lcr)
+        ok(lib, lib.lcr_rope_write_kv(ctypes.byref(vw), ctypes.c_void_p(qkv.ptr + 2 * q_dim),
+                                      ctypes.c_void_p(qkv.ptr + 2 * (q_dim + kv_dim)), p(freq_d), T, start,
+                                      1 if paged else 0, N, NULL), "rope_write_kv")
+        q_got = zeros_dev(nh * T * hd)
+        vg = got_cache.view(lcr)
+        ok(lib, lib.lcr_gemm_qkv_rope_ws(p(q_got), ctypes.byref(vg), p(Xd), p(Wd), p(table), T, nh, K, start,
+                                         1 if paged else 0, wsp, wsb, NULL), "gemm_qkv_rope_ws")
+        sync()
+        pairs = ((q_got, q_want, "queries"), (got_cache.keys, want_cache.keys, "keys"),
+                 (got_cache.values, want_cache.values, "values"))
+        for got, want, name in pairs:
+            if hd == 128 and wsb:
+                expect_close(to_f32(host(got)), to_f32(host(want)), 8e-3, f"{what}: {name}")
+            else:
+                expect_bits_equal(host(got), host(want), f"{what}: {name}")
+
+
 PREFILL_CASES = [
     # (num_heads, kv_heads, head_dim, tokens, start, paged)
     (32, 8, 64, 7, 0, False),

@@ -881,7 +881,7 @@ struct FlashShared {
 };
 
 template <bool kPaged, int kHeadDim, int kRF>
-__global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
+__global__ __launch_bounds__(kFlashThreads, 4) void flash_prefill_kernel(
     elem_t* __restrict__ out, const elem_t* __restrict__ q_heads, KvCacheView view, int num_heads,
     int group, int tokens, int start_position, float scale_log2e) {
   constexpr int kRows = 16 * kRF;                         // query positions per block
@@ -895,8 +895,17 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
   static_assert(kKeyGroups * 4 == kFlashThreads / 64, "one wave per (head, key group)");
   __shared__ __attribute__((aligned(16))) FlashShared<kHeadDim, kRows> sh;
 
-  const int r0 = static_cast<int>(gridDim.x - 1u - blockIdx.x) * kRows;  // longest rows first
-  const int kv = blockIdx.y;
+  // XCD-aware order: XCD x (block id mod 8) takes the contiguous run of units
+  // [x * per, (x + 1) * per) of the kv-head-major order, so one XCD's L2 holds
+  // the keys and values of few kv heads (one, for 8 kv heads); within a head,
+  // the longest rows start first.
+  const int row_blocks = (tokens + kRows - 1) / kRows;
+  const int units = row_blocks * view.num_kv_heads;
+  const int per_xcd = (units + 7) / 8;
+  const int u = static_cast<int>(blockIdx.x % 8u) * per_xcd + static_cast<int>(blockIdx.x / 8u);
+  if (u >= units) return;  // the whole block: no barrier has been met
+  const int kv = u / row_blocks;
+  const int r0 = (row_blocks - 1 - u % row_blocks) * kRows;
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
   const int col = lane & 15;
@@ -926,41 +935,56 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
     }
   }
 
-  // Step `step` stages tiles 2 step and 2 step + 1: keys 128 step .. +127.
+  // Step `step` stages tiles 2 step and 2 step + 1: keys 128 step .. +127. A
+  // thread moves the same 16-byte chunk of two consecutive keys (even key
+  // first), whose transposed values sit in adjacent slots and go to LDS as
+  // 32-bit pairs.
+  constexpr int kPairs = kPer / 2;
+  static_assert(kPer % 2 == 0, "chunks move in key pairs");
   vec16 kreg[kPer], vreg[kPer];
   auto fetch = [&](int step, bool with_values) {
 #pragma unroll
-    for (int c = 0; c < kPer; ++c) {
-      const int chunk = c * kFlashThreads + threadIdx.x;
-      const int key = chunk / (kHeadDim / 8);
-      const int d0 = (chunk % (kHeadDim / 8)) * 8;
-      const size_t at = view.offset<kPaged>(kv, min(step * kPairKeys + key, last_key)) + d0;
-      kreg[c] = load16(view.keys + at);
-      if (with_values) vreg[c] = load16(view.values + at);
+    for (int c = 0; c < kPairs; ++c) {
+      const int pair = c * kFlashThreads + threadIdx.x;
+      const int key = 2 * (pair / (kHeadDim / 8));
+      const int d0 = (pair % (kHeadDim / 8)) * 8;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const size_t at = view.offset<kPaged>(kv, min(step * kPairKeys + key + e, last_key)) + d0;
+        kreg[2 * c + e] = load16(view.keys + at);
+        if (with_values) vreg[2 * c + e] = load16(view.values + at);
+      }
     }
   };
   auto deposit = [&](int buf, bool with_values) {
 #pragma unroll
-    for (int c = 0; c < kPer; ++c) {
-      const int chunk = c * kFlashThreads + threadIdx.x;
-      const int key = chunk / (kHeadDim / 8);
-      const int d0 = (chunk % (kHeadDim / 8)) * 8;
-      store16(&sh.keys[buf][key * kKeyPitch + (((d0 >> 3) ^ key_swizzle<kHeadDim>(key)) << 3)], kreg[c]);
+    for (int c = 0; c < kPairs; ++c) {
+      const int pair = c * kFlashThreads + threadIdx.x;
+      const int key = 2 * (pair / (kHeadDim / 8));
+      const int d0 = (pair % (kHeadDim / 8)) * 8;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        store16(&sh.keys[buf][(key + e) * kKeyPitch + (((d0 >> 3) ^ key_swizzle<kHeadDim>(key + e)) << 3)],
+                kreg[2 * c + e]);
+      }
       if (!with_values) continue;
-      const int slot = value_slot(key & (kFlashKeys - 1));
+      const int slot = value_slot(key & (kFlashKeys - 1));  // even; key + 1 takes slot + 1
       elem_t* vt = sh.values_t[buf][key / kFlashKeys];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int d = d0 + j;
-        const uint16_t bits = static_cast<uint16_t>(vreg[c].w[j >> 1] >> (16 * (j & 1)));
-        vt[d * kFlashKeys + ((((slot >> 3) ^ value_swizzle(d)) << 3) | (slot & 7))] = elem_t{bits};
+        const uint32_t lo = (vreg[2 * c].w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+        const uint32_t hi = (vreg[2 * c + 1].w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(&vt[d * kFlashKeys + ((((slot >> 3) ^ value_swizzle(d)) << 3) | (slot & 7))]) =
+            lo | (hi << 16);
       }
     }
   };
-  // Scores of this wave's tile of a staged step in base-2 units
-  // (scale * log2(e) * q . k), transposed: s[rf][kf][v] is row 16rf + col
-  // against key 16kf + 4grp + v of tile `tile`; keys past a row's position
-  // are -inf.
+  // Scores q . k of this wave's tile of a staged step, transposed:
+  // s[rf][kf][v] is row 16rf + col against key 16kf + 4grp + v of tile
+  // `tile`; keys past a row's position are -inf. The scale (in base-2 units,
+  // scale * log2(e)) is applied inside the exponentials, as one fma with the
+  // row max: exp2(c s - c m).
   auto scores = [&](int buf, int tile, mfma_acc4 (&s)[kRF][4]) {
     const elem_t* kb = &sh.keys[buf][kg * kFlashKeys * kKeyPitch];
 #pragma unroll
@@ -973,14 +997,6 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
             kb + (kf * 16 + col) * kKeyPitch + (((ks * 4 + grp) ^ key_swizzle<kHeadDim>(col)) << 3));
 #pragma unroll
         for (int rf = 0; rf < kRF; ++rf) s[rf][kf] = mfma16x16x32(a, qf[rf][ks], s[rf][kf]);
-      }
-    }
-#pragma unroll
-    for (int rf = 0; rf < kRF; ++rf) {
-#pragma unroll
-      for (int kf = 0; kf < 4; ++kf) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) s[rf][kf][v] *= scale_log2e;
       }
     }
     const int key0 = tile * kFlashKeys;
@@ -1032,14 +1048,15 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
         // tiles can be fully masked for the early rows) its max is -inf; the
         // exponentials are then taken against 0, all of them are 0, and l
         // stays 0.
-        const float base = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
+        const float neg_base = m_new == -__builtin_huge_valf() ? 0.0f : -m_new * scale_log2e;
         float sum = 0.0f;
 #pragma unroll
         for (int kf = 0; kf < 4; ++kf) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) sum += __builtin_amdgcn_exp2f(s[rf][kf][v] - base);
+          for (int v = 0; v < 4; ++v) sum += __builtin_amdgcn_exp2f(__builtin_fmaf(s[rf][kf][v], scale_log2e, neg_base));
         }
-        l[rf] = m[rf] == m_new ? l[rf] + sum : __builtin_fmaf(l[rf], __builtin_amdgcn_exp2f(m[rf] - base), sum);
+        l[rf] = m[rf] == m_new ? l[rf] + sum
+                               : __builtin_fmaf(l[rf], __builtin_amdgcn_exp2f(__builtin_fmaf(m[rf], scale_log2e, neg_base)), sum);
         m[rf] = m_new;
       }
     }
@@ -1068,8 +1085,9 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
     const float m0 = sh.stats[h][rf * 16 + col][0], l0 = sh.stats[h][rf * 16 + col][1];
     const float m1 = sh.stats[h + 4][rf * 16 + col][0], l1 = sh.stats[h + 4][rf * 16 + col][1];
     const float M = fmaxf(m0, m1);
-    const float L = __builtin_fmaf(l1, __builtin_amdgcn_exp2f(m1 - M), l0 * __builtin_amdgcn_exp2f(m0 - M));
-    m[rf] = M;
+    const float L = __builtin_fmaf(l1, __builtin_amdgcn_exp2f((m1 - M) * scale_log2e),
+                                   l0 * __builtin_amdgcn_exp2f((m0 - M) * scale_log2e));
+    m[rf] = -M * scale_log2e;  // pass 2 takes exp2(c s - c M) as one fma
     inv[rf] = 1.0f / L;
   }
 
@@ -1100,7 +1118,9 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(
         for (int kf = 0; kf < 4; ++kf) {
           float pr[4];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) pr[v] = __builtin_amdgcn_exp2f(s[rf][kf][v] - m[rf]) * inv[rf];
+          for (int v = 0; v < 4; ++v) {
+            pr[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rf][kf][v], scale_log2e, m[rf])) * inv[rf];
+          }
           pk[kf][0] = pack_rounded(pr[0], pr[1]);
           pk[kf][1] = pack_rounded(pr[2], pr[3]);
         }
@@ -1224,7 +1244,8 @@ void launch_flash(elem_t* o, const elem_t* q, const KvCacheView& v, int num_head
   const unsigned zs = static_cast<unsigned>((group + 3) / 4);
   // One row fragment (16 positions) per wave: more, lighter blocks (two per
   // compute unit) measured faster than two fragments per wave at every T.
-  const dim3 grid(static_cast<unsigned>((tokens + 15) / 16), static_cast<unsigned>(v.num_kv_heads), zs);
+  const int units = (tokens + 15) / 16 * v.num_kv_heads;
+  const dim3 grid(static_cast<unsigned>((units + 7) / 8 * 8), 1u, zs);
   flash_prefill_kernel<kPaged, kHeadDim, 1><<<grid, kFlashThreads, 0, s>>>(o, q, v, num_heads, group, tokens,
                                                                           start_position, scale_log2e);
 }

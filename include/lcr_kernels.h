@@ -165,6 +165,17 @@ size_t lcr_gemm_workspace_bytes(int T, int N, int K);
 int lcr_gemm_swiglu_ws(void* act, const void* X, const void* W_gate_up, int T, int ffn, int K,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* A projection followed by the residual join and RMSNorm that always follows
+ * it: o_proj (src/model.cu:420-427) or the MLP down projection and the next
+ * layer's input norm (src/model.cu:441-458), i.e. lcr_gemm_ws into delta
+ * [T][N] and lcr_add_residual_rmsnorm(out, x, delta, weight) (src/kernels.cuh:39),
+ * bit-identical to that pair. When the plan splits K, the norm's row pass
+ * sums the slices itself and delta is left unwritten; otherwise delta holds
+ * the projection. Workspace as for lcr_gemm_ws. */
+int lcr_gemm_residual_rmsnorm_ws(void* out, void* x, void* delta, const void* X, const void* W,
+                                 const void* weight, int T, int N, int K, float eps, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* table[p * (head_dim / 2) + i] = (cos a, sin a) for a = float(p) * inv_freq[i]
  * and p < positions: the per-position angles lcr_rope_q and lcr_rope_write_kv
  * evaluate (src/kernels/rope.cu:33-87), the same values, tabulated once. The

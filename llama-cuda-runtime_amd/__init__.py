@@ -149,6 +149,7 @@ SIGNATURES = {
     "lcr_gemm_ws": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, ctypes.c_size_t, _P]),
     "lcr_gemm_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I]),
     "lcr_gemm_swiglu_ws": (_I, [_P, _P, _P, _I, _I, _I, _P, ctypes.c_size_t, _P]),
+    "lcr_gemm_residual_rmsnorm_ws": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, ctypes.c_size_t, _P]),
     "lcr_rope_table": (_I, [_P, _P, _I, _I, _P]),
     "lcr_gemm_qkv_rope_ws": (_I, [_P, ctypes.POINTER(KvView), _P, _P, _P, _I, _I, _I, _I, _I, _P,
                                   ctypes.c_size_t, _P]),

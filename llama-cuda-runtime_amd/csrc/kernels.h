@@ -129,6 +129,13 @@ inline void launch_gemm_swiglu(elem_t* act, const elem_t* X, const elem_t* W_gat
   check_kernel_status(lcr_gemm_swiglu_ws(act, X, W_gate_up, T, ffn, K, workspace, workspace_bytes, stream));
 }
 
+inline void launch_gemm_residual_rmsnorm(elem_t* out, elem_t* x, elem_t* delta, const elem_t* X, const elem_t* W,
+                                         const elem_t* weight, int T, int N, int K, float eps, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream) {
+  check_kernel_status(
+      lcr_gemm_residual_rmsnorm_ws(out, x, delta, X, W, weight, T, N, K, eps, workspace, workspace_bytes, stream));
+}
+
 inline void launch_gemm_qkv_rope(elem_t* q_heads, const KvCacheView& view, const elem_t* X, const elem_t* W_qkv,
                                  const float2* rope_table, int T, int num_heads, int K, int start_position,
                                  bool paged, void* workspace, size_t workspace_bytes, hipStream_t stream) {

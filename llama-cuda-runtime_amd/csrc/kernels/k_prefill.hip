@@ -34,6 +34,7 @@
 #include "../capi_util.h"
 #include "../kv_cache.h"
 #include "device_common.h"
+#include "row_norm.h"
 
 namespace lcr {
 namespace {
@@ -675,6 +676,43 @@ __global__ __launch_bounds__(256) void gemm_reduce_rope_kernel(const float* __re
   emit_rope_quad<kPaged>(r, T, t, h * head_dim, 4 * q, head_dim, l, hh);
 }
 
+// The residual add and RMSNorm that follow a projection (x += Y, out =
+// RMSNorm(x) * weight) on a split launch: one 256-thread block per token row
+// sums each chunk's slices in slice order and rounds it to the element type,
+// as the reduction's output, then runs the norm row on it: bit for bit the
+// reduction followed by the residual RMSNorm kernel.
+struct GemmNorm {
+  elem_t* out;
+  elem_t* x;
+  const elem_t* weight;
+  float eps;
+};
+
+template <int kChunks>
+__global__ __launch_bounds__(kNormThreads) void gemm_reduce_norm_kernel(const float* __restrict__ partial, int splits,
+                                                                        int T, int dim, GemmNorm n) {
+  __shared__ float scratch[9];
+  const size_t base = static_cast<size_t>(blockIdx.x) * dim;
+  const size_t count = static_cast<size_t>(T) * dim;
+  norm_row_vec<true, kChunks>(
+      n.out + base, n.x + base, n.weight, dim, n.eps,
+      [&](int c, float* df) {
+        const float* p = partial + base + 8 * c;
+        float4 a = *reinterpret_cast<const float4*>(p);
+        float4 b = *reinterpret_cast<const float4*>(p + 4);
+        for (int sl = 1; sl < splits; ++sl) {
+          const float4 sa = *reinterpret_cast<const float4*>(p + static_cast<size_t>(sl) * count);
+          const float4 sb = *reinterpret_cast<const float4*>(p + static_cast<size_t>(sl) * count + 4);
+          a.x += sa.x; a.y += sa.y; a.z += sa.z; a.w += sa.w;
+          b.x += sb.x; b.y += sb.y; b.z += sb.z; b.w += sb.w;
+        }
+        df[0] = round_to_elem(a.x); df[1] = round_to_elem(a.y); df[2] = round_to_elem(a.z);
+        df[3] = round_to_elem(a.w); df[4] = round_to_elem(b.x); df[5] = round_to_elem(b.y);
+        df[6] = round_to_elem(b.z); df[7] = round_to_elem(b.w);
+      },
+      scratch);
+}
+
 // Y = sum over slices of the fp32 partial products, in slice order.
 template <bool kFp32Out>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(void* __restrict__ Y, const float* __restrict__ partial,
@@ -793,8 +831,11 @@ void launch_gemm_ring(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, 
   }
 }
 
-void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K, void* workspace,
-              size_t workspace_bytes, int ffn, hipStream_t s, const GemmRope* rope = nullptr) {
+// Returns whether the residual RMSNorm `norm` was applied (a split plan whose
+// rows the fused reduction covers); otherwise Y holds the projection.
+bool run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K, void* workspace,
+              size_t workspace_bytes, int ffn, hipStream_t s, const GemmRope* rope = nullptr,
+              const GemmNorm* norm = nullptr) {
   const bool wide_waves = rope != nullptr && rope->view.head_dim == 128;
   const GemmPlan plan =
       plan_gemm(T, N, K, device_compute_units(), workspace != nullptr ? workspace_bytes : 0, wide_waves);
@@ -818,6 +859,20 @@ void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
       launch_gemm_tiles<128, 128, 2, 2>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
   }
+  const int norm_chunks = (N / 8 + kNormThreads - 1) / kNormThreads;
+  if (plan.splits > 1 && norm != nullptr && N % 8 == 0 && norm_chunks <= 4 &&
+      ((reinterpret_cast<uintptr_t>(norm->out) | reinterpret_cast<uintptr_t>(norm->x) |
+        reinterpret_cast<uintptr_t>(norm->weight)) & 15u) == 0) {
+    const unsigned rows = static_cast<unsigned>(T);
+    if (norm_chunks == 1) {
+      gemm_reduce_norm_kernel<1><<<rows, kNormThreads, 0, s>>>(grid.partial, plan.splits, T, N, *norm);
+    } else if (norm_chunks == 2) {
+      gemm_reduce_norm_kernel<2><<<rows, kNormThreads, 0, s>>>(grid.partial, plan.splits, T, N, *norm);
+    } else {
+      gemm_reduce_norm_kernel<4><<<rows, kNormThreads, 0, s>>>(grid.partial, plan.splits, T, N, *norm);
+    }
+    return true;
+  }
   if (plan.splits > 1 && rope != nullptr) {
     const size_t threads = static_cast<size_t>(T) * (N / rope->view.head_dim) * (rope->view.head_dim / 8);
     const unsigned blocks = static_cast<unsigned>((threads + 255) / 256);
@@ -839,6 +894,7 @@ void run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
       gemm_reduce_kernel<false><<<blocks, 256, 0, s>>>(Y, grid.partial, plan.splits, count);
     }
   }
+  return false;
 }
 
 // ---------------------------------------------------------------------------
@@ -881,7 +937,7 @@ struct FlashShared {
 };
 
 template <bool kPaged, int kHeadDim, int kRF>
-__global__ __launch_bounds__(kFlashThreads, 4) void flash_prefill_kernel(
+__global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_prefill_kernel(
     elem_t* __restrict__ out, const elem_t* __restrict__ q_heads, KvCacheView view, int num_heads,
     int group, int tokens, int start_position, float scale_log2e) {
   constexpr int kRows = 16 * kRF;                         // query positions per block
@@ -1307,6 +1363,24 @@ extern "C" int lcr_gemm_swiglu_ws(void* act, const void* X, const void* W_gate_u
            workspace, workspace_bytes, ffn, static_cast<hipStream_t>(stream));
   CAPI_LAUNCHED();
   return LCR_OK;
+}
+
+extern "C" int lcr_gemm_residual_rmsnorm_ws(void* out, void* x, void* delta, const void* X, const void* W,
+                                            const void* weight, int T, int N, int K, float eps, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  const int status = gemm_checks(delta, X, W, T, N, K);
+  if (status != LCR_OK || T == 0 || N == 0) return status;
+  CAPI_CHECK(out != nullptr && x != nullptr && weight != nullptr,
+             "gemm_residual_rmsnorm needs the output, the residual and the norm weight");
+  CAPI_CHECK(workspace != nullptr || workspace_bytes == 0, "gemm workspace of " << workspace_bytes
+                                                                               << " bytes has no pointer");
+  CAPI_CHECK((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "gemm workspace must be 16-byte aligned");
+  const GemmNorm norm{static_cast<elem_t*>(out), static_cast<elem_t*>(x), static_cast<const elem_t*>(weight), eps};
+  const bool fused = run_gemm(delta, false, static_cast<const elem_t*>(X), static_cast<const elem_t*>(W), T, N, K,
+                              workspace, workspace_bytes, 0, static_cast<hipStream_t>(stream), nullptr, &norm);
+  CAPI_LAUNCHED();
+  if (fused) return LCR_OK;
+  return lcr_add_residual_rmsnorm(out, x, delta, weight, T, N, eps, stream);
 }
 
 extern "C" int lcr_gemm_qkv_rope_ws(void* q_heads, const lcr_kv_view* view, const void* X, const void* W_qkv,

@@ -68,11 +68,9 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(elem_t* __restric
   }
 }
 
-// The same arithmetic with 16-byte accesses and the row in registers, for rows
-// of dim = 8 * chunks elements with at most kChunks chunks per thread: thread t
-// holds chunks t, t + 256, ... (the order block_sum_squares walks), so the sum
-// of squares, the rounding of the residual and of the output are those of the
-// kernel above, bit for bit.
+// The same arithmetic with 16-byte accesses and the row in registers
+// (norm_row_vec), for rows of dim = 8 * chunks elements with at most kChunks
+// chunks per thread: bit for bit the kernel above.
 template <bool kResidual, int kChunks>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(elem_t* __restrict__ out,
                                                                    elem_t* __restrict__ x,
@@ -81,51 +79,9 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(elem_t* __res
                                                                    int dim, float eps) {
   __shared__ float scratch[9];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * dim;
-  const int chunks = dim / 8;
-  const int t = static_cast<int>(threadIdx.x);
-  float v[kChunks][8];
-  vec16 w[kChunks];
-  float s = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kChunks; ++k) {
-    const int c = t + k * kNormThreads;
-    if (c >= chunks) continue;
-    const vec16 xv = load16(x + base + 8 * c);
-    w[k] = load16(weight + 8 * c);
-    float xf[8];
-    unpack8(xv, xf);
-    if (kResidual) {
-      float df[8];
-      unpack8(load16(delta + base + 8 * c), df);
-      vec16 r;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[k][j] = xf[j] + df[j];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) r.w[j] = pack_elems(v[k][2 * j], v[k][2 * j + 1]);
-      store16(x + base + 8 * c, r);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[k][j] = xf[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s = __builtin_fmaf(v[k][j], v[k][j], s);
-  }
-  const float scale = norm_scale(block_norm_total(s, scratch), dim, eps);
-#pragma unroll
-  for (int k = 0; k < kChunks; ++k) {
-    const int c = t + k * kNormThreads;
-    if (c >= chunks) continue;
-    float wf[8];
-    unpack8(w[k], wf);
-    vec16 r;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float a = elem_bits_to_float(float_to_elem_bits(v[k][2 * j]));
-      const float b = elem_bits_to_float(float_to_elem_bits(v[k][2 * j + 1]));
-      r.w[j] = pack_elems((a * scale) * wf[2 * j], (b * scale) * wf[2 * j + 1]);
-    }
-    store16(out + base + 8 * c, r);
-  }
+  norm_row_vec<kResidual, kChunks>(
+      out + base, x + base, weight, dim, eps,
+      [&](int c, float* df) { unpack8(load16(delta + base + 8 * c), df); }, scratch);
 }
 
 }  // namespace

@@ -67,4 +67,61 @@ __device__ __forceinline__ float norm_scale(float total, int dim, float eps) {
   return 1.0f / __builtin_sqrtf(total / static_cast<float>(dim) + eps);
 }
 
+// One row of RMSNorm (kResidual: of the residual add x += delta first) with
+// 16-byte accesses and the row in registers, for rows of dim = 8 * chunks
+// elements with at most kChunks chunks per thread: thread t holds chunks
+// t, t + 256, ... (the order block_sum_squares walks), so the sum of squares
+// and the roundings are those of block_sum_squares' element loop, bit for bit.
+// delta(c, df) writes the eight addends of chunk c to df[0..7].
+template <bool kResidual, int kChunks, typename Delta>
+__device__ __forceinline__ void norm_row_vec(elem_t* __restrict__ orow, elem_t* __restrict__ xrow,
+                                             const elem_t* __restrict__ weight, int dim, float eps,
+                                             Delta delta, float* scratch) {
+  const int chunks = dim / 8;
+  const int t = static_cast<int>(threadIdx.x);
+  float v[kChunks][8];
+  vec16 w[kChunks];
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const int c = t + k * kNormThreads;
+    if (c >= chunks) continue;
+    const vec16 xv = load16(xrow + 8 * c);
+    w[k] = load16(weight + 8 * c);
+    float xf[8];
+    unpack8(xv, xf);
+    if (kResidual) {
+      float df[8];
+      delta(c, df);
+      vec16 r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[k][j] = xf[j] + df[j];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.w[j] = pack_elems(v[k][2 * j], v[k][2 * j + 1]);
+      store16(xrow + 8 * c, r);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[k][j] = xf[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = __builtin_fmaf(v[k][j], v[k][j], s);
+  }
+  const float scale = norm_scale(block_norm_total(s, scratch), dim, eps);
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const int c = t + k * kNormThreads;
+    if (c >= chunks) continue;
+    float wf[8];
+    unpack8(w[k], wf);
+    vec16 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = elem_bits_to_float(float_to_elem_bits(v[k][2 * j]));
+      const float b = elem_bits_to_float(float_to_elem_bits(v[k][2 * j + 1]));
+      r.w[j] = pack_elems((a * scale) * wf[2 * j], (b * scale) * wf[2 * j + 1]);
+    }
+    store16(orow + 8 * c, r);
+  }
+}
+
 }  // namespace lcr

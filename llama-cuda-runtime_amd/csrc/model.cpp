@@ -609,16 +609,16 @@ void Model::run_layers(int tokens, int start_position) {
         attention_prefill(layer, tokens, start_position);
       }
     }
-    {
-      ProfileScope scope(&profiler_, "o_proj", stream_);
-      if (tokens == 1) {
+    if (tokens > 1) {
+      ProfileScope scope(&profiler_, "o_proj + residual+rmsnorm", stream_);
+      launch_gemm_residual_rmsnorm(normed_, x_, proj_out_, attn_out_, w.o_proj, w.post_attention_norm, tokens,
+                                   hidden, config_.q_dim(), config_.rms_norm_eps, gemm_workspace_,
+                                   gemm_workspace_size_, stream_);
+    } else {
+      {
+        ProfileScope scope(&profiler_, "o_proj", stream_);
         launch_gemv(proj_out_, false, w.o_proj, attn_out_, hidden, config_.q_dim(), stream_);
-      } else {
-        launch_gemm(proj_out_, false, attn_out_, w.o_proj, tokens, hidden, config_.q_dim(),
-                    gemm_workspace_, gemm_workspace_size_, stream_);
       }
-    }
-    {
       ProfileScope scope(&profiler_, "residual+rmsnorm", stream_);
       launch_add_residual_rmsnorm(normed_, x_, proj_out_, w.post_attention_norm, tokens, hidden,
                                   config_.rms_norm_eps, stream_);
@@ -643,21 +643,23 @@ void Model::run_layers(int tokens, int start_position) {
       }
     }
     {
-      ProfileScope scope(&profiler_, "down", stream_);
-      if (tokens == 1) {
-        launch_gemv(proj_out_, false, w.down_proj, act_, hidden, ffn, stream_);
-      } else {
-        launch_gemm(proj_out_, false, act_, w.down_proj, tokens, hidden, ffn, gemm_workspace_,
-                    gemm_workspace_size_, stream_);
-      }
-    }
-    {
+      // The MLP residual join fuses with the norm that comes next: the next
+      // layer's input norm, or the final norm after the last layer.
       const elem_t* next = (layer + 1 < config_.num_layers)
                                ? layers_[static_cast<size_t>(layer + 1)].input_norm
                                : final_norm_;
-      ProfileScope scope(&profiler_, "residual+rmsnorm", stream_);
-      launch_add_residual_rmsnorm(normed_, x_, proj_out_, next, tokens, hidden,
-                                  config_.rms_norm_eps, stream_);
+      if (tokens > 1) {
+        ProfileScope scope(&profiler_, "down + residual+rmsnorm", stream_);
+        launch_gemm_residual_rmsnorm(normed_, x_, proj_out_, act_, w.down_proj, next, tokens, hidden, ffn,
+                                     config_.rms_norm_eps, gemm_workspace_, gemm_workspace_size_, stream_);
+      } else {
+        {
+          ProfileScope scope(&profiler_, "down", stream_);
+          launch_gemv(proj_out_, false, w.down_proj, act_, hidden, ffn, stream_);
+        }
+        ProfileScope scope(&profiler_, "residual+rmsnorm", stream_);
+        launch_add_residual_rmsnorm(normed_, x_, proj_out_, next, tokens, hidden, config_.rms_norm_eps, stream_);
+      }
       input_norm_done_ = true;
     }
     if (capture_activations_) capture("layer_" + std::to_string(layer), x_, tokens, hidden);

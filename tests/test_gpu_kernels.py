@@ -442,6 +442,39 @@ def test_gemm_swiglu_matches_gemm_then_swiglu(gpu, T, F, K):
         expect_bits_equal(host(got), host(want), f"gemm+swiglu {T}x{F}x{K} workspace {wsb}")
 
 
+@pytest.mark.parametrize("T,N,K", [(2048, 2048, 2048), (2048, 2048, 8192), (512, 2048, 2048), (512, 2048, 8192),
+                                   (37, 2048, 8192), (130, 1004, 512), (64, 9000, 256)])
+def test_gemm_residual_rmsnorm_matches_unfused(gpu, T, N, K):
+    """The projection followed by the residual RMSNorm gives the bits of
+    lcr_gemm_ws into delta and lcr_add_residual_rmsnorm: for unsplit plans
+    (o_proj at 2048 tokens), for split plans whose reduction runs inside the
+    norm (down at 2048, both at 512, a ragged 37-token chunk), and for rows the
+    fused reduction does not take (N not a multiple of 8; N past 8192)."""
+    lib = gpu
+    r = rng(T + N + K)
+    Xd = dev(random_elems(r, (T, K)))
+    Wd = dev(random_elems(r, (N, K), 0.05))
+    x0 = random_elems(r, (T, N))
+    weight = dev(random_elems(r, (N,), 0.5))
+    ws_bytes = lib.lcr_gemm_workspace_bytes(T, N, K)
+    ws = zeros_dev(max(ws_bytes, 16) // 4, np.float32)
+    eps = 1e-5
+    for wsp, wsb in ((p(ws), ws_bytes), (None, 0)):
+        what = f"gemm+residual+rmsnorm {T}x{N}x{K} workspace {wsb}"
+        x_want, x_got = dev(x0), dev(x0)
+        delta = zeros_dev(T * N)
+        ok(lib, lib.lcr_gemm_ws(p(delta), 0, p(Xd), p(Wd), T, N, K, wsp, wsb, NULL), "gemm_ws")
+        want = zeros_dev(T * N)
+        ok(lib, lib.lcr_add_residual_rmsnorm(p(want), p(x_want), p(delta), p(weight), T, N, eps, NULL),
+           "add_residual_rmsnorm")
+        got = zeros_dev(T * N)
+        scratch = zeros_dev(T * N)
+        ok(lib, lib.lcr_gemm_residual_rmsnorm_ws(p(got), p(x_got), p(scratch), p(Xd), p(Wd), p(weight), T, N, K, eps,
+                                                 wsp, wsb, NULL), "gemm_residual_rmsnorm_ws")
+        expect_bits_equal(host(got), host(want), f"{what}: normed")
+        expect_bits_equal(host(x_got), host(x_want), f"{what}: residual")
+
+
 def test_rope_table_matches_oracle(gpu, orc):
     """lcr_rope_table holds the (cos, sin) the RoPE kernels evaluate per
     token: the oracle's sincos of float(p) * inv_freq[i], bit for bit."""

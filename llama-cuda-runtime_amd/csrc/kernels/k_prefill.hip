@@ -463,7 +463,6 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
 // deep. Loads the compiler does not count can only make its own in-order
 // count waits stricter.
 constexpr int kRingK = 32;
-constexpr int kRingW = 256;  // W rows per block tile (the stage's first rows; tokens follow)
 
 __device__ __forceinline__ void load_to_lds16(const elem_t* src, uint32_t lds_address) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_address) : "memory");
@@ -483,24 +482,27 @@ __device__ __forceinline__ void wait_stage_landed() {
   __builtin_amdgcn_s_waitcnt((kCount & 15) | ((kCount >> 4) << 14) | (7 << 4));
 }
 
-// Block tiles of 256 W rows x BT tokens:
-//  - BT = 256, kWaves = 8: wave tiles of 128 W rows x 64 tokens (two waves
+// Block tiles of BW W rows x BT tokens:
+//  - 256 x 256, kWaves = 8: wave tiles of 128 W rows x 64 tokens (two waves
 //    per SIMD);
-//  - BT = 256, kWaves = 4: wave tiles of 128 x 128 (one wave per SIMD, its
+//  - 256 x 256, kWaves = 4: wave tiles of 128 x 128 (one wave per SIMD, its
 //    256 fp32 accumulators in the accumulation registers);
-//  - BT = 128, kWaves = 8: wave tiles of 64 x 64, for token counts whose
-//    256-token tiles would leave compute units idle.
-template <int kStages, int kWaves, int BT, bool kFp32Out>
+//  - 256 x 128, kWaves = 8: wave tiles of 64 x 64, for token counts whose
+//    256-token tiles would leave compute units idle;
+//  - 128 x 128, kWaves = 8: wave tiles of 64 x 32, for projections whose
+//    larger tiles would leave compute units idle (two blocks fit a CU).
+template <int kStages, int kWaves, int BW, int BT, bool kFp32Out>
 __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict__ Y, const elem_t* __restrict__ X,
                                                                 const elem_t* __restrict__ W, int T, int N, int K,
                                                                 GemmGrid grid) {
-  static_assert((BT == 256 && (kWaves == 4 || kWaves == 8)) || (BT == 128 && kWaves == 8),
-                "supported ring tiles: 256 x 256 on 4 or 8 waves, 256 x 128 on 8 waves");
-  constexpr int kWavesW = BT == 256 ? 2 : 4;  // waves along W; the rest split the tokens
+  static_assert((BW == 256 && BT == 256 && (kWaves == 4 || kWaves == 8)) ||
+                    (BW == 256 && BT == 128 && kWaves == 8) || (BW == 128 && BT == 128 && kWaves == 8),
+                "supported ring tiles: 256 x 256 on 4 or 8 waves, 256 x 128 and 128 x 128 on 8 waves");
+  constexpr int kWavesW = (BW == 128 || BT == 256) ? 2 : 4;  // waves along W; the rest split the tokens
   constexpr int kWavesT = kWaves / kWavesW;
-  constexpr int FW = kRingW / kWavesW / 16;  // W fragments of 16 rows per wave
+  constexpr int FW = BW / kWavesW / 16;  // W fragments of 16 rows per wave
   constexpr int FT = BT / kWavesT / 16;      // token fragments of 16 tokens per wave
-  constexpr int kRows = kRingW + BT;
+  constexpr int kRows = BW + BT;
   constexpr int kStageElems = kRows * kRingK;
   constexpr int kLoads = kRows / 16 / kWaves;  // 1 KB loads (16 rows) per wave per stage
   static_assert(kLoads * 16 * kWaves == kRows, "stage rows split evenly over the waves");
@@ -508,7 +510,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   __shared__ __attribute__((aligned(1024))) elem_t ring[kStages * kStageElems];
 
   GemmWork work;
-  if (!gemm_work(grid, kRingW, BT, K, work)) return;
+  if (!gemm_work(grid, BW, BT, K, work)) return;
   const int w0 = work.w0, t0 = work.t0;
 
   const int lane = lane_id();
@@ -525,8 +527,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   for (int i = 0; i < kLoads; ++i) {
     const int row = 16 * (kWaves * i + wave) + (lane >> 2);
     const int chunk = (lane & 3) ^ ((row >> 1) & 3);
-    src[i] = (row < kRingW ? W + static_cast<size_t>(weight_row(min(w0 + row, N - 1), grid.ffn)) * K
-                           : X + static_cast<size_t>(min(t0 + row - kRingW, T - 1)) * K) + work.k_first + 8 * chunk;
+    src[i] = (row < BW ? W + static_cast<size_t>(weight_row(min(w0 + row, N - 1), grid.ffn)) * K
+                           : X + static_cast<size_t>(min(t0 + row - BW, T - 1)) * K) + work.k_first + 8 * chunk;
   }
   const uint32_t ring_base = lds_address_of(ring) + static_cast<uint32_t>(wave * 16 * kRingK * 2);
   auto issue = [&](int s) {
@@ -555,7 +557,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   auto read_tokens = [&](int s, mfma_in8 (&bt)[FT]) {
     const elem_t* base = ring + (s % kStages) * kStageElems;
 #pragma unroll
-    for (int j = 0; j < FT; ++j) bt[j] = lds_operand(base + (kRingW + wt + 16 * j + col) * kRingK + swz);
+    for (int j = 0; j < FT; ++j) bt[j] = lds_operand(base + (BW + wt + 16 * j + col) * kRingK + swz);
   };
   // Products of the stage whose fragments are in aw / bt, reading stage
   // `next` into aw / bt_next. After the last stage `next` repeats a stage
@@ -614,6 +616,11 @@ constexpr int kRingStages = 4;
 // (measured on MI355X; the plan compares it with the other shapes').
 constexpr double kRing256x128Efficiency = 0.30;
 constexpr int kRing256x128Stages = 4;
+// The 128 x 128 ring tile: o_proj at 2048 tokens (one tile per compute unit)
+// takes 24.2 us, 0.28 of a compute unit's peak, against 34-36 us for the
+// register-staged 128 x 128 kernel.
+constexpr double kRing128x128Efficiency = 0.28;
+constexpr int kRing128x128Stages = 4;
 // Waves per ring block. Eight (two per SIMD) measured faster than four with
 // 128 x 128 wave tiles: 143 against 176 us for T = 2048, N = 16384, K = 2048;
 // one wave per SIMD leaves the LDS and barrier latencies uncovered.
@@ -749,7 +756,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(void* __restrict__ Y, 
   }
 }
 
-enum class GemmShape { kRing256x256, kRing256x128, k256x256, k256x128, k128x128 };
+enum class GemmShape { kRing256x256, kRing256x128, kRing128x128, k256x256, k256x128, k128x128 };
 
 struct GemmPlan {
   GemmShape shape;
@@ -778,7 +785,8 @@ GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wi
       {ring ? GemmShape::kRing256x256 : GemmShape::k256x256, 256, 256, ring ? kRingK : kStageK, ring ? 0.37 : 0.31},
       {ring ? GemmShape::kRing256x128 : GemmShape::k256x128, 256, 128, ring ? kRingK : kStageK,
        ring ? kRing256x128Efficiency : 0.23},
-      {GemmShape::k128x128, 128, 128, kStageK, 0.20}};
+      {ring ? GemmShape::kRing128x128 : GemmShape::k128x128, 128, 128, ring ? kRingK : kStageK,
+       ring ? kRing128x128Efficiency : 0.20}};
   constexpr double kCuPeak = 9.8e12;     // bf16 dense flop/s per compute unit
   constexpr double kBandwidth = 5.0e12;  // sustained bytes/s for the partials' round trip
   constexpr double kLaunch = 4e-6;
@@ -819,15 +827,15 @@ void launch_gemm_tiles(void* Y, bool fp32_out, const elem_t* X, const elem_t* W,
   }
 }
 
-template <int BT, int kWaves, int kStages>
+template <int BW, int BT, int kWaves, int kStages>
 void launch_gemm_ring(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K,
                       const GemmGrid& grid, hipStream_t s) {
   const int units = grid.tiles_t * grid.tiles_w * grid.splits;
   const unsigned blocks = static_cast<unsigned>(((units + 7) / 8) * 8);
   if (fp32_out) {
-    gemm_ring_kernel<kStages, kWaves, BT, true><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
+    gemm_ring_kernel<kStages, kWaves, BW, BT, true><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
   } else {
-    gemm_ring_kernel<kStages, kWaves, BT, false><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
+    gemm_ring_kernel<kStages, kWaves, BW, BT, false><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
   }
 }
 
@@ -844,10 +852,13 @@ bool run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
                 rope != nullptr ? *rope : GemmRope{}};
   switch (plan.shape) {
     case GemmShape::kRing256x256:
-      launch_gemm_ring<256, kRingWaves, kRingStages>(Y, fp32_out, X, W, T, N, K, grid, s);
+      launch_gemm_ring<256, 256, kRingWaves, kRingStages>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
     case GemmShape::kRing256x128:
-      launch_gemm_ring<128, 8, kRing256x128Stages>(Y, fp32_out, X, W, T, N, K, grid, s);
+      launch_gemm_ring<256, 128, 8, kRing256x128Stages>(Y, fp32_out, X, W, T, N, K, grid, s);
+      break;
+    case GemmShape::kRing128x128:
+      launch_gemm_ring<128, 128, 8, kRing128x128Stages>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
     case GemmShape::k256x256:
       launch_gemm_tiles<256, 256, 2, 4>(Y, fp32_out, X, W, T, N, K, grid, s);

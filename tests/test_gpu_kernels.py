@@ -373,6 +373,9 @@ GEMM_CASES = [
     (1000, 16384, 2048), (512, 65536, 64), (512, 65536, 32), (1024, 16384, 520),
     # 256 x 128 ring tiles (a few hundred tokens): whole, ragged tokens, split K
     (512, 16384, 2048), (520, 3072, 2048), (384, 2048, 8192),
+    # 128 x 128 ring tiles: o_proj at 2048 tokens (one tile per compute unit),
+    # ragged tokens and rows, and a split K
+    (2048, 2048, 2048), (1500, 1000, 1024), (512, 3072, 2048),
 ]
 
 

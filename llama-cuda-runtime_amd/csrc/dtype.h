@@ -49,11 +49,12 @@ __host__ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
-// The f32 -> f16 rounding is written with integer operations, as the bf16
-// one is. With the hardware conversion the compiler merges a multiply and the
-// following rounding into one mixed-precision fma with a +0 addend, which
-// turns a -0 product into +0; here every product is rounded to f32 first and
-// the conversion cannot be merged, so device, host and oracle agree.
+// The f32 -> f16 rounding is written with integer operations for the host,
+// as the bf16 one is; device code issues the hardware conversion as its own
+// instruction (below), which rounds every f32 input the same way. Left to
+// the compiler, a plain conversion would be merged with the multiply before
+// it into one mixed-precision fma with a +0 addend, which rounds the exact
+// product once and turns a -0 product into +0.
 // Widening f16 -> f32 is exact, so device code uses the hardware conversion
 // (which the compiler may merge into a mixed-precision fma, also exact): the
 // same value as the integer form below for every input but a signalling NaN,
@@ -74,6 +75,16 @@ __host__ __device__ __forceinline__ float half_bits_to_float(uint32_t b) {
 }
 
 __host__ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // v_cvt_f16_f32 gives the integer form's result below for every f32 input
+  // (an exhaustive comparison of all 2^32 inputs on gfx950, NaN payloads
+  // included). Inline assembly keeps the compiler from folding a preceding
+  // multiply into a mixed-precision fma, which would round the exact product
+  // once and turn -0 into +0.
+  uint32_t hw;
+  asm("v_cvt_f16_f32 %0, %1" : "=v"(hw) : "v"(f));
+  return static_cast<uint16_t>(hw & 0xffffu);
+#endif
   const uint32_t u = f32_as_u32(f);
   const uint32_t sign = (u >> 16) & 0x8000u;
   const uint32_t a = u & 0x7fffffffu;

@@ -62,8 +62,16 @@ __device__ __forceinline__ float elem_hi(uint32_t p) {
 #endif
 }
 __device__ __forceinline__ uint32_t pack_elems(float lo, float hi) {
+#if defined(LCR_ELEM_FP16)
   return static_cast<uint32_t>(float_to_elem_bits(lo)) |
          (static_cast<uint32_t>(float_to_elem_bits(hi)) << 16);
+#else
+  // one v_cvt_pk_bf16_f32 for the pair: per element the rounding of
+  // float_to_elem_bits
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+#endif
 }
 
 // Half-split RoPE of one pair by the angle's (cos, sin): (lo c - hi s,

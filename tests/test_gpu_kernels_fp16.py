@@ -153,6 +153,60 @@ def test_gemm_fp16(gpu, lcr, T, N, K):
     expect_bits_equal(host(fused), host(want), "fp16 gemm+swiglu")
 
 
+@pytest.mark.parametrize("T,K,paged", [(512, 2048, True), (2048, 2048, False)])
+def test_fused_prefill_entries_fp16(gpu, lcr, T, K, paged):
+    """The fp16 build's fused prefill entries against their unfused pairs, bit
+    for bit: the q/k/v projection with RoPE and the KV append (split at 512
+    tokens, rotated in the reduction; unsplit at 2048, rotated in the
+    epilogue), and o_proj / down with the residual RMSNorm (split and
+    unsplit). These epilogues round to fp16 with the hardware conversion."""
+    from test_gpu_kernels import Cache, rope_table
+    lib = lcr.load_library("fp16")
+    r = rng(T + K + int(paged))
+    nh, kv, hd, start = 32, 8, 64, 3
+    N = (nh + 2 * kv) * hd
+    Xd = dev(random_elems(r, (T, K), kind=FP16))
+    Wd = dev(random_elems(r, (N, K), 0.05, kind=FP16))
+    freq = dev(rope_table(hd))
+    table = zeros_dev((start + T) * hd, np.float32)
+    ok(lib, lib.lcr_rope_table(p(table), p(freq), start + T, hd, None), "rope_table fp16")
+    ws_bytes = max(lib.lcr_gemm_workspace_bytes(T, N, K), lib.lcr_gemm_workspace_bytes(T, 2048, 8192))
+    ws = zeros_dev(max(ws_bytes, 16) // 4, np.float32)
+    max_seq = -(-(start + T) // 16) * 16
+    pages = r.permutation(max_seq // 16) if paged else None
+    want_cache, got_cache = Cache(kv, hd, max_seq, paged, 16, pages), Cache(kv, hd, max_seq, paged, 16, pages)
+    qkv = zeros_dev(T * N)
+    ok(lib, lib.lcr_gemm_ws(p(qkv), 0, p(Xd), p(Wd), T, N, K, p(ws), ws_bytes, None), "gemm_ws fp16")
+    q_want, q_got = zeros_dev(nh * T * hd), zeros_dev(nh * T * hd)
+    ok(lib, lib.lcr_rope_q(p(q_want), p(qkv), p(freq), T, start, nh, hd, N, None), "rope_q fp16")
+    vw, vg = want_cache.view(lcr), got_cache.view(lcr)
+    ok(lib, lib.lcr_rope_write_kv(ctypes.byref(vw), ctypes.c_void_p(qkv.ptr + 2 * nh * hd),
+                                  ctypes.c_void_p(qkv.ptr + 2 * (nh + kv) * hd), p(freq), T, start,
+                                  1 if paged else 0, N, None), "rope_write_kv fp16")
+    ok(lib, lib.lcr_gemm_qkv_rope_ws(p(q_got), ctypes.byref(vg), p(Xd), p(Wd), p(table), T, nh, K, start,
+                                     1 if paged else 0, p(ws), ws_bytes, None), "gemm_qkv_rope fp16")
+    expect_bits_equal(host(q_got), host(q_want), "fp16 qkv+rope: queries")
+    expect_bits_equal(host(got_cache.keys), host(want_cache.keys), "fp16 qkv+rope: keys")
+    expect_bits_equal(host(got_cache.values), host(want_cache.values), "fp16 qkv+rope: values")
+    for n_out, k_in in ((2048, 2048), (2048, 8192)):
+        A = dev(random_elems(r, (T, k_in), kind=FP16))
+        Wo = dev(random_elems(r, (n_out, k_in), 0.05, kind=FP16))
+        w = dev(random_elems(r, (n_out,), 0.5, kind=FP16))
+        x0 = random_elems(r, (T, n_out), kind=FP16)
+        x_want, x_got = dev(x0), dev(x0)
+        delta = zeros_dev(T * n_out)
+        ok(lib, lib.lcr_gemm_ws(p(delta), 0, p(A), p(Wo), T, n_out, k_in, p(ws), ws_bytes, None), "gemm_ws fp16")
+        want = zeros_dev(T * n_out)
+        ok(lib, lib.lcr_add_residual_rmsnorm(p(want), p(x_want), p(delta), p(w), T, n_out, 1e-5, None),
+           "add_residual_rmsnorm fp16")
+        got = zeros_dev(T * n_out)
+        ok(lib, lib.lcr_gemm_residual_rmsnorm_ws(p(got), p(x_got), p(zeros_dev(T * n_out)), p(A), p(Wo), p(w), T,
+                                                 n_out, k_in, 1e-5, p(ws), ws_bytes, None),
+           "gemm_residual_rmsnorm fp16")
+        expect_bits_equal(host(got), host(want), f"fp16 {n_out}x{k_in} residual norm")
+        expect_bits_equal(host(x_got), host(x_want), f"fp16 {n_out}x{k_in} residual")
+
+
 def test_small_model_fp16_mfma_prefill(gpu, lcr, tmp_path):
     """The fp16 build's MFMA prefill (GEMMs, fused SwiGLU, two-pass attention)
     against the oracle's fp16 chunked prefill: logits within 2e-2 of the

@@ -693,6 +693,26 @@ def test_argument_errors(gpu, lcr):
     assert b"empty vocabulary" in lib.lcr_last_error_message()
     assert lib.lcr_sample(None, None, 10, 1.0, 0, 1.5, 0.1, None, NULL) == -1
     assert b"top_p must be in (0, 1]" in lib.lcr_last_error_message()
+    # the fused prefill entries check their arguments before any launch
+    v.head_dim = 96
+    assert lib.lcr_gemm_qkv_rope_ws(None, ctypes.byref(v), None, None, None, 16, 32, 2048, 0, 0, None, 0,
+                                    NULL) == -1
+    assert b"head_dim 64 or 128" in lib.lcr_last_error_message()
+    assert lib.lcr_gemm_qkv_rope_ws(None, None, None, None, None, 16, 32, 2048, 0, 0, None, 0, NULL) == -1
+    assert b"cache view" in lib.lcr_last_error_message()
+    v.head_dim = 64
+    assert lib.lcr_gemm_qkv_rope_ws(None, ctypes.byref(v), None, None, None, 16, 32, 2048, 0, 0, None, 0,
+                                    NULL) == -1
+    assert b"RoPE table" in lib.lcr_last_error_message()
+    assert lib.lcr_gemm_residual_rmsnorm_ws(None, None, None, None, None, None, 16, 2048, 2048, 1e-5, None, 0,
+                                            NULL) == -1
+    assert b"the output, the residual and the norm weight" in lib.lcr_last_error_message()
+    assert lib.lcr_rope_table(None, None, 16, 63, NULL) == -1
+    assert b"even" in lib.lcr_last_error_message()
     # empty inputs return early and succeed
     assert lib.lcr_rmsnorm(None, None, None, 0, 2048, 1e-5, NULL) == 0
     assert lib.lcr_embedding_lookup(None, None, None, 0, 2048, NULL) == 0
+    assert lib.lcr_gemm_qkv_rope_ws(None, ctypes.byref(v), None, None, None, 0, 32, 2048, 0, 0, None, 0, NULL) == 0
+    assert lib.lcr_gemm_residual_rmsnorm_ws(None, None, None, None, None, None, 0, 2048, 2048, 1e-5, None, 0,
+                                            NULL) == 0
+    assert lib.lcr_rope_table(None, None, 0, 64, NULL) == 0

@@ -53,6 +53,8 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
 // Loads per thread in flight in the passes over the logits (element i of a
 // batch is base + i * kSampleThreads, so each thread keeps its order).
 constexpr int kSampleBatch = 8;
+// Loads in flight per thread of the sum blocks (one wave per compute unit).
+constexpr int kSumBatch = 32;
 constexpr int kSampleWaves = kSampleThreads / 64;
 
 __device__ __forceinline__ int wave_sum_int(int v) {
@@ -61,13 +63,78 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   return v;
 }
 
+// The maximum logit from the argmax blocks' partial keys (exact in any
+// order): the value half of the largest key. Every lane of the wave gets it.
+__device__ __forceinline__ float max_from_keys(const unsigned long long* __restrict__ block_best, int blocks) {
+  unsigned long long key = 0;
+  for (int b = lane_id(); b < blocks; b += 64) key = umax64(key, block_best[b]);
+  key = wave_max_u64(key);
+  const uint32_t k = static_cast<uint32_t>(key >> 32);
+  return u32_as_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Step 2 over many compute units: block b (one wave) runs threads
+// 64 b .. 64 b + 63 of the 1024-thread order, each adding exp(scaled_i) for
+// i = t, t + 1024, ... in order, exactly as one 1024-thread block would; the
+// thread's partial sum goes to partial_sums[t] and the block's histogram of
+// bins to block_hist[b][bin] (counts, so their order of addition is free).
+constexpr int kSumBlocks = kSampleThreads / 64;
+
+__global__ __launch_bounds__(64) void sample_sum_kernel(float* __restrict__ partial_sums, int* __restrict__ block_hist,
+                                                        const unsigned long long* __restrict__ block_best,
+                                                        int best_blocks, const float* __restrict__ logits,
+                                                        int vocab, float inv_temperature) {
+  __shared__ int hist[kHistogramBins];
+  const int lane = lane_id();
+  const int t = static_cast<int>(blockIdx.x) * 64 + lane;
+  const float max_logit = max_from_keys(block_best, best_blocks);
+  for (int b = lane; b < kHistogramBins; b += 64) hist[b] = 0;
+  __syncthreads();
+  float local_sum = 0.0f;
+  int last_bin = 0;
+  for (int base = t; base < vocab; base += kSumBatch * kSampleThreads) {
+    float v[kSumBatch];
+#pragma unroll
+    for (int k = 0; k < kSumBatch; ++k) {
+      const int i = base + k * kSampleThreads;
+      v[k] = i < vocab ? logits[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kSumBatch; ++k) {
+      if (base + k * kSampleThreads < vocab) {
+        const float scaled = (v[k] - max_logit) * inv_temperature;
+        local_sum += lcr_expf(scaled);
+        const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
+        if (bin == kHistogramBins - 1) {
+          ++last_bin;
+        } else if (bin >= 0) {
+          atomicAdd(&hist[bin], 1);
+        }
+      }
+    }
+  }
+  last_bin = wave_sum_int(last_bin);
+  partial_sums[t] = local_sum;
+  __syncthreads();
+  if (lane == 0) hist[kHistogramBins - 1] += last_bin;
+  __syncthreads();
+  for (int b = lane; b < kHistogramBins; b += 64) block_hist[blockIdx.x * kHistogramBins + b] = hist[b];
+}
+
+// Steps 1-6 after sample_sum_kernel: the maximum and the total from the
+// partials (the total in the 1024-thread tree of block_sum_1024), the
+// histogram from the blocks' counts, then the cutoff, the compaction, the
+// sort and the walk in one 1024-thread block.
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restrict__ out_id,
                                                                 const float* __restrict__ logits,
                                                                 int vocab, float inv_temperature,
                                                                 int top_k, float top_p,
-                                                                float uniform) {
+                                                                float uniform,
+                                                                const unsigned long long* __restrict__ block_best,
+                                                                int best_blocks,
+                                                                const float* __restrict__ partial_sums,
+                                                                const int* __restrict__ block_hist) {
   __shared__ float lds32[32];
-  __shared__ unsigned long long lds_u64[16];
   __shared__ int histogram[kHistogramBins];
   __shared__ int wave_counts[kSampleWaves];
   __shared__ int shared_cutoff;
@@ -77,58 +144,23 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
   const int lane = lane_id();
   const int wave = t >> 6;
 
-  // 1. Maximum logit (exact in any order).
-  float local_max = -FLT_MAX;
-  for (int base = t; base < vocab; base += kSampleBatch * kSampleThreads) {
-    float v[kSampleBatch];
-#pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) {
-      const int i = base + k * kSampleThreads;
-      v[k] = i < vocab ? logits[i] : -FLT_MAX;
-    }
-#pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) local_max = fmaxf(local_max, v[k]);
+  // 1. Maximum logit; 2. the exponential sum and the histogram, from the
+  // partials of sample_sum_kernel.
+  float max_logit = 0.0f;
+  if (wave == 0) {
+    max_logit = max_from_keys(block_best, best_blocks);
+    if (lane == 0) lds32[0] = max_logit;
   }
-  {
-    // Reuse the u64 block max on the order key of the float (ties irrelevant).
-    unsigned long long key = static_cast<unsigned long long>(order_key(local_max)) << 32;
-    key = block_max_u64(key, lds_u64);
-    const uint32_t k = static_cast<uint32_t>(key >> 32);
-    local_max = u32_as_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+  for (int b = t; b < kHistogramBins; b += kSampleThreads) {
+    int count = 0;
+#pragma unroll
+    for (int w = 0; w < kSumBlocks; ++w) count += block_hist[w * kHistogramBins + b];
+    histogram[b] = count;
   }
-  const float max_logit = local_max;
-
-  // 2. Exponential sum over the whole vocabulary, and the histogram. Most
-  // logits fall in the last (clamped) bin: that bin is counted in registers
-  // and added once per wave, the others with LDS atomics.
-  for (int b = t; b < kHistogramBins; b += kSampleThreads) histogram[b] = 0;
   __syncthreads();
-  float local_sum = 0.0f;
-  int last_bin = 0;
-  for (int base = t; base < vocab; base += kSampleBatch * kSampleThreads) {
-    float v[kSampleBatch];
-#pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) {
-      const int i = base + k * kSampleThreads;
-      v[k] = i < vocab ? logits[i] : 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) {
-      if (base + k * kSampleThreads < vocab) {
-        const float scaled = (v[k] - max_logit) * inv_temperature;
-        local_sum += lcr_expf(scaled);
-        const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
-        if (bin == kHistogramBins - 1) {
-          ++last_bin;
-        } else if (bin >= 0) {
-          atomicAdd(&histogram[bin], 1);
-        }
-      }
-    }
-  }
-  last_bin = wave_sum_int(last_bin);
-  if (lane == 0) atomicAdd(&histogram[kHistogramBins - 1], last_bin);
-  const float total_sum = block_sum_1024(local_sum, lds32);  // its barriers order the atomics
+  max_logit = lds32[0];
+  __syncthreads();
+  const float total_sum = block_sum_1024(partial_sums[t], lds32);
 
   // 3. Cutoff bin: the number of leading bins whose running count stays
   // <= kMaxCandidates (at least 1). Wave 0, four bins per lane, in bin order.
@@ -276,11 +308,16 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
 
 using namespace lcr;
 
+// Scratch floats: one 64-bit partial maximum per argmax block, then (for
+// sampling) the 1024 partial exponential sums and the sum blocks' histograms.
+constexpr size_t kScratchKeys = 2 * static_cast<size_t>(kArgmaxBlocks);
+constexpr size_t kScratchSums = kSampleThreads;
+constexpr size_t kScratchHist = static_cast<size_t>(kSumBlocks) * kHistogramBins;
+
 extern "C" size_t lcr_sample_scratch_floats(int vocab, int top_k) {
   (void)vocab;
   (void)top_k;
-  // One 64-bit partial maximum per argmax block.
-  return 2 * static_cast<size_t>(kArgmaxBlocks);
+  return kScratchKeys + kScratchSums + kScratchHist;
 }
 
 extern "C" int lcr_sample(int32_t* out_id, const float* logits, int vocab, float temperature,
@@ -300,8 +337,19 @@ extern "C" int lcr_sample(int32_t* out_id, const float* logits, int vocab, float
     return LCR_OK;
   }
   CAPI_CHECK(top_p > 0.0f && top_p <= 1.0f, "top_p must be in (0, 1], got " << top_p);
-  sample_kernel<<<1, kSampleThreads, 0, s>>>(out_id, logits, vocab, 1.0f / temperature, top_k,
-                                             top_p, uniform);
+  CAPI_CHECK(scratch != nullptr, "sampling needs scratch space for its partial sums");
+  CAPI_CHECK((reinterpret_cast<uintptr_t>(scratch) & 7u) == 0, "sampling scratch must be 8-byte aligned");
+  auto* best = reinterpret_cast<unsigned long long*>(scratch);
+  float* sums = scratch + kScratchKeys;
+  int* hist = reinterpret_cast<int*>(scratch + kScratchKeys + kScratchSums);
+  const int blocks = std::min(kArgmaxBlocks, (vocab + kArgmaxThreads - 1) / kArgmaxThreads);
+  const float inv_temperature = 1.0f / temperature;
+  argmax_partial_kernel<<<blocks, kArgmaxThreads, 0, s>>>(best, logits, vocab);
+  CAPI_LAUNCHED();
+  sample_sum_kernel<<<kSumBlocks, 64, 0, s>>>(sums, hist, best, blocks, logits, vocab, inv_temperature);
+  CAPI_LAUNCHED();
+  sample_kernel<<<1, kSampleThreads, 0, s>>>(out_id, logits, vocab, inv_temperature, top_k, top_p, uniform, best,
+                                             blocks, sums, hist);
   CAPI_LAUNCHED();
   return LCR_OK;
 }

@@ -9,7 +9,11 @@
 // reduces those and writes the id, so there is nothing to clear between calls.
 //
 // Stochastic: the reference's one-block sampler (sampling.cu:97-224) with its
-// two scheduling-dependent steps made deterministic:
+// two scheduling-dependent steps made deterministic. Steps 1-2 run on many
+// compute units (the argmax blocks' partial maxima; sixteen one-wave blocks
+// that each run 64 threads of the 1024-thread order below and write their
+// partial sums and bin counts), steps 2's final sum and 3-6 in one
+// 1024-thread block:
 //  1. max logit (exact), scaled_i = (l_i - max) * inv_temperature;
 //  2. total = sum of exp(scaled_i): thread t (of 1024) adds i = t, t+1024, ...
 //     in order, then a butterfly in each 32-thread group (offsets 16..1), then

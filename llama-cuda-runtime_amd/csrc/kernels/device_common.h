@@ -45,6 +45,14 @@ __device__ __forceinline__ vec16 load16(const void* p) {
 __device__ __forceinline__ void store16(void* p, const vec16& v) {
   *reinterpret_cast<vec16*>(p) = v;
 }
+// A 16-byte load marked non-temporal, for data streamed once (the decode
+// GEMVs' weights): it does not displace cached lines. The value is that of
+// load16.
+__device__ __forceinline__ vec16 load16_stream(const void* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return vec16{{v.x, v.y, v.z, v.w}};
+}
 
 // The two elements packed in one 32-bit word (element 2i in the low half).
 __device__ __forceinline__ float elem_lo(uint32_t p) {

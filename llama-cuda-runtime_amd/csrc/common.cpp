@@ -3,75 +3,73 @@
 #include <cstdio>
 
 namespace lcr {
+
 namespace detail {
 
-void throw_failure(const char* file, int line, const char* cond,
-                   const std::string& msg) {
-  std::ostringstream text;
-  text << file << ":" << line << ": check failed: " << cond;
-  if (!msg.empty()) text << "\n  " << msg;
-  throw Error(text.str());
+void fail_check(const CheckSite& site, const std::string& message) {
+  std::string text = message.empty() ? std::string("check failed") : message;
+  text += " [check `";
+  text += site.condition;
+  text += "` at ";
+  text += site.file;
+  text += ":";
+  text += std::to_string(site.line);
+  text += "]";
+  throw Error(text);
 }
 
 }  // namespace detail
 
-size_t dtype_size(DType dt) {
-  switch (dt) {
-    case DType::kI64: return 8;
-    case DType::kF32:
-    case DType::kI32: return 4;
-    case DType::kF16:
-    case DType::kBF16: return 2;
-    case DType::kI8:
-    case DType::kU8:
-    case DType::kBool: return 1;
+namespace {
+
+struct ElementType {
+  DType type;
+  const char* header_name;  // spelling in a safetensors header
+  uint8_t bytes;
+};
+
+// One row per DType, in enum order.
+constexpr ElementType kElementTypes[] = {
+    {DType::kF32, "F32", 4}, {DType::kF16, "F16", 2}, {DType::kBF16, "BF16", 2},
+    {DType::kI64, "I64", 8}, {DType::kI32, "I32", 4}, {DType::kI8, "I8", 1},
+    {DType::kU8, "U8", 1},   {DType::kBool, "BOOL", 1},
+};
+
+const ElementType& element_type(DType dt) {
+  for (const ElementType& e : kElementTypes) {
+    if (e.type == dt) return e;
   }
-  LCR_FAIL("unknown dtype");
+  LCR_FAIL("DType value " << static_cast<int>(dt) << " has no table entry");
 }
 
-const char* dtype_name(DType dt) {
-  switch (dt) {
-    case DType::kF32: return "F32";
-    case DType::kF16: return "F16";
-    case DType::kBF16: return "BF16";
-    case DType::kI64: return "I64";
-    case DType::kI32: return "I32";
-    case DType::kI8: return "I8";
-    case DType::kU8: return "U8";
-    case DType::kBool: return "BOOL";
-  }
-  LCR_FAIL("unknown dtype");
-}
+}  // namespace
+
+size_t dtype_size(DType dt) { return element_type(dt).bytes; }
+
+const char* dtype_name(DType dt) { return element_type(dt).header_name; }
 
 DType dtype_from_string(const std::string& s) {
-  // The names are the ones the safetensors format writes in its header.
-  if (s == "F32") return DType::kF32;
-  if (s == "F16") return DType::kF16;
-  if (s == "BF16") return DType::kBF16;
-  if (s == "I64") return DType::kI64;
-  if (s == "I32") return DType::kI32;
-  if (s == "I8") return DType::kI8;
-  if (s == "U8") return DType::kU8;
-  if (s == "BOOL") return DType::kBool;
+  for (const ElementType& e : kElementTypes) {
+    if (s == e.header_name) return e.type;
+  }
+  // Float64 is a valid safetensors type, just not one this runtime computes in.
   LCR_CHECK(s != "F64", "F64 tensors are not supported");
   LCR_FAIL("unknown safetensors dtype \"" << s << "\"");
 }
 
 std::string format_bytes(size_t bytes) {
-  static const char* const kUnits[] = {"B", "KiB", "MiB", "GiB", "TiB"};
-  double value = static_cast<double>(bytes);
+  if (bytes < 1024) return std::to_string(bytes) + " B";
+  const char* const units[] = {"KiB", "MiB", "GiB", "TiB", "PiB"};
   int unit = 0;
-  while (value >= 1024.0 && unit < 4) {
-    value /= 1024.0;
+  size_t scale = 1024;
+  while (unit + 1 < 5 && bytes / scale >= 1024) {
+    scale *= 1024;
     ++unit;
   }
-  char buffer[48];
-  if (unit == 0) {
-    std::snprintf(buffer, sizeof(buffer), "%zu B", bytes);
-  } else {
-    std::snprintf(buffer, sizeof(buffer), "%.2f %s", value, kUnits[unit]);
-  }
-  return buffer;
+  char text[40];
+  std::snprintf(text, sizeof(text), "%.2f %s",
+                static_cast<double>(bytes) / static_cast<double>(scale), units[unit]);
+  return text;
 }
 
 }  // namespace lcr

@@ -1,15 +1,22 @@
-// Key/value cache, contiguous or paged (drop-in for the reference's
-// src/kv_cache.cuh:30-118).
+// Key/value cache of the token loop, contiguous or paged.
 //
-// Per layer, keys and values are stored head-major, K[kv_head][position][d],
-// so one head's history is a straight run of memory. The contiguous layout
-// reserves max_seq positions per head; the paged layout hands out pages of
-// page_size positions from a pool, in order, as the sequence grows, and keeps a
-// per-layer page table on the device. Both are addressed by one formula
-// (KvCacheView::offset), with the table lookup compiled away when contiguous.
+// Interface of the reference's KvCache and KvCacheView
+// (src/kv_cache.cuh:30-118): KvLayout, the view's fields and its offset
+// formula (the addressing contract between the KV append and attention),
+// reserve_length, view(layer), and the byte accounting.
+//
+// Design. Both layouts are one geometry (KvGeometry): a page holds
+// [kv_head][page_size][head_dim] elements, and the contiguous layout is the
+// case of one page of max_seq positions per layer (page_stride 0, no table).
+// Keys, values and the page tables live in one device block, allocated once;
+// the tables are mirrored on the host, which hands out pages in the
+// reference's order (sequentially, layer after layer, as positions are
+// reserved: src/kv_cache.cu:84-92) and uploads the changed span of all layers
+// in one copy.
 #pragma once
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -21,7 +28,7 @@ namespace lcr {
 
 enum class KvLayout { kContiguous, kPaged };
 
-// Non-owning, trivially copyable handle to one layer; same fields and order as
+// Non-owning, trivially copyable handle to one layer; the fields and order of
 // the C-ABI's lcr_kv_view.
 struct KvCacheView {
   elem_t* keys = nullptr;
@@ -33,6 +40,8 @@ struct KvCacheView {
   int num_kv_heads = 0;
   int head_dim = 0;
 
+  // Element offset of (head, position): page * page_stride + head *
+  // head_stride + slot * head_dim (src/kv_cache.cuh:49-56).
   template <bool kPaged>
   __host__ __device__ __forceinline__ size_t offset(int head, int position) const {
     const int page = kPaged ? page_table[position / page_size] : 0;
@@ -43,29 +52,29 @@ struct KvCacheView {
   }
 
   lcr_kv_view to_c() const {
-    lcr_kv_view v;
-    v.keys = keys;
-    v.values = values;
-    v.page_table = page_table;
-    v.page_size = page_size;
-    v.page_stride = page_stride;
-    v.head_stride = head_stride;
-    v.num_kv_heads = num_kv_heads;
-    v.head_dim = head_dim;
-    return v;
+    return lcr_kv_view{keys, values, page_table, page_size, page_stride, head_stride, num_kv_heads, head_dim};
   }
   static KvCacheView from_c(const lcr_kv_view& c) {
-    KvCacheView v;
-    v.keys = static_cast<elem_t*>(c.keys);
-    v.values = static_cast<elem_t*>(c.values);
-    v.page_table = c.page_table;
-    v.page_size = c.page_size;
-    v.page_stride = c.page_stride;
-    v.head_stride = c.head_stride;
-    v.num_kv_heads = c.num_kv_heads;
-    v.head_dim = c.head_dim;
-    return v;
+    return KvCacheView{static_cast<elem_t*>(c.keys), static_cast<elem_t*>(c.values), c.page_table, c.page_size,
+                       c.page_stride,  c.head_stride, c.num_kv_heads, c.head_dim};
   }
+};
+
+// Sizes of a cache, computed without touching the device.
+struct KvGeometry {
+  KvLayout layout = KvLayout::kContiguous;
+  int num_layers = 0;
+  int num_kv_heads = 0;
+  int head_dim = 0;
+  int max_seq = 0;
+  int page_size = 0;        // positions per page (max_seq when contiguous)
+  int pages_per_layer = 0;  // table entries per layer (0 when contiguous)
+  int pool_pages = 0;       // pages in each of the K and V pools
+  size_t page_elements = 0; // num_kv_heads * page_size * head_dim
+  size_t pool_elements() const { return static_cast<size_t>(pool_pages) * page_elements; }
+  size_t table_entries() const { return static_cast<size_t>(num_layers) * pages_per_layer; }
+
+  static KvGeometry plan(const ModelConfig& config, int max_seq, KvLayout layout, int page_size);
 };
 
 class KvCache {
@@ -75,57 +84,56 @@ class KvCache {
   KvCache(const KvCache&) = delete;
   KvCache& operator=(const KvCache&) = delete;
 
-  // Makes room for `length` positions: a bound check when contiguous; maps the
-  // pages that length needs, in order, when paged. Synchronous (page-table
-  // upload), so it is called outside any captured graph.
+  // Makes `length` positions addressable: a bound check when contiguous; in the
+  // paged layout, maps the pages that length needs in every layer. Blocking
+  // (it uploads table entries), so it runs outside any captured graph.
   void reserve_length(int length);
 
   KvCacheView view(int layer) const;
 
-  KvLayout layout() const { return layout_; }
-  int page_size() const { return page_size_; }
-  int max_seq() const { return max_seq_; }
+  KvLayout layout() const { return geo_.layout; }
+  const KvGeometry& geometry() const { return geo_; }
+  int page_size() const { return geo_.page_size; }
+  int max_seq() const { return geo_.max_seq; }
   int length() const { return length_; }
-  int max_pages() const { return max_pages_; }
-  int pool_pages() const { return pool_pages_; }
+  int max_pages() const { return geo_.pages_per_layer; }
+  int pool_pages() const { return geo_.pool_pages; }
 
   size_t allocated_bytes() const { return allocated_bytes_; }
+  // Bytes of the pages handed out so far (all of both pools when contiguous).
   size_t live_bytes() const;
+  // Bytes `length()` positions need with no rounding to pages.
   size_t ideal_bytes() const;
   std::string usage_string() const;
 
   static size_t bytes_for(const ModelConfig& config, int64_t positions);
 
-  // Test and benchmark hook, not in the reference: replaces the page table of
-  // every layer with `tables` ([num_layers][max_pages] physical page ids, each
-  // a distinct page of the pool) and marks `length` positions as present. Used
-  // for the long-context stress case, whose block table is a seeded random
-  // permutation of the pool rather than the reference's in-order assignment.
+  // Test and benchmark hook, not in the reference: installs `tables`
+  // ([num_layers][max_pages] physical page ids, distinct, -1 for unmapped) and
+  // marks `length` positions present, so a cache can be laid out as a seeded
+  // random permutation of the pool instead of in handout order.
   void set_page_tables(const std::vector<int32_t>& tables, int length);
-  // Raw pools, for filling the cache directly in that stress case.
-  elem_t* key_pool() const { return key_pool_; }
-  elem_t* value_pool() const { return value_pool_; }
-  size_t pool_elements() const { return pool_elements_; }
+  // Raw pools, for filling a cache directly.
+  elem_t* key_pool() const { return keys_; }
+  elem_t* value_pool() const { return values_; }
+  size_t pool_elements() const { return geo_.pool_elements(); }
 
  private:
-  size_t layer_elements() const;
+  void upload_tables(size_t first, size_t count);
 
-  ModelConfig config_;
-  KvLayout layout_;
-  int max_seq_ = 0;
-  int page_size_ = 0;
+  struct HipFree {
+    void operator()(void* p) const;
+  };
+
+  KvGeometry geo_;
   int length_ = 0;
-
-  elem_t* key_pool_ = nullptr;
-  elem_t* value_pool_ = nullptr;
-  size_t pool_elements_ = 0;
+  std::unique_ptr<unsigned char, HipFree> block_;
+  elem_t* keys_ = nullptr;
+  elem_t* values_ = nullptr;
+  int32_t* tables_ = nullptr;        // device, [num_layers][pages_per_layer]
+  std::vector<int32_t> host_tables_; // mirror
+  int next_page_ = 0;                // next physical page to hand out
   size_t allocated_bytes_ = 0;
-
-  int32_t* page_tables_device_ = nullptr;
-  std::vector<int32_t> page_tables_host_;
-  int max_pages_ = 0;
-  int pool_pages_ = 0;
-  int pages_mapped_ = 0;
 };
 
 }  // namespace lcr

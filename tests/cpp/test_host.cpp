@@ -16,8 +16,10 @@
 #include <string>
 #include <vector>
 
+#include "common.h"
 #include "config.h"
 #include "json.h"
+#include "kv_cache.h"
 #include "safetensors.h"
 
 namespace {
@@ -308,6 +310,60 @@ void test_json() {
   EXPECT_EQ(o.dump(), std::string(R"({"k":3,"s":"a\"b"})"));
 }
 
+// Element-type table, size formatting and the check macro (common.h).
+void test_common() {
+  using lcr::DType;
+  for (DType t : {DType::kF32, DType::kF16, DType::kBF16, DType::kI64, DType::kI32, DType::kI8, DType::kU8,
+                  DType::kBool}) {
+    EXPECT(lcr::dtype_from_string(lcr::dtype_name(t)) == t);
+  }
+  EXPECT_EQ(lcr::dtype_size(DType::kBF16), static_cast<size_t>(2));
+  EXPECT_EQ(lcr::dtype_size(DType::kI64), static_cast<size_t>(8));
+  EXPECT_EQ(lcr::dtype_size(DType::kBool), static_cast<size_t>(1));
+  EXPECT_EQ(std::string(lcr::dtype_name(DType::kBF16)), std::string("BF16"));
+  EXPECT_THROWS("F64 tensors are not supported", { lcr::dtype_from_string("F64"); });
+  EXPECT_THROWS("unknown safetensors dtype \"F8_E4M3\"", { lcr::dtype_from_string("F8_E4M3"); });
+  EXPECT_EQ(lcr::format_bytes(0), std::string("0 B"));
+  EXPECT_EQ(lcr::format_bytes(1023), std::string("1023 B"));
+  EXPECT_EQ(lcr::format_bytes(1024), std::string("1.00 KiB"));
+  EXPECT_EQ(lcr::format_bytes(1536), std::string("1.50 KiB"));
+  EXPECT_EQ(lcr::format_bytes(static_cast<size_t>(2471628800)), std::string("2.30 GiB"));
+  EXPECT_EQ(lcr::align_up(257, 256), static_cast<size_t>(512));
+  EXPECT_EQ(lcr::align_up(256, 256), static_cast<size_t>(256));
+  try {
+    const int n = -3;
+    LCR_CHECK(n > 0, "expected a positive length, got " << n);
+    report(false, __FILE__, __LINE__, "LCR_CHECK did not throw");
+  } catch (const lcr::Error& e) {
+    const std::string what = e.what();
+    EXPECT(what.find("expected a positive length, got -3") != std::string::npos);
+    EXPECT(what.find("n > 0") != std::string::npos);
+    EXPECT(what.find("test_host.cpp") != std::string::npos);
+  }
+}
+
+// Pool and table sizes of both KV layouts (no device memory is touched).
+void test_kv_geometry() {
+  const ModelConfig c = ModelConfig::from_json_string(kLlama32_1B);
+  const lcr::KvGeometry contiguous = lcr::KvGeometry::plan(c, 2048, lcr::KvLayout::kContiguous, 16);
+  EXPECT_EQ(contiguous.page_size, 2048);
+  EXPECT_EQ(contiguous.pool_pages, 16);
+  EXPECT_EQ(contiguous.table_entries(), static_cast<size_t>(0));
+  // [16 layers][8 kv heads][2048][64] per pool, as the reference sizes it.
+  EXPECT_EQ(contiguous.pool_elements(), static_cast<size_t>(16) * 8 * 2048 * 64);
+  const lcr::KvGeometry paged = lcr::KvGeometry::plan(c, 2050, lcr::KvLayout::kPaged, 16);
+  EXPECT_EQ(paged.pages_per_layer, 129);  // ceil(2050 / 16)
+  EXPECT_EQ(paged.pool_pages, 129 * 16);
+  EXPECT_EQ(paged.page_elements, static_cast<size_t>(8) * 16 * 64);
+  EXPECT_EQ(paged.table_entries(), static_cast<size_t>(129) * 16);
+  EXPECT_EQ(paged.pool_elements(), static_cast<size_t>(129) * 16 * 8 * 16 * 64);
+  // 32,768 bytes of keys and values per position (bf16), the reference's
+  // per-position accounting.
+  EXPECT_EQ(lcr::KvCache::bytes_for(c, 1), static_cast<size_t>(32768));
+  EXPECT_THROWS("positive maximum sequence length", { lcr::KvGeometry::plan(c, 0, lcr::KvLayout::kPaged, 16); });
+  EXPECT_THROWS("positive page size", { lcr::KvGeometry::plan(c, 64, lcr::KvLayout::kPaged, 0); });
+}
+
 }  // namespace
 
 int main() {
@@ -320,6 +376,8 @@ int main() {
   test_safetensors_rejections();
   test_safetensors_writer_round_trip();
   test_json();
+  test_common();
+  test_kv_geometry();
   if (g_failures == 0) {
     std::printf("test_host: all checks passed\n");
     return 0;

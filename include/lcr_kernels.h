@@ -113,6 +113,24 @@ int lcr_decode_attention(void* out, const void* q, const lcr_kv_view* view, int 
                          int heads_per_kv, int seq_len, float scale, int paged, int splits,
                          float* scratch, void* stream);
 
+/* Largest partials buffer lcr_decode_attention_noalloc holds: 2 MiB of floats
+ * (32 heads x 64 splits x (2 + 128) = 266,240 floats fit). */
+#define LCR_NOALLOC_ATTENTION_SCRATCH_FLOATS (524288)
+
+/* lcr_decode_attention without a scratch argument and without allocating: the
+ * split partials go to a fixed device array of the library
+ * (LCR_NOALLOC_ATTENTION_SCRATCH_FLOATS floats, one per device, held until the
+ * process ends). No counterpart in the reference; it is for callers that cannot
+ * allocate (code under graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Arguments and results are those of lcr_decode_attention;
+ * a call whose partials would exceed the array fails with LCR_ERR_ARGUMENT.
+ * Every call on a device shares that device's array (nothing in it needs to
+ * start at zero: each split writes all of its partials before the merge reads
+ * them), so calls that overlap in time on one device race. */
+int lcr_decode_attention_noalloc(void* out, const void* q, const lcr_kv_view* view, int num_heads,
+                                 int heads_per_kv, int seq_len, float scale, int paged, int splits,
+                                 void* stream);
+
 /* Floats of scratch lcr_decode_attention needs (0 when splits <= 1) —
  * src/kernels.cuh:114 */
 size_t lcr_decode_attention_scratch_floats(int num_heads, int head_dim, int splits);

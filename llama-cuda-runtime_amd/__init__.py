@@ -140,6 +140,7 @@ SIGNATURES = {
     "lcr_merge_heads": (_I, [_P, _P, _I, _I, _I, _P]),
     "lcr_gather_kv": (_I, [_P, _P, ctypes.POINTER(KvView), _I, _P]),
     "lcr_decode_attention": (_I, [_P, _P, ctypes.POINTER(KvView), _I, _I, _I, _F, _I, _I, _P, _P]),
+    "lcr_decode_attention_noalloc": (_I, [_P, _P, ctypes.POINTER(KvView), _I, _I, _I, _F, _I, _I, _P]),
     "lcr_decode_attention_scratch_floats": (_SZ, [_I, _I, _I]),
     "lcr_choose_attention_splits": (_I, [_I, _I, _I]),
     "lcr_sample": (_I, [_P, _P, _I, _F, _I, _F, _F, _P, _P]),

@@ -11,6 +11,8 @@
 // combining its own state with thread i^o's, in that argument order), then the
 // 8 group results combined in order by thread 0.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "../capi_util.h"
 #include "attention_decode.h"
@@ -169,6 +171,44 @@ int launch_by_head_dim(int head_dim, int heads_per_kv, const DecodeArgs& a) {
 }  // namespace
 }  // namespace lcr
 
+// Split partials of lcr_decode_attention_noalloc: one array per device, alive
+// until the process ends. Every call on a device shares its array.
+static __device__ __align__(256) float scratch[LCR_NOALLOC_ATTENTION_SCRATCH_FLOATS];
+
+namespace lcr {
+namespace {
+
+// Device address of `scratch` per device, looked up once (with that device
+// current) on the entry point's first call there. In host code the array's
+// name is only a host-side stand-in, never a device address.
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_noalloc_scratch[kMaxDevices];
+std::mutex g_noalloc_mutex;
+
+int noalloc_scratch(float** out) {
+  int device = -1;
+  CAPI_HIP(hipGetDevice(&device));
+  CAPI_CHECK(device >= 0 && device < kMaxDevices,
+             "device " << device << " is beyond the " << kMaxDevices << " this library tracks");
+  float* ptr = g_noalloc_scratch[device].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    ptr = g_noalloc_scratch[device].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      void* address = nullptr;
+      CAPI_HIP(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)));
+      CAPI_CHECK(address != nullptr, "hipGetSymbolAddress gave no address for the attention scratch");
+      ptr = static_cast<float*>(address);
+      g_noalloc_scratch[device].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return LCR_OK;
+}
+
+}  // namespace
+}  // namespace lcr
+
 using namespace lcr;
 
 extern "C" size_t lcr_decode_attention_scratch_floats(int num_heads, int head_dim, int splits) {
@@ -190,11 +230,11 @@ extern "C" int lcr_choose_attention_splits(int num_kv_heads, int seq_len, int mu
 
 extern "C" int lcr_decode_attention(void* out, const void* q, const lcr_kv_view* view,
                                     int num_heads, int heads_per_kv, int seq_len, float scale,
-                                    int paged, int splits, float* scratch, void* stream) {
+                                    int paged, int splits, float* partials, void* stream) {
   CAPI_CHECK(view != nullptr, "decode attention needs a cache view");
   CAPI_CHECK(seq_len > 0, "decode attention needs at least one cached position");
   CAPI_CHECK(splits >= 1, "split count must be positive, got " << splits);
-  CAPI_CHECK(splits == 1 || scratch != nullptr,
+  CAPI_CHECK(splits == 1 || partials != nullptr,
              "a split decode attention needs scratch space for the partials");
   CAPI_CHECK(view->head_dim % 32 == 0,
              "decode attention needs head_dim to be a multiple of the warp width, got "
@@ -210,7 +250,7 @@ extern "C" int lcr_decode_attention(void* out, const void* q, const lcr_kv_view*
              "decode attention needs 16-byte aligned q and cache pointers");
   DecodeArgs a;
   a.out = static_cast<elem_t*>(out);
-  a.partials = scratch;
+  a.partials = partials;
   a.q = static_cast<const elem_t*>(q);
   a.view = KvCacheView::from_c(*view);
   a.num_heads = num_heads;
@@ -220,6 +260,30 @@ extern "C" int lcr_decode_attention(void* out, const void* q, const lcr_kv_view*
   a.stream = static_cast<hipStream_t>(stream);
   return paged ? launch_by_head_dim<true>(view->head_dim, heads_per_kv, a)
                : launch_by_head_dim<false>(view->head_dim, heads_per_kv, a);
+}
+
+extern "C" int lcr_decode_attention_noalloc(void* out, const void* q, const lcr_kv_view* view,
+                                            int num_heads, int heads_per_kv, int seq_len, float scale,
+                                            int paged, int splits, void* stream) {
+  CAPI_CHECK(view != nullptr, "decode attention needs a cache view");
+  CAPI_CHECK(seq_len > 0, "decode attention needs at least one cached position");
+  CAPI_CHECK(splits >= 1, "split count must be positive, got " << splits);
+  CAPI_CHECK(num_heads > 0 && view->head_dim > 0, "decode attention needs positive head counts and head_dim");
+  // The split count the launch will use (lcr_decode_attention clamps the same way).
+  const int used_splits = std::min(std::min(splits, seq_len), kMaxSplits);
+  const size_t need = lcr_decode_attention_scratch_floats(num_heads, view->head_dim, used_splits);
+  CAPI_CHECK(need <= LCR_NOALLOC_ATTENTION_SCRATCH_FLOATS,
+             "decode attention without allocation holds at most " << LCR_NOALLOC_ATTENTION_SCRATCH_FLOATS
+                 << " partial floats, this call needs " << need << " (" << num_heads << " heads x "
+                 << used_splits << " splits x " << (kPartialHeader + view->head_dim)
+                 << "); pass fewer splits or call lcr_decode_attention with a workspace");
+  float* partials = nullptr;
+  if (need > 0) {
+    const int status = noalloc_scratch(&partials);
+    if (status != LCR_OK) return status;
+  }
+  return lcr_decode_attention(out, q, view, num_heads, heads_per_kv, seq_len, scale, paged, used_splits, partials,
+                              stream);
 }
 
 extern "C" int lcr_causal_softmax(void* probs, const float* scores, int num_heads, int rows,

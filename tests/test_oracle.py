@@ -476,3 +476,168 @@ def test_sample_matches_float64_walk_away_from_boundaries():
         assert oracle.sample(logits, T, k, p, u) == want, (trial, vocab, T, k, p, u)
         checked += 1
     assert checked > 150
+
+
+# ---------------------------------------------------------------------------
+# prefill attention (src/model.cu:509-560 with src/kernels/attention.cu:42-100)
+# ---------------------------------------------------------------------------
+
+def fp64_causal_attention(q, keys, values, heads, kv, hd, tokens, start, mistake=None):
+    """Exact causal softmax attention in float64, written from the semantics
+    of the reference's prefill: query row r sits at position start + r and
+    sees keys 0..start + r of its kv head (h // (heads / kv)); scores are
+    scaled by 1/sqrt(head_dim). `mistake` plants one plausible error, to show
+    that the tolerance below catches it."""
+    G = heads // kv
+    scale = 1.0 / math.sqrt(hd)
+    out = np.zeros((tokens, heads, hd))
+    for h in range(heads):
+        g = (h % kv) if mistake == "kv_head" else h // G
+        k = keys[:, g * hd:(g + 1) * hd]
+        v = values[:, g * hd:(g + 1) * hd]
+        if mistake == "swap_kv":
+            k, v = v, k
+        for r in range(tokens):
+            limit = start + r + (2 if mistake == "mask_off_by_one" else 1)
+            if mistake == "no_start":
+                limit = r + 1
+            limit = min(limit, keys.shape[0])
+            s = k[:limit] @ q[h, r] * (1.0 if mistake == "no_scale" else scale)
+            p = np.exp(s - s.max())
+            out[r, h] = (p @ v[:limit]) / p.sum()
+    return out.reshape(tokens, heads * hd)
+
+
+def oracle_prefill_attention(L, q_heads, keys, values, heads, kv, hd, tokens, start, table):
+    n = start + tokens
+    ps = 16
+    pages = len(table)
+    pool_k = np.zeros(pages * kv * ps * hd, dtype=np.uint16)
+    pool_v = np.zeros_like(pool_k)
+    view = oracle_view(pool_k, pool_v, table, ps, kv * ps * hd, ps * hd, kv, hd)
+    zeros = np.zeros(hd // 2, dtype=np.float32)
+    L.orc_rope_write_kv(BF16, ctypes.byref(view), keys.ctypes.data, values.ctypes.data, zeros.ctypes.data, n, 0,
+                        1, kv * hd)
+    out = np.zeros(tokens * heads * hd, dtype=np.uint16)
+    L.orc_prefill_attention(BF16, out.ctypes.data, q_heads.ctypes.data, ctypes.byref(view), heads, heads // kv,
+                            tokens, start, float(np.float32(1.0) / np.sqrt(np.float32(hd))), 1)
+    return to_f32(out).reshape(tokens, heads * hd)
+
+
+PREFILL_ATTENTION_TOL = 1e-2  # worst |diff| over max |exact|; bf16 probabilities and output give ~4e-3
+
+
+@pytest.mark.parametrize("heads,kv,hd,tokens,start", [
+    (8, 8, 64, 37, 0),     # group of 1
+    (32, 8, 64, 45, 0),    # group of 4 (Llama-3.2-1B)
+    (16, 2, 64, 33, 29),   # group of 8, a later chunk: queries at positions 29..61
+    (32, 8, 64, 20, 300),  # a short chunk after a long history
+    (8, 2, 128, 19, 5),    # head_dim 128
+])
+def test_prefill_attention_vs_fp64(L, heads, kv, hd, tokens, start):
+    r = rng(tokens * 7 + start)
+    n = start + tokens
+    keys = random_elems(r, (n, kv * hd))
+    values = random_elems(r, (n, kv * hd))
+    q = random_elems(r, (heads, tokens, hd))  # head-major, as the RoPE kernel writes it
+    table = r.permutation(-(-n // 16) + 2).astype(np.int32)  # a shuffled page table with spare pages
+    got = oracle_prefill_attention(L, q, keys, values, heads, kv, hd, tokens, start, table)
+    qf, kf, vf = (to_f32(a).astype(np.float64) for a in (q, keys, values))
+    want = fp64_causal_attention(qf, kf, vf, heads, kv, hd, tokens, start)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err <= PREFILL_ATTENTION_TOL, err
+    # Each planted mistake lands far outside the tolerance (the ones that
+    # cannot change this case are skipped: no start offset when start == 0,
+    # a kv-head mix-up when every head has its own).
+    for mistake in ("kv_head", "swap_kv", "mask_off_by_one", "no_scale", "no_start"):
+        if (mistake == "no_start" and start == 0) or (mistake == "kv_head" and heads == kv):
+            continue
+        bad = fp64_causal_attention(qf, kf, vf, heads, kv, hd, tokens, start, mistake)
+        assert np.abs(got - bad).max() / np.abs(bad).max() > 5 * PREFILL_ATTENTION_TOL, mistake
+
+
+def test_prefill_attention_first_row_is_first_value(L):
+    """A query at position 0 sees one key: its softmax weight is exactly 1 and
+    the output is that key's value row, bit for bit."""
+    r = rng(31)
+    heads, kv, hd, tokens = 32, 8, 64, 9
+    keys = random_elems(r, (tokens, kv * hd))
+    values = random_elems(r, (tokens, kv * hd))
+    q = random_elems(r, (heads, tokens, hd))
+    table = np.arange(1, dtype=np.int32)
+    got = oracle_prefill_attention(L, q, keys, values, heads, kv, hd, tokens, 0, table)
+    for h in range(heads):
+        g = h // (heads // kv)
+        assert np.array_equal(elems(got[0, h * hd:(h + 1) * hd]), values[0, g * hd:(g + 1) * hd])
+
+
+# ---------------------------------------------------------------------------
+# strided SwiGLU (src/kernels/elementwise.cu:96-121)
+# ---------------------------------------------------------------------------
+
+def test_swiglu_strided_closed_form(L):
+    """act[t][i] = silu(g) * u with g = row[t][i] and u = row[t][F + i] of the
+    fused gate/up projection (row stride 2F): within one bf16 ulp of the
+    float64 closed form g * u / (1 + exp(-g)), for every element."""
+    r = rng(32)
+    tokens, F = 5, 1000
+    rows = random_elems(r, (tokens, 2 * F), 3.0)
+    out = np.zeros(tokens * F, dtype=np.uint16)
+    up = rows.ctypes.data + F * rows.itemsize  # the up half starts F elements into row 0
+    L.orc_swiglu_strided(BF16, out.ctypes.data, rows.ctypes.data, up, tokens, F, 2 * F)
+    rf = to_f32(rows).astype(np.float64)
+    g, u = rf[:, :F], rf[:, F:]
+    want = g * u / (1.0 + np.exp(-g))
+    got = to_f32(out).reshape(tokens, F).astype(np.float64)
+    ulp = np.maximum(np.abs(want), 1e-30) * 2.0 ** -7
+    assert np.all(np.abs(got - want) <= ulp)
+    # the two halves are not interchangeable: silu(u) * g is a different function
+    swapped = u * g / (1.0 + np.exp(-u))
+    assert np.mean(np.abs(got - swapped) > ulp) > 0.5
+    # the stride is honoured: token t reads row t, not row 0
+    assert np.mean(np.abs(got[1:] - want[0]) > ulp[1:]) > 0.5
+
+
+# ---------------------------------------------------------------------------
+# the sampler over the full Llama-3 vocabulary
+# ---------------------------------------------------------------------------
+
+def test_sample_full_vocabulary_matches_float64_walk():
+    """128256 logits, temperature 0.8, top-k 40, top-p 0.95 (configuration 5)
+    and also top-k off: the histogram cut (src/kernels/sampling.cu:128-180)
+    keeps at most 1024 candidates; whenever the top-k / top-p nucleus lies
+    inside them, the result must equal a float64 walk over the fully sorted
+    vocabulary. Draws within float32 noise of a cumulative boundary, or whose
+    nucleus boundary is a near tie with top_p, are skipped."""
+    r = rng(33)
+    vocab = 128256
+    checked = 0
+    cases = 0
+    for trial in range(24):
+        sigma = float(r.choice([1.0, 2.0, 3.0, 4.0]))
+        logits = r.normal(0, sigma, vocab).astype(np.float32)
+        T = 0.8
+        k = 40 if trial % 3 else 0
+        p = 0.95
+        scaled = (logits.astype(np.float64) - logits.max()) / T
+        order = np.lexsort((np.arange(vocab), -logits))
+        prob = np.exp(scaled[order]) / np.exp(scaled).sum()
+        limit = vocab if k <= 0 else k
+        csum = np.cumsum(prob[:limit])
+        crossing = int(np.searchsorted(csum, p))  # first index with csum >= p
+        keep = min(crossing + 1, limit)
+        # the nucleus must fit the 1024-candidate cut for the algorithm to be exact
+        if keep > 1024:
+            continue
+        if abs(csum[min(crossing, limit - 1)] - p) < 1e-5:
+            continue
+        cases += 1
+        mass = csum[keep - 1]
+        for u in r.uniform(0, 1, 8):
+            target = u * mass
+            if np.min(np.abs(csum[:keep] - target)) < 1e-5 * max(1.0, target):
+                continue
+            want = int(order[int(np.searchsorted(csum[:keep], target))])
+            assert oracle.sample(logits, T, k, p, float(u)) == want, (trial, sigma, k, u)
+            checked += 1
+    assert cases >= 12 and checked >= 80, (cases, checked)

@@ -1,0 +1,101 @@
+"""Pins the oracle's whole-model composition (src/model.cu:303-503) on the CPU.
+
+The oracle's model chains its own kernels in the reference's order, with bf16
+roundings where the reference rounds. It is compared here with a float64
+Llama forward pass written from the architecture (tests/llama_fp64.py), on a
+tiny two-layer model with grouped-query attention (8 query heads on 2 key/value
+heads), Llama 3 RoPE scaling, tied embeddings and random (not unit) norm
+weights. The comparison uses the figures of the reference's validator
+(tools/validate_main.cu:95-137): per-tensor max-abs, rel-RMS and cosine, for the
+logits and for the residual stream after every layer. A bf16 implementation
+sits at 1-2 % rel-RMS from float64 here; each planted architectural mistake
+(tests/llama_fp64.MISTAKES) sits at 28 % or more.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+import llama_fp64 as F
+
+REL_RMS_MAX = 0.03
+COSINE_MIN = 0.9995
+
+PROMPT_LEN = 24
+STEPS = 8
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    cfg = F.tiny_config()
+    d = tmp_path_factory.mktemp("tiny_llama")
+    w = F.write_checkpoint(d, cfg)
+    prompt = np.random.default_rng(3).integers(0, cfg["vocab_size"], PROMPT_LEN)
+    return cfg, d, w, prompt
+
+
+def check(got, want, what):
+    dr = F.drift(got, want)
+    assert dr["rel_rms"] <= REL_RMS_MAX and dr["cosine"] >= COSINE_MIN, (what, dr)
+    return dr
+
+
+@pytest.mark.parametrize("path", ["decode", "chunked", "paged_chunked"])
+def test_oracle_model_matches_fp64_llama(tiny, path):
+    """Prefill (through the decode path, or chunked by 16 so the second chunk
+    starts at position 16), then 8 greedy decode steps: logits and the
+    per-layer residual stream within the validator's bounds at every step,
+    and the same greedy token wherever float64's top-two margin exceeds four
+    times the observed logit drift."""
+    cfg, d, w, prompt = tiny
+    m = oracle.OracleModel(d, max_seq=64, prefill_chunk=16, paged=path == "paged_chunked", page_size=4)
+    try:
+        logits = m.prefill(prompt, use_decode_path=path == "decode")
+        ref, hidden, final = F.forward(cfg, w, prompt, return_hidden=True)
+        dr = check(logits, ref[-1], f"{path} prefill logits")
+        for i in range(len(hidden) + 1):
+            tap = m.tap(i, PROMPT_LEN)
+            want = (hidden[i] if i < len(hidden) else final)[-tap.shape[0]:]
+            check(tap, want, f"{path} prefill tap {i}")
+        seq = list(prompt)
+        compared = 0
+        for step in range(STEPS):
+            top2 = np.sort(ref[-1])[-2:]
+            tok = oracle.argmax(logits)
+            if top2[1] - top2[0] > 4 * dr["max_abs"]:
+                assert tok == int(np.argmax(ref[-1])), (path, step)
+                compared += 1
+            seq.append(tok)
+            logits = m.decode(tok)
+            ref = F.forward(cfg, w, seq)
+            dr = check(logits, ref[-1], f"{path} step {step} logits")
+        assert compared >= 3
+    finally:
+        m.close()
+
+
+def test_paged_oracle_equals_contiguous(tiny):
+    """The page table only moves cache rows: paged and contiguous runs give
+    the same bits."""
+    cfg, d, w, prompt = tiny
+    outs = []
+    for paged in (False, True):
+        m = oracle.OracleModel(d, max_seq=64, prefill_chunk=16, paged=paged, page_size=4)
+        first = m.prefill(prompt)
+        outs.append(np.concatenate([first, m.decode(oracle.argmax(first))]))
+        m.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("mistake", F.MISTAKES)
+def test_planted_mistakes_exceed_the_bounds(tiny, mistake):
+    """Each architectural mistake, planted in the float64 model, lands at
+    least five times outside the bound the oracle is held to."""
+    cfg, d, w, prompt = tiny
+    m = oracle.OracleModel(d, max_seq=64, prefill_chunk=16)
+    try:
+        logits = m.prefill(prompt)
+    finally:
+        m.close()
+    bad = F.forward(cfg, w, prompt, mistake=mistake)[-1]
+    assert F.drift(logits, bad)["rel_rms"] > 5 * REL_RMS_MAX, mistake

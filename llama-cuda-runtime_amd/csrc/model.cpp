@@ -296,6 +296,11 @@ const float* Model::prefill(const std::vector<int>& tokens) {
   while (consumed < tokens.size()) {
     const int chunk = static_cast<int>(std::min<size_t>(static_cast<size_t>(max_tokens_),
                                                         tokens.size() - consumed));
+    if (chunk < kMinMfmaPrefillTokens) {
+      for (int i = 0; i < chunk; ++i) decode(tokens[consumed + static_cast<size_t>(i)]);
+      consumed += static_cast<size_t>(chunk);
+      continue;
+    }
     std::vector<int32_t> ids(tokens.begin() + static_cast<long>(consumed),
                              tokens.begin() + static_cast<long>(consumed) + chunk);
     HIP_CHECK(hipMemcpyAsync(token_ids_, ids.data(), ids.size() * sizeof(int32_t),

@@ -66,6 +66,11 @@ class Model {
     bool prefill_via_decode = false; // run prompts token by token through decode
   };
 
+  // Prompt chunks shorter than this run token by token through the decode
+  // step (GEMV path, bit-identical to decoding them) rather than through the
+  // MFMA GEMMs, which only pay off from a few tiles of tokens upward.
+  static constexpr int kMinMfmaPrefillTokens = 64;
+
   Model(const std::string& model_dir, const Options& options);
   ~Model();
   Model(const Model&) = delete;

@@ -33,10 +33,13 @@
 // Build: oracle/Makefile (g++ -O3 -mavx2 -mfma -fopenmp -ffp-contract=off).
 #include "lcr_oracle.h"
 
+#include <immintrin.h>
+
 #include <algorithm>
 #include <cfloat>
 #include <climits>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -748,34 +751,56 @@ void orc_prefill_attention(int kind, uint16_t* out, const uint16_t* q_heads,
                            const orc_kv_view* view, int num_heads, int heads_per_kv, int tokens,
                            int start_position, float scale, int paged) {
   const int hd = view->head_dim;
-#pragma omp parallel for collapse(2) schedule(dynamic)
-  for (int h = 0; h < num_heads; ++h) {
-    for (int r = 0; r < tokens; ++r) {
-      const int kv = h / heads_per_kv;
-      const int limit = start_position + r + 1;
-      const uint16_t* q = q_heads + (static_cast<size_t>(h) * tokens + r) * hd;
-      std::vector<float> s(static_cast<size_t>(limit));
-      float m = -FLT_MAX;
-      for (int k = 0; k < limit; ++k) {
-        const int64_t off = kv_off(*view, paged != 0, kv, k);
-        double d = 0.0;
-        for (int i = 0; i < hd; ++i) {
-          d += static_cast<double>(e2f(q[i], kind)) * e2f(view->keys[off + i], kind);
+  const int n = start_position + tokens;
+  const int kv_heads = num_heads / heads_per_kv;
+  // Keys and values of every kv head as floats, in position order.
+  std::vector<float> kf(static_cast<size_t>(kv_heads) * n * hd), vf(kf.size());
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int g = 0; g < kv_heads; ++g) {
+    for (int k = 0; k < n; ++k) {
+      const int64_t off = kv_off(*view, paged != 0, g, k);
+      float* kr = kf.data() + (static_cast<size_t>(g) * n + k) * hd;
+      float* vr = vf.data() + (static_cast<size_t>(g) * n + k) * hd;
+      for (int i = 0; i < hd; ++i) {
+        kr[i] = e2f(view->keys[off + i], kind);
+        vr[i] = e2f(view->values[off + i], kind);
+      }
+    }
+  }
+#pragma omp parallel
+  {
+    std::vector<float> s(static_cast<size_t>(n));
+    std::vector<double> qd(static_cast<size_t>(hd)), acc(static_cast<size_t>(hd));
+#pragma omp for collapse(2) schedule(dynamic, 4)
+    for (int h = 0; h < num_heads; ++h) {
+      for (int r = 0; r < tokens; ++r) {
+        const int g = h / heads_per_kv;
+        const int limit = start_position + r + 1;
+        const uint16_t* q = q_heads + (static_cast<size_t>(h) * tokens + r) * hd;
+        for (int i = 0; i < hd; ++i) qd[static_cast<size_t>(i)] = e2f(q[i], kind);
+        const float* K = kf.data() + static_cast<size_t>(g) * n * hd;
+        const float* V = vf.data() + static_cast<size_t>(g) * n * hd;
+        float m = -FLT_MAX;
+        for (int k = 0; k < limit; ++k) {
+          const float* kr = K + static_cast<size_t>(k) * hd;
+          double d = 0.0;
+          for (int i = 0; i < hd; ++i) d += qd[static_cast<size_t>(i)] * kr[i];
+          s[static_cast<size_t>(k)] = static_cast<float>(d) * scale;
+          m = std::fmax(m, s[static_cast<size_t>(k)]);
         }
-        s[static_cast<size_t>(k)] = static_cast<float>(d) * scale;
-        m = std::fmax(m, s[static_cast<size_t>(k)]);
+        double l = 0.0;
+        for (int k = 0; k < limit; ++k) l += std::exp(static_cast<double>(s[static_cast<size_t>(k)] - m));
+        const float inv = static_cast<float>(1.0 / l);
+        std::fill(acc.begin(), acc.end(), 0.0);
+        for (int k = 0; k < limit; ++k) {
+          const float p = e2f(f2e(static_cast<float>(std::exp(static_cast<double>(s[static_cast<size_t>(k)] - m))) * inv,
+                                  kind), kind);
+          const float* vr = V + static_cast<size_t>(k) * hd;
+          for (int i = 0; i < hd; ++i) acc[static_cast<size_t>(i)] += static_cast<double>(p) * vr[i];
+        }
+        uint16_t* o = out + static_cast<size_t>(r) * num_heads * hd + static_cast<size_t>(h) * hd;
+        for (int i = 0; i < hd; ++i) o[i] = f2e(static_cast<float>(acc[static_cast<size_t>(i)]), kind);
       }
-      double l = 0.0;
-      for (int k = 0; k < limit; ++k) l += std::exp(static_cast<double>(s[static_cast<size_t>(k)] - m));
-      const float inv = static_cast<float>(1.0 / l);
-      std::vector<double> acc(static_cast<size_t>(hd), 0.0);
-      for (int k = 0; k < limit; ++k) {
-        const float p = e2f(f2e(static_cast<float>(std::exp(static_cast<double>(s[static_cast<size_t>(k)] - m))) * inv, kind), kind);
-        const int64_t off = kv_off(*view, paged != 0, kv, k);
-        for (int i = 0; i < hd; ++i) acc[static_cast<size_t>(i)] += static_cast<double>(p) * e2f(view->values[off + i], kind);
-      }
-      uint16_t* o = out + static_cast<size_t>(r) * num_heads * hd + static_cast<size_t>(h) * hd;
-      for (int i = 0; i < hd; ++i) o[i] = f2e(static_cast<float>(acc[static_cast<size_t>(i)]), kind);
     }
   }
 }
@@ -784,8 +809,110 @@ void orc_gemv(int kind, void* y, int y_fp32, const uint16_t* W, const uint16_t* 
   gemv_rows(kind, y, y_fp32, W, x, N, K);
 }
 
+// Sixteen tokens of a bf16 GEMM at once: for every token the operation order
+// of dot_fixed_bf16 (blocks of 2048, lanes of 8-element fma chains, the 64-lane
+// butterfly, block sums left to right), vectorised over the tokens (two 8-wide
+// vectors per lane), so each weight row is converted and read once per sixteen
+// tokens. Bit-identical to sixteen gemv_rows calls. Of the butterfly only lane
+// 0 is used, and after the step with offset o lane i holds v[i] + v[i + o] for
+// i < o (and the same sum, commuted, for i >= o), so the reduction keeps the
+// lower half at each step. xT is the token block transposed, [K][16].
+constexpr int kTokenBlock = 16;
+
+void gemm_rows_bf16_block(int tokens, void* Y, int y_fp32, const uint16_t* W, const float* xT, int N,
+                          int K) {
+#pragma omp parallel
+  {
+    std::vector<float> wf(static_cast<size_t>(K));
+    alignas(32) float lanes[64][kTokenBlock];
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; ++n) {
+      const uint16_t* w = W + static_cast<size_t>(n) * K;
+      for (int k = 0; k < K; ++k) wf[static_cast<size_t>(k)] = bf16_to_f(w[k]);
+      alignas(32) float total[kTokenBlock] = {0};
+      const int blocks = (K + 2047) / 2048;
+      for (int b = 0; b < blocks; ++b) {
+        std::memset(lanes, 0, sizeof(lanes));
+        for (int c = 0; c < 4; ++c) {
+          const int base = b * 2048 + c * 512;
+          if (base >= K) break;
+          const int nl = std::min(64, (K - base) / 8);  // lanes whose chunk starts below K
+          int l0 = 0;
+          // Four lanes at a time: eight independent fma chains (two token
+          // halves per lane), each lane in its own element order.
+          for (; l0 + 4 <= nl; l0 += 4) {
+            __m256 a[4][2];
+            for (int q = 0; q < 4; ++q) {
+              a[q][0] = _mm256_load_ps(lanes[l0 + q]);
+              a[q][1] = _mm256_load_ps(lanes[l0 + q] + 8);
+            }
+            const int e0 = base + 8 * l0;
+            for (int j = 0; j < 8; ++j) {
+              for (int q = 0; q < 4; ++q) {
+                const int e = e0 + 8 * q + j;
+                const __m256 wv = _mm256_broadcast_ss(&wf[static_cast<size_t>(e)]);
+                const float* xr = xT + static_cast<size_t>(e) * kTokenBlock;
+                a[q][0] = _mm256_fmadd_ps(wv, _mm256_load_ps(xr), a[q][0]);
+                a[q][1] = _mm256_fmadd_ps(wv, _mm256_load_ps(xr + 8), a[q][1]);
+              }
+            }
+            for (int q = 0; q < 4; ++q) {
+              _mm256_store_ps(lanes[l0 + q], a[q][0]);
+              _mm256_store_ps(lanes[l0 + q] + 8, a[q][1]);
+            }
+          }
+          for (; l0 < nl; ++l0) {
+            __m256 lo = _mm256_load_ps(lanes[l0]);
+            __m256 hi = _mm256_load_ps(lanes[l0] + 8);
+            for (int j = 0; j < 8; ++j) {
+              const int e = base + 8 * l0 + j;
+              const __m256 wv = _mm256_broadcast_ss(&wf[static_cast<size_t>(e)]);
+              const float* xr = xT + static_cast<size_t>(e) * kTokenBlock;
+              lo = _mm256_fmadd_ps(wv, _mm256_load_ps(xr), lo);
+              hi = _mm256_fmadd_ps(wv, _mm256_load_ps(xr + 8), hi);
+            }
+            _mm256_store_ps(lanes[l0], lo);
+            _mm256_store_ps(lanes[l0] + 8, hi);
+          }
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+          for (int i = 0; i < o; ++i) {
+            _mm256_store_ps(lanes[i], _mm256_add_ps(_mm256_load_ps(lanes[i]), _mm256_load_ps(lanes[i + o])));
+            _mm256_store_ps(lanes[i] + 8,
+                            _mm256_add_ps(_mm256_load_ps(lanes[i] + 8), _mm256_load_ps(lanes[i + o] + 8)));
+          }
+        }
+        for (int t = 0; t < kTokenBlock; ++t) total[t] = (b == 0) ? lanes[0][t] : total[t] + lanes[0][t];
+      }
+      for (int t = 0; t < tokens; ++t) {
+        if (y_fp32) {
+          static_cast<float*>(Y)[static_cast<size_t>(t) * N + n] = total[t];
+        } else {
+          static_cast<uint16_t*>(Y)[static_cast<size_t>(t) * N + n] = f_to_bf16(total[t]);
+        }
+      }
+    }
+  }
+}
+
 void orc_gemm(int kind, void* Y, int y_fp32, const uint16_t* X, const uint16_t* W, int T, int N,
               int K) {
+  if (kind == ORC_BF16 && T > 1) {
+    float* xT = static_cast<float*>(std::aligned_alloc(32, static_cast<size_t>(K) * kTokenBlock * sizeof(float)));
+    for (int t0 = 0; t0 < T; t0 += kTokenBlock) {
+      const int tb = std::min(kTokenBlock, T - t0);
+      std::memset(xT, 0, static_cast<size_t>(K) * kTokenBlock * sizeof(float));
+      for (int t = 0; t < tb; ++t) {
+        const uint16_t* x = X + static_cast<size_t>(t0 + t) * K;
+        for (int k = 0; k < K; ++k) xT[static_cast<size_t>(k) * kTokenBlock + t] = bf16_to_f(x[k]);
+      }
+      void* yblock = y_fp32 ? static_cast<void*>(static_cast<float*>(Y) + static_cast<size_t>(t0) * N)
+                            : static_cast<void*>(static_cast<uint16_t*>(Y) + static_cast<size_t>(t0) * N);
+      gemm_rows_bf16_block(tb, yblock, y_fp32, W, xT, N, K);
+    }
+    std::free(xT);
+    return;
+  }
   for (int t = 0; t < T; ++t) {
     void* yrow = y_fp32 ? static_cast<void*>(static_cast<float*>(Y) + static_cast<size_t>(t) * N)
                         : static_cast<void*>(static_cast<uint16_t*>(Y) + static_cast<size_t>(t) * N);

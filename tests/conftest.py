@@ -53,3 +53,12 @@ def gpu(lcr):
     if lib.lcr_device_count() < 1:
         pytest.skip("no HIP device")
     return lib
+
+
+@pytest.fixture(scope="session")
+def full_ckpt(lcr, tmp_path_factory):
+    """The benchmark's full-size Llama-3.2-1B-architecture checkpoint (seeded
+    N(0, 0.02) bf16 weights), written once per test session."""
+    d = tmp_path_factory.mktemp("full_model")
+    lcr.write_synthetic_checkpoint(d, lcr.llama_config(), seed=lcr.WEIGHT_SEED)
+    return d

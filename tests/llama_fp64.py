@@ -105,11 +105,36 @@ def llama3_inv_freq(cfg: dict) -> np.ndarray:
     return np.where(medium, (1 - smooth) * out / factor + smooth * out, out)
 
 
-def forward(cfg: dict, w: dict, tokens, mistake: str | None = None, return_hidden: bool = False):
-    """Logits of every position of `tokens` (float64 [T, vocab]); with
-    return_hidden also the residual stream after the embedding and after each
-    layer, and the final normed rows."""
-    w = {k: np.asarray(v, dtype=np.float64) for k, v in w.items()}
+class _Float64View(dict):
+    """Tensors converted to float64 on first use and dropped from memory by
+    `release` (a full-size checkpoint in float64 would be 10 GB)."""
+
+    def __init__(self, source):
+        super().__init__()
+        self.source = source
+
+    def __missing__(self, name):
+        v = self.source[name]
+        if v.dtype == np.uint16:
+            v = oracle.bf16_bits_to_f32(np.asarray(v))
+        out = np.asarray(v, dtype=np.float64)
+        self[name] = out
+        return out
+
+    def release(self, prefix):
+        for k in [k for k in self if k.startswith(prefix)]:
+            del self[k]
+
+
+def forward(cfg: dict, w: dict, tokens, mistake: str | None = None, return_hidden: bool = False,
+            last_logits_only: bool = False):
+    """Logits of every position of `tokens` (float64 [T, vocab]; only the last
+    row's, [1, vocab], with last_logits_only); with return_hidden also the
+    residual stream after the embedding and after each layer, and the final
+    normed rows. `w` maps tensor names to float values or to bf16 bits
+    (uint16, e.g. the memory-mapped arrays of oracle.read_safetensors), and
+    is converted to float64 one layer at a time."""
+    w = _Float64View(w)
     H = cfg["hidden_size"]
     nh, nkv, hd = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
     G = nh // nkv
@@ -136,7 +161,7 @@ def forward(cfg: dict, w: dict, tokens, mistake: str | None = None, return_hidde
         return np.concatenate([lo * cos - hi * sin, hi * cos + lo * sin], axis=-1)
 
     E = w["model.embed_tokens.weight"]
-    x = E[tokens]
+    x = E[tokens].copy()
     hidden = [x.copy()]
     mask = np.triu(np.full((T, T), -np.inf), k=1)
     if mistake == "no_causal_mask":
@@ -165,22 +190,71 @@ def forward(cfg: dict, w: dict, tokens, mistake: str | None = None, return_hidde
             g_, u_ = u_, g_
         x = x + (g_ / (1 + np.exp(-g_)) * u_) @ w[p + "mlp.down_proj.weight"].T
         hidden.append(x.copy())
+        w.release(p)
     final = x if mistake == "no_final_norm" else rms(x, w["model.norm.weight"])
-    logits = final @ E.T
+    logits = (final[-1:] if last_logits_only else final) @ E.T
     if return_hidden:
         return logits, hidden, final
     return logits
 
 
 def drift(got, want) -> dict:
-    """The per-tensor agreement figures of the reference's validator
-    (tools/validate_main.cu:95-137): max-abs, rel-RMS and cosine."""
-    a = np.asarray(got, dtype=np.float64).ravel()
-    b = np.asarray(want, dtype=np.float64).ravel()
+    """The agreement figures of the reference's validator
+    (tools/validate_main.cu:95-137) for a [rows, width] tensor (a vector is
+    one row): max-abs, RMS of the error over RMS of the reference (rel-RMS),
+    and the smallest per-row cosine."""
+    a = np.asarray(got, dtype=np.float64)
+    b = np.asarray(want, dtype=np.float64)
+    assert a.size == b.size, (a.shape, b.shape)
+    width = b.shape[-1] if b.ndim > 1 else b.size
+    a = a.reshape(-1, width)
+    b = b.reshape(-1, width)
     d = a - b
-    nb = np.sqrt(np.mean(b * b))
+    rms_ref = float(np.sqrt(np.mean(b * b)))
+    rms_err = float(np.sqrt(np.mean(d * d)))
+    na = np.linalg.norm(a, axis=1)
+    nb = np.linalg.norm(b, axis=1)
+    live = (na > 0) & (nb > 0)
+    cos = np.einsum("ij,ij->i", a[live], b[live]) / (na[live] * nb[live])
     return {
         "max_abs": float(np.abs(d).max()),
-        "rel_rms": float(np.sqrt(np.mean(d * d)) / nb) if nb > 0 else float("inf"),
-        "cosine": float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b))),
+        "rms_error": rms_err,
+        "rel_rms": rms_err / rms_ref if rms_ref > 0 else 0.0,
+        "cosine": float(cos.min()) if cos.size else 1.0,
     }
+
+
+# How much less accurate than the oracle a prefill may be, layer by layer:
+# its rel-RMS distance to float64 within this factor of the oracle's (plus a
+# small floor for layers where both are tiny), and every row's cosine to
+# float64 at least COSINE_MIN.
+ACCURACY_FACTOR = 1.25
+ACCURACY_FLOOR = 1e-3
+COSINE_MIN = 0.999
+
+
+def accuracy_report(names, gpu_taps, gpu_logits, oracle_model, tokens, hidden, final, logits64):
+    """Per tensor: the GPU's and the oracle's drift from the float64 forward,
+    and the GPU's drift from the oracle. `hidden`, `final`, `logits64` come
+    from forward(..., return_hidden=True, last_logits_only=True)."""
+    rows = []
+    for i, name in enumerate(names):
+        exact = hidden[i] if i < len(hidden) else final
+        orc = oracle_model.tap(i, tokens)
+        rows.append((name, drift(gpu_taps[name], exact), drift(orc, exact), drift(gpu_taps[name], orc)))
+    return rows
+
+
+def check_accuracy(rows, logits_row):
+    """Asserts the bounds above for every tap row and for the logits row
+    (name, gpu-vs-fp64, oracle-vs-fp64, gpu-vs-oracle)."""
+    for name, g, o, _ in list(rows) + [logits_row]:
+        assert g["rel_rms"] <= ACCURACY_FACTOR * o["rel_rms"] + ACCURACY_FLOOR, (name, g, o)
+        assert g["cosine"] >= COSINE_MIN, (name, g)
+
+
+def format_report(rows) -> str:
+    lines = [f"{'tensor':11s} {'rel-RMS gpu':>12s} {'rel-RMS orc':>12s} {'gpu-orc':>9s} {'cos gpu':>9s}"]
+    for name, g, o, go in rows:
+        lines.append(f"{name:11s} {g['rel_rms']:12.4e} {o['rel_rms']:12.4e} {go['rel_rms']:9.2e} {g['cosine']:9.6f}")
+    return "\n".join(lines)

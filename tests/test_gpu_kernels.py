@@ -673,7 +673,13 @@ def test_argmax_ties_and_edges(gpu, orc):
         assert got == oracle.argmax(logits) == int(np.argmax(logits))
         logits[:] = 0.5
         assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0) == 0
-        logits[vocab - 1] = np.float32(-0.0)
+        # Signed zeros: the reference's order-preserving key
+        # (src/kernels/sampling.cu:37-40) ranks -0.0 below +0.0, so a +0.0
+        # after a run of -0.0 wins, and among -0.0 alone the first one does.
+        logits[:] = np.float32(-0.0)
+        assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0) == oracle.argmax(logits) == 0
+        logits[vocab - 1] = np.float32(0.0)
+        assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0) == oracle.argmax(logits) == vocab - 1
         logits[:] = -np.inf
         logits[vocab // 2] = -1e30
         assert gpu_sample(lib, logits, 0.0, 0, 1.0, 0.0) == vocab // 2

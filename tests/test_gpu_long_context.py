@@ -24,10 +24,8 @@ STEPS = 4
 
 
 @pytest.fixture(scope="module")
-def ckpt(lcr, tmp_path_factory):
-    d = tmp_path_factory.mktemp("long_context")
-    lcr.write_synthetic_checkpoint(d, lcr.llama_config(), seed=lcr.WEIGHT_SEED)
-    return d
+def ckpt(full_ckpt):
+    return full_ckpt
 
 
 def permuted_tables(layers: int, max_pages: int, seed: int) -> np.ndarray:

@@ -11,7 +11,10 @@ and a smaller vocabulary so the oracle finishes in seconds. On it:
   - paged page tables equal the oracle's in-order assignment;
   - the MFMA prefill path matches the oracle within 2e-2 on the logits and
     gives the same greedy continuation;
-  - activation taps of the unfused path equal the oracle's.
+  - activation taps: an MFMA prefill's within the reference validator's
+    bounds of the oracle's, an unfused decode step's bit for bit;
+  - the fused step for groups of 1, 2, 4 and 8 query heads per kv head, per
+    head and whole-group attention blocks, both cache layouts.
 """
 
 import numpy as np
@@ -70,12 +73,31 @@ def test_decode_bit_exact(lcr, small_ckpt, paged, mode):
     run_steps(m, o, prompt, 12)
 
 
-@pytest.mark.parametrize("splits", [3, 8])
-def test_decode_bit_exact_split_merge(lcr, small_ckpt, splits):
-    """Forced split counts exercise the fused last-block merge at small contexts."""
-    m, o = make_pair(lcr, small_ckpt, splits=splits, prefill_via_decode=1)
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("splits", [3, 8, 16, 64])
+def test_decode_bit_exact_split_merge(lcr, small_ckpt, splits, paged):
+    """Forced split counts exercise the split merge at small contexts; from 16
+    splits on, the step runs whole-group blocks (one block per kv head and
+    split serving its four query heads), in both cache layouts."""
+    m, o = make_pair(lcr, small_ckpt, splits=splits, paged=paged, prefill_via_decode=1)
     prompt = lcr.synthetic_tokens(70, m.vocab, seed=99)
     run_steps(m, o, prompt, 6, check_every=2)
+
+
+@pytest.mark.parametrize("kv_heads", [32, 16, 4])
+@pytest.mark.parametrize("splits", [1, 16])
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_bit_exact_group_sizes(lcr, tmp_path_factory, kv_heads, splits, paged):
+    """32 query heads on 32, 16 or 4 kv heads (groups of 1, 2 and 8; the
+    Llama-3.2-1B group of 4 runs everywhere else): per-head blocks at one
+    split; at 16 splits whole-group blocks of two heads (group 2) and two
+    blocks of four per group (group 8)."""
+    d = tmp_path_factory.mktemp(f"group_{kv_heads}")
+    ckpt = lcr.write_synthetic_checkpoint(d, lcr.llama_config(num_key_value_heads=kv_heads, **SMALL))
+    m, o = make_pair(lcr, ckpt, splits=splits, paged=paged, prefill_via_decode=1)
+    assert m.stats().fused == 1
+    prompt = lcr.synthetic_tokens(40, m.vocab, seed=kv_heads)
+    run_steps(m, o, prompt, 4, check_every=1)
 
 
 def test_paged_tables_match_oracle(lcr, small_ckpt):
@@ -159,9 +181,13 @@ def test_prefill_chunking(lcr, small_ckpt):
 
 
 def test_activation_taps_match_oracle(lcr, small_ckpt):
+    """Taps of a 70-token MFMA prefill against the oracle's chunked prefill
+    (the reference validator's figures and bounds), and of a decode step on
+    the unfused path, bit for bit against the oracle's decode path."""
+    from llama_fp64 import drift
     m, o = make_pair(lcr, small_ckpt, fused_decode=0)
     m.set_capture_activations(True)
-    prompt = lcr.synthetic_tokens(9, m.vocab)
+    prompt = lcr.synthetic_tokens(70, m.vocab)
     m.prefill(prompt)
     o.prefill(prompt)
     taps = m.taps()
@@ -170,7 +196,18 @@ def test_activation_taps_match_oracle(lcr, small_ckpt):
     for i, name in enumerate(names):
         ref = o.tap(i, len(prompt))
         assert taps[name].shape == ref.shape
-        assert np.abs(taps[name] - ref).max() <= 2e-2 * max(1.0, np.abs(ref).max()), name
+        dr = drift(taps[name], ref)
+        assert dr["rel_rms"] <= 0.02 and dr["cosine"] >= 0.999, (name, dr)
+    # one decode step after the prompt: unfused kernels, one row per tap
+    m2, o2 = make_pair(lcr, small_ckpt, fused_decode=0, prefill_via_decode=1)
+    m2.prefill(prompt)
+    o2.prefill(prompt, use_decode_path=True)
+    m2.set_capture_activations(True)
+    m2.decode(5)
+    o2.decode(5)
+    taps = m2.taps()
+    for i, name in enumerate(names):
+        expect_bits_equal(taps[name].view(np.uint32), o2.tap(i, 1).view(np.uint32), f"decode tap {name}")
 
 
 def test_model_errors(lcr, small_ckpt):

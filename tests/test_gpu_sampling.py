@@ -57,3 +57,44 @@ def test_fp16_paged_stochastic_sampling_matches_oracle(lcr, fp16_ckpt):
     assert len(set(tokens)) > STEPS // 4
     ref.close()
     m.close()
+
+
+def test_fp16_mfma_prefill_then_sampling_matches_oracle_on_exported_cache(lcr, fp16_ckpt):
+    """Config 5 as the benchmark runs it: the 512-token prompt prefilled on the
+    fp16 MFMA path, then 256 sampled tokens. The prefill logits are within the
+    reference validator's bounds of the oracle's fp16 chunked prefill and the
+    first draw picks the same id from them on both samplers; then the GPU's
+    cache is loaded into the oracle, and every later step's logits must be
+    bit-identical and every sampled id the same."""
+    from llama_fp64 import drift
+    cfg = lcr.llama_config()
+    prompt = lcr.synthetic_tokens(PROMPT, cfg["vocab_size"], seed=lcr.PROMPT_SEED, variant="fp16")
+    uniforms = lcr.philox_uniforms(UNIFORM_SEED, STEPS)
+    max_seq = PROMPT + STEPS + 1
+    m = lcr.Model(fp16_ckpt, variant="fp16", max_seq=max_seq, paged=1, page_size=16)
+    ref = oracle.OracleModel(fp16_ckpt, kind=oracle.FP16, max_seq=max_seq, prefill_chunk=PROMPT,
+                             multiprocessors=m.stats().multiprocessors)
+    ptr = m.prefill(prompt)
+    got = m.logits(ptr)
+    want = ref.prefill(prompt)
+    dr = drift(got, want)
+    assert dr["rel_rms"] <= 0.02 and dr["cosine"] >= 0.999, dr
+    tok = m.sample(ptr, T, TOP_K, TOP_P, uniforms[0])
+    assert tok == oracle.sample(got, T, TOP_K, TOP_P, uniforms[0])
+    for layer in range(cfg["num_hidden_layers"]):
+        k, v = m.kv_export(layer, PROMPT, cfg["num_key_value_heads"], cfg["head_dim"])
+        ref.set_kv(layer, k, v)
+    ref.set_position(PROMPT)
+    tokens = [tok]
+    for step in range(1, STEPS):
+        ptr = m.decode(tok)
+        want = ref.decode(tok)
+        got = m.logits(ptr)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"logits differ at step {step}"
+        u = uniforms[step]
+        tok = m.sample(ptr, T, TOP_K, TOP_P, u)
+        assert tok == oracle.sample(want, T, TOP_K, TOP_P, u), f"sampled id differs at step {step}"
+        tokens.append(tok)
+    assert len(set(tokens)) > STEPS // 4
+    ref.close()
+    m.close()

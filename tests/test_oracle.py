@@ -293,18 +293,23 @@ def test_gemv_random_vs_fp64(L):
     assert np.abs(y - want).max() <= 1e-5 * np.abs(want).max() + 1e-6
 
 
-def test_gemm_rows_equal_gemv(L):
-    r = rng(12)
-    T, N, K = 6, 40, 2048
+@pytest.mark.parametrize("T,N,K", [(6, 40, 2048), (13, 97, 2048), (37, 33, 8192), (9, 40, 2056), (17, 5, 4104)])
+@pytest.mark.parametrize("y_fp32", [0, 1])
+def test_gemm_rows_equal_gemv(L, T, N, K, y_fp32):
+    """The GEMM (blocked over eight tokens at a time) gives every row the
+    GEMV's bits, for token counts that leave a partial block and K that
+    leaves a partial 2048-element block."""
+    r = rng(12 + T)
     X = random_elems(r, (T, K))
     W = random_elems(r, (N, K), 0.02)
-    Y = np.zeros(T * N, dtype=np.uint16)
-    L.orc_gemm(BF16, Y.ctypes.data, 0, X.ctypes.data, W.ctypes.data, T, N, K)
+    dt = np.float32 if y_fp32 else np.uint16
+    Y = np.zeros(T * N, dtype=dt)
+    L.orc_gemm(BF16, Y.ctypes.data, y_fp32, X.ctypes.data, W.ctypes.data, T, N, K)
     for t in range(T):
-        y = np.zeros(N, dtype=np.uint16)
+        y = np.zeros(N, dtype=dt)
         row = np.ascontiguousarray(X[t])
-        L.orc_gemv(BF16, y.ctypes.data, 0, W.ctypes.data, row.ctypes.data, N, K)
-        assert np.array_equal(Y[t * N:(t + 1) * N], y)
+        L.orc_gemv(BF16, y.ctypes.data, y_fp32, W.ctypes.data, row.ctypes.data, N, K)
+        assert np.array_equal(Y[t * N:(t + 1) * N].view(np.uint8), y.view(np.uint8)), t
 
 
 # ---------------------------------------------------------------------------

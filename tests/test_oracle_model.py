@@ -99,3 +99,18 @@ def test_planted_mistakes_exceed_the_bounds(tiny, mistake):
         m.close()
     bad = F.forward(cfg, w, prompt, mistake=mistake)[-1]
     assert F.drift(logits, bad)["rel_rms"] > 5 * REL_RMS_MAX, mistake
+
+
+def test_oracle_chunked_prefill_is_chunk_size_invariant(tiny):
+    """Later chunks read the earlier chunks' keys and values from the cache,
+    rounded exactly as one pass would hold them, and every GEMM row is its
+    own: one pass and chunks of 5 or 16 give the same bits (so a one-chunk
+    oracle run stands for the reference's 256-token chunking)."""
+    cfg, d, w, prompt = tiny
+    outs = []
+    for chunk in (PROMPT_LEN, 16, 5):
+        m = oracle.OracleModel(d, max_seq=64, prefill_chunk=chunk)
+        outs.append(m.prefill(prompt))
+        m.close()
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))

@@ -23,15 +23,15 @@ The JSON line also carries:
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
                 profiles/, else null;
   cpu_baseline  the CPU oracle (oracle/, the restatement of the reference's
-                decode step) on this box's host cores: the same prompt is
-                prefilled untimed, then a bounded number of greedy decode steps
-                (decode + argmax) over the same context range is timed;
+                decode step) on this box's host cores, on the timed run's own
+                workload: it loads the GPU's KV cache after the prompt and
+                decodes greedily from the GPU's first token (all threads, then
+                one thread on a shorter sample; CPU model and GB/s reported);
   oracle_greedy_parity
-                the GPU's greedy sequence, with the prompt prefilled through the
-                decode path as the oracle's is, against the oracle's sequence
-                from that CPU run (the timed run's MFMA prefill is within
-                tolerance of the oracle, not bit-exact, so its continuation can
-                part from the oracle's at a near-tie).
+                the timed run's ids against that CPU run's (bit-exact decode
+                from the same cache gives the same sequence), and the first
+                token (from the MFMA prefill) against the oracle's chunked
+                prefill.
 
 --counters runs a short eager (un-captured) decode plus one device copy of
 256 MiB and prints a line: the program to put under rocprofv3 --pmc, where the
@@ -67,14 +67,14 @@ def load_package():
     return mod
 
 
-def checkpoint_dir(lcr, config, seed, fp16: bool = False) -> Path:
+def checkpoint_dir(lcr, config, seed, fp16: bool = False, variant: str = "bf16") -> Path:
     base = Path(os.environ.get("LCR_SYNTH_DIR", tempfile.gettempdir()))
     d = base / f"lcr_synth_llama32_1b_{'fp16' if fp16 else 'bf16'}_{seed}"
     st = d / "model.safetensors"
     stamp = d / "STAMP"
     want = json.dumps({"config": config, "seed": seed, "fp16": fp16})
     if not (st.exists() and stamp.exists() and stamp.read_text() == want):
-        lcr.write_synthetic_checkpoint(d, config, seed=seed, fp16=fp16)
+        lcr.write_synthetic_checkpoint(d, config, seed=seed, fp16=fp16, variant=variant)
         stamp.write_text(want)
     return d
 
@@ -93,53 +93,93 @@ def traffic_from_profiles():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(model_dir: Path, prompt, steps: int, max_seq: int):
-    sys.path.insert(0, str(REPO))
-    import oracle  # the checker, timed as the CPU baseline only
+def cpu_model_name() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+
+def oracle_from_gpu_cache(model_dir: Path, kv: list, prompt_len: int, max_seq: int):
+    """The CPU oracle holding the GPU's KV cache of the prefilled prompt (the
+    rows the timed run decoded from), positioned after the prompt."""
+    sys.path.insert(0, str(REPO))
+    import oracle  # the checker, and the CPU baseline's code
     ref = oracle.OracleModel(model_dir, max_seq=max_seq)
-    tok = oracle.argmax(ref.prefill(prompt, use_decode_path=True))  # untimed: fills the KV cache
-    tokens = [tok]
-    t0 = time.perf_counter()
-    done = 0
-    while done < steps:
-        tok = oracle.argmax(ref.decode(tok))
-        tokens.append(tok)
-        done += 1
-        if time.perf_counter() - t0 > CPU_BASELINE_SECONDS:
-            break  # bounded sample on a slow host
-    dt = time.perf_counter() - t0
-    ref.close()
-    steps = done
+    for layer, (k, v) in enumerate(kv):
+        ref.set_kv(layer, k, v)
+    ref.set_position(prompt_len)
+    return ref, oracle
+
+
+def cpu_baseline(model_dir: Path, prompt, first: int, kv: list, steps: int, max_seq: int,
+                 bytes_per_token: float, gpu_ids: list) -> tuple:
+    """The CPU oracle (the restatement of the reference's decode step, OpenMP
+    over GEMV rows) timed on this box's host cores on the timed GPU run's own
+    workload: greedy decode from the GPU's cache after the prompt, starting at
+    the GPU's first token, so its ids are also the parity check of the timed
+    sequence. All threads on up to `steps` steps (capped at
+    CPU_BASELINE_SECONDS), then one thread on a shorter sample."""
+    ref, oracle = oracle_from_gpu_cache(model_dir, kv, len(prompt), max_seq)
+    lib = oracle.load()
+    threads = lib.orc_threads()
     n = len(prompt)
-    return {
-        "value": steps / dt,
+
+    def run(count, cap_s):
+        ref.set_position(n)
+        tok = first
+        out = [tok]
+        t0 = time.perf_counter()
+        done = 0
+        while done < count:
+            tok = oracle.argmax(ref.decode(tok))
+            out.append(tok)
+            done += 1
+            if time.perf_counter() - t0 > cap_s:
+                break  # bounded sample on a slow host
+        return out, done, time.perf_counter() - t0
+
+    tokens, done, dt = run(steps, CPU_BASELINE_SECONDS)
+    lib.orc_set_threads(1)
+    _, done1, dt1 = run(max(1, min(steps, 16)), CPU_BASELINE_SECONDS / 3)
+    lib.orc_set_threads(threads)
+    ref.close()
+    cpu = {
+        "value": done / dt,
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{steps} greedy decode steps (decode + argmax) at context {n + 1}..{n + steps} after an "
-                  f"untimed {n}-token prefill of the same prompt and model (CPU oracle, OpenMP over GEMV "
-                  f"rows, {threads} threads)",
-        "ms_per_token": 1000.0 * dt / steps,
+        "sample": f"{done} greedy decode steps (decode + argmax) at context {n + 1}..{n + done}, from the timed GPU "
+                  f"run's KV cache after its {n}-token prefill (CPU oracle, OpenMP over GEMV rows, {threads} "
+                  f"threads); single thread: {done1} steps",
+        "ms_per_token": 1000.0 * dt / done,
+        "gbs": bytes_per_token / (dt / done) / 1e9,
         "seconds": dt,
-        "_tokens": tokens,  # the greedy sequence, compared with the GPU's below (not printed)
+        "cpu_model": cpu_model_name(),
+        "single_thread": {"value": done1 / dt1, "ms_per_token": 1000.0 * dt1 / done1,
+                          "gbs": bytes_per_token / (dt1 / done1) / 1e9, "steps": done1, "seconds": dt1},
     }
+    m = min(len(tokens), len(gpu_ids))
+    diverge = next((i for i in range(m) if tokens[i] != gpu_ids[i]), None)
+    parity = {"greedy_tokens_compared": m, "identical": diverge is None, "first_divergence": diverge,
+              "sequence": "the timed run's own ids (MFMA prefill, then the graph-replayed decode step) against "
+                          "the CPU oracle decoding from the GPU's exported KV cache"}
+    return cpu, parity
 
 
-def greedy_parity(lcr, model_dir: Path, prompt, steps: int, max_seq: int, oracle_tokens) -> dict:
-    """The GPU's greedy sequence with the prompt prefilled through the decode
-    path (bit-exact against the oracle, like the decode steps themselves)
-    against the oracle's sequence from the CPU baseline run."""
-    m = lcr.Model(model_dir, max_seq=max_seq, prefill_via_decode=1)
-    first = m.sample(m.prefill(prompt), 0.0)
-    ids, _ = m.generate_greedy(first, steps)
-    m.close()
-    gpu = [int(first)] + [int(x) for x in ids]
-    n = min(len(gpu), len(oracle_tokens))
-    diverge = next((i for i in range(n) if gpu[i] != oracle_tokens[i]), None)
-    return {"greedy_tokens_compared": n, "identical": diverge is None, "first_divergence": diverge,
-            "prefill": "decode path on the GPU and in the CPU oracle"}
+def prefill_first_token_parity(model_dir: Path, prompt, first: int, max_seq: int) -> dict:
+    """The timed run's first token (argmax of its MFMA prefill logits) against
+    the oracle's chunked prefill of the same prompt."""
+    sys.path.insert(0, str(REPO))
+    import oracle
+    ref = oracle.OracleModel(model_dir, max_seq=max_seq, prefill_chunk=len(prompt))
+    want = oracle.argmax(ref.prefill(prompt))
+    ref.close()
+    return {"first_token": int(first), "oracle_chunked_prefill_first_token": int(want),
+            "identical": int(first) == int(want)}
 
 
 def prefill_flops(config: dict, T: int) -> float:
@@ -211,7 +251,7 @@ def sampling_run(lcr, config: dict, prompt_len: int = 512, steps: int = 256) -> 
     token (src/main.cu:442-466). Timed on the host clock, with the per-token
     device-to-host copy of the sampled id inside; one untimed pass first."""
     cfg16 = lcr.llama_config(torch_dtype="float16")
-    d = checkpoint_dir(lcr, cfg16, lcr.WEIGHT_SEED, fp16=True)
+    d = checkpoint_dir(lcr, cfg16, lcr.WEIGHT_SEED, fp16=True, variant="fp16")
     prompt = lcr.synthetic_tokens(prompt_len, config["vocab_size"], seed=lcr.PROMPT_SEED, variant="fp16")
     uniforms = lcr.philox_uniforms(SAMPLING_UNIFORM_SEED, steps)
     m = lcr.Model(d, variant="fp16", max_seq=prompt_len + steps + 1, paged=1, page_size=16)
@@ -291,10 +331,17 @@ def main() -> int:
         return 2
 
     lcr = load_package()
+    config = lcr.llama_config()
+    if args.sampling:
+        # This process loads only the fp16 library.
+        if lcr.device_count("fp16") < 1:
+            print("no HIP device visible", file=sys.stderr)
+            return 1
+        print(json.dumps({"sampling_config5": sampling_run(lcr, config)}))
+        return 0
     if lcr.device_count() < 1:
         print("no HIP device visible", file=sys.stderr)
         return 1
-    config = lcr.llama_config()
     seed = args.seed if args.seed is not None else lcr.WEIGHT_SEED
     t0 = time.perf_counter()
     model_dir = checkpoint_dir(lcr, config, seed)
@@ -307,9 +354,6 @@ def main() -> int:
         return 0
     if args.long_context > 0:
         print(json.dumps({"long_context": long_context(lcr, model_dir, config, args.long_context)}))
-        return 0
-    if args.sampling:
-        print(json.dumps({"sampling_config5": sampling_run(lcr, config)}))
         return 0
     t0 = time.perf_counter()
     model = lcr.Model(model_dir, max_seq=args.max_seq)
@@ -329,6 +373,10 @@ def main() -> int:
     first = model.sample(logits, 0.0)
     ids, decode_ms = model.generate_greedy(first, args.steps)
     K = args.steps
+    timed_ids = [int(first)] + [int(x) for x in ids]
+    kv = ([] if args.no_cpu_baseline else
+          [model.kv_export(layer, args.prompt, config["num_key_value_heads"], config["head_dim"])
+           for layer in range(config["num_hidden_layers"])])
     ms_per_step = decode_ms / K
     tok_s = K / (decode_ms / 1000.0)
     mean_len = args.prompt + (K + 1) / 2.0
@@ -370,9 +418,9 @@ def main() -> int:
     cpu = None
     parity = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(model_dir, prompt, args.cpu_steps, args.max_seq)
-        parity = greedy_parity(lcr, model_dir, prompt, len(cpu["_tokens"]) - 1, args.max_seq,
-                               cpu.pop("_tokens"))
+        cpu, parity = cpu_baseline(model_dir, prompt, int(first), kv, args.cpu_steps, args.max_seq,
+                                   bytes_per_token, timed_ids)
+        parity["prefill"] = prefill_first_token_parity(model_dir, prompt, first, args.max_seq)
 
     result = {
         "metric": "decode tok/s + HBM GB/s (% of peak), Llama-3.2-1B-arch bf16 batch 1",
@@ -390,8 +438,9 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded random-init N(0,0.02) bf16 weights, norms 1.0; seeded uniform prompt ids)",
         "config": {
-            "workload": "config 2: 128-token prompt prefill + 255 greedy decode steps (256 generated tokens), "
-                        "batch 1, contiguous KV bf16 [16x2x8x2048x64], hipGraph-captured decode step",
+            "workload": f"config 2: {args.prompt}-token prompt (MFMA prefill, untimed) then {K} timed greedy "
+                        f"decode steps at context {args.prompt + 1}..{args.prompt + K}, batch 1, contiguous KV bf16 "
+                        f"[16x2x8x{args.max_seq}x64], hipGraph-captured decode step",
             "prompt_tokens": args.prompt,
             "decode_steps": K,
             "max_seq": args.max_seq,
@@ -422,7 +471,7 @@ def main() -> int:
         **extra,
         "cpu_baseline": cpu,
         "oracle_greedy_parity": parity,
-        "generated_first_ids": [int(x) for x in ids[:8]],
+        "generated_first_ids": timed_ids[:8],
         "setup_s": {"checkpoint": gen_s, "load": load_s},
         "reference_frac_of_peak": REFERENCE_PEAK_FRAC,
     }

@@ -115,6 +115,8 @@ SIGNATURES = {
     "orc_model_set_kv": (_I, [_P, _I, _I, _P, _P]),
     "orc_model_set_position": (_I, [_P, _I]),
     "orc_last_error": (ctypes.c_char_p, []),
+    "orc_set_threads": (None, [_I]),
+    "orc_threads": (_I, []),
 }
 
 

@@ -34,6 +34,7 @@
 #include "lcr_oracle.h"
 
 #include <immintrin.h>
+#include <omp.h>
 
 #include <algorithm>
 #include <cfloat>
@@ -503,6 +504,9 @@ inline uint32_t order_key(float v) {
 extern "C" {
 
 const char* orc_last_error(void) { return g_error.c_str(); }
+
+void orc_set_threads(int n) { omp_set_num_threads(n < 1 ? 1 : n); }
+int orc_threads(void) { return omp_get_max_threads(); }
 
 float orc_elem_to_float(uint16_t bits, int kind) { return e2f(bits, kind); }
 uint16_t orc_float_to_elem(float value, int kind) { return f2e(value, kind); }

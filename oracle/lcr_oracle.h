@@ -154,6 +154,10 @@ int orc_model_set_kv(orc_model* model, int layer, int positions, const uint16_t*
                      const uint16_t* values);
 int orc_model_set_position(orc_model* model, int position);
 const char* orc_last_error(void);
+/* OpenMP threads the oracle's parallel loops use from now on (n >= 1), and
+ * the current count. */
+void orc_set_threads(int n);
+int orc_threads(void);
 
 #ifdef __cplusplus
 }

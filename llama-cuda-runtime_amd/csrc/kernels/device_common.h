@@ -54,6 +54,23 @@ __device__ __forceinline__ vec16 load16_stream(const void* p) {
   return vec16{{v.x, v.y, v.z, v.w}};
 }
 
+// Direct global-to-LDS load (global_load_lds_dwordx4): lane L's 16 bytes from
+// `src` land at LDS byte address `lds_address` + 16 L (lds_address is the
+// wave's base, uniform across the wave). The load counts in the wave's
+// vector-memory counter like any other and leaves no registers busy; the
+// compiler does not see it as an LDS write, so a reader waits for it by hand
+// (vmcnt) and every read of the target is ordered after it by the memory
+// clobber.
+__device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds_address) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_address) : "memory");
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_address_of(const void* p) {
+  typedef const __attribute__((address_space(3))) char* lds_char_ptr;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char_ptr)p));
+}
+
 // The two elements packed in one 32-bit word (element 2i in the low half).
 __device__ __forceinline__ float elem_lo(uint32_t p) {
 #if defined(LCR_ELEM_FP16)

@@ -464,15 +464,6 @@ __global__ __launch_bounds__(64 * kWavesW * kWavesT) void gemm_nt_kernel(
 // count waits stricter.
 constexpr int kRingK = 32;
 
-__device__ __forceinline__ void load_to_lds16(const elem_t* src, uint32_t lds_address) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_address) : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_address_of(const elem_t* p) {
-  typedef const __attribute__((address_space(3))) elem_t* lds_elem_ptr;
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_elem_ptr)p));
-}
-
 // Wait until at most kCount vector-memory operations of this wave are in
 // flight and every LDS read has returned (gfx9 encoding: vmcnt bits 3:0 and
 // 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 zero).

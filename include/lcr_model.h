@@ -120,6 +120,10 @@ int lcr_model_kv_export(const lcr_model* model, int layer, int positions, void* 
 int lcr_write_synthetic_checkpoint(const char* dir, const char* config_json, uint64_t seed,
                                    float stddev, int fp16, int threads);
 int lcr_synthetic_tokens(uint64_t seed, int count, int vocab, int32_t* out);
+/* extension: `count` draws of the Philox4x32-10 uniform stream of `seed` (the
+ * sampling draws of llama-run and of the sampling tests); see
+ * llama-cuda-runtime_amd/csrc/philox.h. */
+int lcr_philox_uniforms(uint64_t seed, int count, float* out);
 
 /* Number of visible HIP devices (0 without a GPU; never an error). */
 int lcr_device_count(void);

@@ -183,7 +183,19 @@ SIGNATURES = {
     "lcr_model_kv_export": (_I, [_P, _I, _I, _P, _P]),
     "lcr_write_synthetic_checkpoint": (_I, [ctypes.c_char_p, ctypes.c_char_p, _U64, _F, _I, _I]),
     "lcr_synthetic_tokens": (_I, [_U64, _I, _I, _P]),
+    "lcr_philox_uniforms": (_I, [_U64, _I, _P]),
     "lcr_device_count": (_I, []),
+    # lcr_tokenizer.h
+    "lcr_tokenizer_create": (_P, [ctypes.c_char_p]),
+    "lcr_tokenizer_create_from_json": (_P, [ctypes.c_char_p, _SZ]),
+    "lcr_tokenizer_destroy": (None, [_P]),
+    "lcr_tokenizer_encode": (_I, [_P, ctypes.c_char_p, _SZ, _I, _I, _P, _SZ, ctypes.POINTER(_SZ)]),
+    "lcr_tokenizer_decode": (_I, [_P, _P, _SZ, _I, _P, _SZ, ctypes.POINTER(_SZ)]),
+    "lcr_tokenizer_vocab_size": (_I, [_P]),
+    "lcr_tokenizer_bos_id": (_I, [_P]),
+    "lcr_tokenizer_token_to_id": (_I, [_P, ctypes.c_char_p, _SZ]),
+    "lcr_tokenizer_is_special": (_I, [_P, _I]),
+    "lcr_split_pretokens": (_I, [ctypes.c_char_p, _SZ, _P, _SZ, ctypes.POINTER(_SZ)]),
     # lcr_runtime.h
     "lcr_device_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
     "lcr_device_free": (_I, [_P]),
@@ -229,6 +241,90 @@ def check(lib, status: int, what: str = "") -> None:
 
 def device_count(variant: str = "bf16") -> int:
     return int(load_library(variant).lcr_device_count())
+
+
+class Tokenizer:
+    """The byte-level BPE tokenizer (include/lcr_tokenizer.h) from a
+    tokenizer.json path or its text. No GPU is involved."""
+
+    def __init__(self, path=None, json_text: Optional[str] = None, variant: str = "bf16"):
+        self.lib = load_library(variant)
+        if json_text is not None:
+            raw = json_text.encode()
+            self.handle = self.lib.lcr_tokenizer_create_from_json(raw, len(raw))
+        else:
+            self.handle = self.lib.lcr_tokenizer_create(str(path).encode())
+        if not self.handle:
+            raise LcrError(self.lib.lcr_last_error_message().decode(errors="replace"))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.lcr_tokenizer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, text, add_bos: bool = False, parse_special: bool = True) -> list:
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        cap = len(raw) + 8
+        while True:
+            out = (ctypes.c_int32 * cap)()
+            n = ctypes.c_size_t()
+            st = self.lib.lcr_tokenizer_encode(self.handle, raw, len(raw), int(add_bos), int(parse_special), out,
+                                               cap, ctypes.byref(n))
+            if st == 0:
+                return list(out[:n.value])
+            if n.value <= cap:
+                check(self.lib, st, "tokenizer encode")
+            cap = n.value
+
+    def decode(self, ids, skip_special: bool = False) -> bytes:
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        cap = 16 * len(ids) + 16
+        while True:
+            buf = ctypes.create_string_buffer(cap)
+            n = ctypes.c_size_t()
+            st = self.lib.lcr_tokenizer_decode(self.handle, arr, len(ids), int(skip_special), buf, cap,
+                                               ctypes.byref(n))
+            if st == 0:
+                return buf.raw[:n.value]
+            if n.value <= cap:
+                check(self.lib, st, "tokenizer decode")
+            cap = n.value
+
+    @property
+    def vocab_size(self) -> int:
+        return int(self.lib.lcr_tokenizer_vocab_size(self.handle))
+
+    @property
+    def bos_id(self) -> int:
+        return int(self.lib.lcr_tokenizer_bos_id(self.handle))
+
+    def token_to_id(self, token: str) -> int:
+        raw = token.encode()
+        return int(self.lib.lcr_tokenizer_token_to_id(self.handle, raw, len(raw)))
+
+    def is_special(self, i: int) -> bool:
+        return bool(self.lib.lcr_tokenizer_is_special(self.handle, i))
+
+
+def split_pretokens(text, variant: str = "bf16") -> list:
+    """The Llama 3 pretokenizer split (bytes pieces)."""
+    lib = load_library(variant)
+    raw = text.encode() if isinstance(text, str) else bytes(text)
+    cap = len(raw) + 1
+    ends = (ctypes.c_size_t * cap)()
+    n = ctypes.c_size_t()
+    check(lib, lib.lcr_split_pretokens(raw, len(raw), ends, cap, ctypes.byref(n)), "split_pretokens")
+    out, start = [], 0
+    for i in range(n.value):
+        out.append(raw[start:ends[i]])
+        start = ends[i]
+    return out
 
 
 def write_synthetic_checkpoint(directory, config: Optional[dict] = None, seed: int = WEIGHT_SEED,

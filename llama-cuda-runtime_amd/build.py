@@ -5,6 +5,9 @@ Two variants, as the reference's LCR_DTYPE switch gives two builds
   liblcr_amd.so       bf16 elements (default)
   liblcr_amd_fp16.so  fp16 elements (-DLCR_ELEM_FP16)
 
+The command-line programs of csrc/tools/ (llama-run, lcr-validate,
+lcr-inspect, lcr-tokenize) are linked against those libraries into bin/.
+
 Every source is compiled with hipcc for gfx950 only, with -ffp-contract=off so
 that only the explicit fma calls in the kernels are fused (the kernels'
 summation orders are part of their contract), and with packed fp32 operations
@@ -99,11 +102,52 @@ def build_variant(name: str, jobs: int) -> Path:
     return lib
 
 
+# Command-line programs (csrc/tools/<name>_main.cpp), linked against the bf16
+# library (the fp16 build when its name ends in -fp16), into bin/.
+TOOLS = {
+    "llama-run": ("run_main.cpp", "bf16"),
+    "llama-run-fp16": ("run_main.cpp", "fp16"),
+    "lcr-validate": ("validate_main.cpp", "bf16"),
+    "lcr-inspect": ("inspect_main.cpp", "bf16"),
+    "lcr-tokenize": ("tokenize_main.cpp", "bf16"),
+}
+
+
+def _build_tool(name: str, source: str, variant: str) -> tuple[str, int, str]:
+    lib_name, defines = VARIANTS[variant]
+    out = PKG / "bin" / name
+    out.parent.mkdir(exist_ok=True)
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [HIPCC, *COMMON_FLAGS, *defines, "-x", "hip", str(CSRC / "tools" / source), "-o", str(tmp),
+           f"-L{PKG}", f"-l:{lib_name}", "-Wl,-rpath,$ORIGIN/.."]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    text = "\n".join(line for line in (proc.stdout + proc.stderr).splitlines() if "packed-fp32-ops" not in line)
+    if proc.returncode == 0:
+        os.replace(tmp, out)
+    return name, proc.returncode, text
+
+
+def build_tools(variants: list[str], jobs: int) -> list[Path]:
+    todo = [(n, s, v) for n, (s, v) in TOOLS.items() if v in variants]
+    failures = []
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        for name, rc, text in pool.map(lambda t: _build_tool(*t), todo):
+            if text.strip():
+                print(f"[{name}]:\n{text}", file=sys.stderr)
+            if rc != 0:
+                failures.append(name)
+    if failures:
+        raise RuntimeError(f"tools failed to build: {', '.join(failures)}")
+    return [PKG / "bin" / n for n, _, _ in todo]
+
+
 def build(variants: list[str] | None = None, jobs: int | None = None) -> list[Path]:
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     jobs = jobs or min(16, os.cpu_count() or 4)
-    return [build_variant(v, jobs) for v in (variants or list(VARIANTS))]
+    variants = variants or list(VARIANTS)
+    libs = [build_variant(v, jobs) for v in variants]
+    return libs + build_tools(variants, jobs)
 
 
 def main() -> int:

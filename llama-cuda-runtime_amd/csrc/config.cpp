@@ -216,6 +216,16 @@ std::vector<WeightSpec> required_weights(const ModelConfig& c) {
   return out;
 }
 
+size_t weight_bytes_per_token(const ModelConfig& config, size_t elem_size) {
+  size_t elements = 0;
+  for (const WeightSpec& w : required_weights(config)) {
+    size_t n = 1;
+    for (int64_t d : w.shape) n *= static_cast<size_t>(d);
+    elements += n;  // the embedding's count stands for the output head's
+  }
+  return elements * elem_size;
+}
+
 // The llama3 band rule of the reference's src/config.cpp:223-259: a pair whose
 // wavelength is shorter than original_context/high_freq_factor keeps its
 // frequency, one longer than original_context/low_freq_factor is divided by

@@ -69,6 +69,13 @@ struct WeightSpec {
 // not listed: it is lm_head.weight if present, else the tied embedding).
 std::vector<WeightSpec> required_weights(const ModelConfig& config);
 
+// Weight bytes one decoded token streams, the reference's accounting
+// (src/model.cu:86-102): every tensor of required_weights() once, except that
+// the step reads one row of the embedding table and all of the output head,
+// which has the embedding's shape (tied or not). 2,471,628,800 for
+// Llama-3.2-1B in bf16.
+size_t weight_bytes_per_token(const ModelConfig& config, size_t elem_size);
+
 // head_dim/2 inverse frequencies, computed in double and rounded to float once,
 // with the llama3 bands applied when the config enables them.
 std::vector<float> compute_rope_inv_freq(const ModelConfig& config);

@@ -65,20 +65,7 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
   }
 
   stats_.kv_bytes_per_position = config_.kv_bytes_per_token(sizeof(elem_t));
-  // Weight bytes streamed per decoded token, counted as the reference does
-  // (src/model.cu:86-102): every projection, both norms per layer, the final
-  // norm and the output head; one embedding row is not counted.
-  size_t per_token = 0;
-  for (int layer = 0; layer < config_.num_layers; ++layer) {
-    per_token += static_cast<size_t>(config_.hidden_size) * 2;
-    per_token += static_cast<size_t>(config_.q_dim()) * config_.hidden_size;
-    per_token += static_cast<size_t>(config_.kv_dim()) * config_.hidden_size * 2;
-    per_token += static_cast<size_t>(config_.hidden_size) * config_.q_dim();
-    per_token += static_cast<size_t>(config_.intermediate_size) * config_.hidden_size * 3;
-  }
-  per_token += config_.hidden_size;
-  per_token += static_cast<size_t>(config_.vocab_size) * config_.hidden_size;
-  stats_.weight_bytes_per_token = per_token * sizeof(elem_t);
+  stats_.weight_bytes_per_token = weight_bytes_per_token(config_, sizeof(elem_t));
 }
 
 Model::~Model() {

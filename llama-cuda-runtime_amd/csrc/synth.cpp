@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "capi_util.h"
+#include "philox.h"
 #include "config.h"
 #include "dtype.h"
 #include "safetensors.h"
@@ -125,5 +126,13 @@ extern "C" int lcr_synthetic_tokens(uint64_t seed, int count, int vocab, int32_t
     const uint64_t hi = h >> 32;
     out[i] = static_cast<int32_t>((hi * static_cast<uint64_t>(vocab)) >> 32);
   }
+  return LCR_OK;
+}
+
+extern "C" int lcr_philox_uniforms(uint64_t seed, int count, float* out) {
+  capi::clear_error();
+  CAPI_CHECK(count >= 0 && (count == 0 || out != nullptr), "philox draws need an output buffer");
+  PhiloxUniforms draws(seed);
+  for (int i = 0; i < count; ++i) out[i] = draws.next();
   return LCR_OK;
 }

@@ -361,6 +361,14 @@ void test_kv_geometry() {
   // per-position accounting.
   EXPECT_EQ(lcr::KvCache::bytes_for(c, 1), static_cast<size_t>(32768));
   EXPECT_THROWS("positive maximum sequence length", { lcr::KvGeometry::plan(c, 0, lcr::KvLayout::kPaged, 16); });
+  // The reference's per-token byte accounting (src/model.cu:86-102), written
+  // out for Llama-3.2-1B: per layer two norms, q, k and v, o, gate/up/down;
+  // then the final norm and the output head.
+  const size_t H = 2048, Q = 2048, KV = 512, F = 8192, V = 128256;
+  const size_t per_layer = 2 * H + Q * H + 2 * KV * H + H * Q + 3 * F * H;
+  EXPECT_EQ(lcr::weight_bytes_per_token(c, 2), (16 * per_layer + H + V * H) * 2);
+  EXPECT_EQ(lcr::weight_bytes_per_token(c, 2), static_cast<size_t>(2471628800));
+  EXPECT_EQ(c.kv_bytes_per_token(2), static_cast<size_t>(32768));
   EXPECT_THROWS("positive page size", { lcr::KvGeometry::plan(c, 64, lcr::KvLayout::kPaged, 0); });
 }
 

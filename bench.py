@@ -326,7 +326,7 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build measures the single-MI355X token loop "
-              f"(--gpus {args.gpus} is not supported; the multi-GPU design is described in DESIGN.md)",
+              f"(--gpus {args.gpus} is not supported: batch-1 decode is measured on one GPU's share)",
               file=sys.stderr)
         return 2
 

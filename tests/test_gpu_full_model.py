@@ -147,8 +147,8 @@ def test_mfma_prefill_then_decode_matches_oracle_on_exported_cache(lcr, full_ckp
 @pytest.mark.xfail(strict=False, reason=(
     "2e-2 max-abs on full-model logits is below the distance between the oracle's own two prefill paths "
     "(chunked vs decode, ~0.105 here): any fp32-accumulating prefill that is not bit-identical to the oracle's "
-    "sits about that far from it. The MFMA prefill is held to the reference validator's rel-RMS/cosine "
-    "bounds instead (test above)."))
+    "sits about that far from it, and the oracle itself is ~0.1 max-abs from a float64 forward here. The MFMA "
+    "prefill is held to the oracle's own accuracy against float64, layer by layer (test above)."))
 def test_mfma_prefill_logits_within_north_star_max_abs(lcr, full_ckpt, fixture):
     prompt = fixture["prompt"]
     m = lcr.Model(full_ckpt, max_seq=2048)

@@ -322,6 +322,12 @@ def main() -> int:
     ap.add_argument("--sampling", action="store_true",
                     help="only run the config 5 fp16 stochastic-sampling loop and print its JSON")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the prefill and the timed graph-replayed decode steps, for a kernel trace "
+                         "in which every decode kernel is an in-step dispatch")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --decode-only: enqueue each step's kernels directly instead of replaying the "
+                         "captured graph (the kernels and their order are the same)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -356,7 +362,7 @@ def main() -> int:
         print(json.dumps({"long_context": long_context(lcr, model_dir, config, args.long_context)}))
         return 0
     t0 = time.perf_counter()
-    model = lcr.Model(model_dir, max_seq=args.max_seq)
+    model = lcr.Model(model_dir, max_seq=args.max_seq, use_graph=0 if args.eager else 1)
     load_s = time.perf_counter() - t0
     st = model.stats()
     assert st.fused == 1, "the benchmark measures the fused decode step"
@@ -382,6 +388,12 @@ def main() -> int:
     mean_len = args.prompt + (K + 1) / 2.0
     bytes_per_token = st.weight_bytes_per_token + mean_len * st.kv_bytes_per_position
     achieved_gbs = bytes_per_token / (ms_per_step / 1000.0) / 1e9
+    if args.decode_only:
+        model.close()
+        print(json.dumps({"decode_only": {"steps": K, "warmup": args.warmup, "ms_per_step": ms_per_step,
+                                          "tok_s": tok_s, "gbs": achieved_gbs,
+                                          "launch": "eager" if args.eager else "graph"}}))
+        return 0
 
     # Reference-style loop: synchronous decode() calls from the host, one per
     # token (src/main.cu:456-466 times decode() only).

@@ -19,7 +19,7 @@
 //    i + head_dim/2 of a head), SwiGLU in the gate/up epilogue (a wave owns
 //    gate row i and up row i), the residual join in the o_proj and down
 //    epilogues;
-//  - the split-K merge runs in the last attention block of each kv head;
+//  - the split-K partials are merged by a separate kernel (long contexts);
 //  - lm_head writes fp32 logits and per-block argmax partials.
 #pragma once
 

@@ -54,6 +54,12 @@ __device__ __forceinline__ vec16 load16_stream(const void* p) {
   return vec16{{v.x, v.y, v.z, v.w}};
 }
 
+// Makes a loaded value live here. A load whose only use is in a branch at the
+// end of a kernel is otherwise moved into that branch, after the loads it
+// was meant to overlap, and costs a whole memory round trip of its own there.
+// Called after the loads issued behind it, it waits only for them to arrive.
+__device__ __forceinline__ void hold_value(float v) { asm volatile("" : : "v"(v)); }
+
 // Direct global-to-LDS load (global_load_lds_dwordx4): lane L's 16 bytes from
 // `src` land at LDS byte address `lds_address` + 16 L (lds_address is the
 // wave's base, uniform across the wave). The load counts in the wave's

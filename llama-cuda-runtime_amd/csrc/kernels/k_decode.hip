@@ -289,10 +289,13 @@ __global__ __launch_bounds__(WAVES * 64) void proj_residual_kernel(DecodeStepArg
   GemvTile<1, NCH> tile;
   const elem_t* rows[1] = {W + static_cast<size_t>(row) * K};
   tile.load(rows, lane);
-  // The residual entry this wave finishes, fetched while the weights stream.
+  // The residual entry this wave finishes, fetched while the weights stream
+  // (held: the compiler would otherwise load it after the products, in the
+  // lane-0 branch, a round trip of its own: down 7.41 -> 7.0 us when held).
   const float vold = a.resid[row];
   vec16 xv[NCH];
   load_x_global<NCH>(xv, x, lane);
+  hold_value(vold);
   float out[1];
   tile.dot(out, xv);
   if (lane == 0) {

@@ -247,9 +247,15 @@ def sampling_run(lcr, config: dict, prompt_len: int = 512, steps: int = 256) -> 
     """the fp16 build, a paged cache of 16-token
     pages, a seeded 512-token prompt (MFMA prefill), then `steps` tokens
     sampled at temperature 0.8, top-k 40, top-p 0.95 with one Philox uniform
-    per token, through the reference's host loop of decode() + sample() per
-    token (src/main.cu:442-466). Timed on the host clock, with the per-token
-    device-to-host copy of the sampled id inside; one untimed pass first."""
+    per token. Two loops, same draws, same ids (checked):
+      - the reference's host loop of decode() + sample() per token
+        (src/main.cu:442-466), timed on the host clock with the per-token
+        device-to-host copy of the sampled id inside;
+      - the same loop kept on the device (generate_sampled: the first id from
+        the prefill's logits on the host, then steps - 1 captured
+        decode + sample steps), timed with hipEvents on the model's stream,
+        as config 2's greedy loop is. This one is `tok_s`.
+    One untimed pass of each first."""
     cfg16 = lcr.llama_config(torch_dtype="float16")
     d = checkpoint_dir(lcr, cfg16, lcr.WEIGHT_SEED, fp16=True, variant="fp16")
     prompt = lcr.synthetic_tokens(prompt_len, config["vocab_size"], seed=lcr.PROMPT_SEED, variant="fp16")
@@ -270,19 +276,58 @@ def sampling_run(lcr, config: dict, prompt_len: int = 512, steps: int = 256) -> 
         seconds = time.perf_counter() - t0
         return ids, seconds, prefill_ms
 
+    def run_device():
+        first = m.sample(m.prefill(prompt), SAMPLING_T, SAMPLING_TOP_K, SAMPLING_TOP_P, uniforms[0])
+        rest, ms = m.generate_sampled(first, steps - 1, SAMPLING_T, SAMPLING_TOP_K, SAMPLING_TOP_P, uniforms[1:])
+        return [int(first)] + [int(x) for x in rest], ms
+
     run()
     m.reset()
     ids, seconds, prefill_ms = run()
+    m.reset()
+    run_device()
+    m.reset()
+    dev_ids, dev_ms = run_device()
     st = m.stats()
     m.close()
     mean_len = prompt_len + steps / 2.0
     bytes_per_token = st.weight_bytes_per_token + mean_len * st.kv_bytes_per_position
-    ms = seconds * 1000.0 / steps
+    host_ms = seconds * 1000.0 / steps
+    ms = dev_ms / (steps - 1)  # one decode + one sample per step
     return {"prompt_tokens": prompt_len, "sampled_tokens": steps, "temperature": SAMPLING_T,
             "top_k": SAMPLING_TOP_K, "top_p": SAMPLING_TOP_P, "prefill_ms": prefill_ms,
             "ms_per_token": ms, "tok_s": 1000.0 / ms,
             "token_gbs": bytes_per_token / (ms / 1000.0) / 1e9,
+            "host_loop_ms_per_token": host_ms, "host_loop_tok_s": 1000.0 / host_ms,
+            "device_loop_ids_equal_host_loop": dev_ids == [int(x) for x in ids],
             "distinct_ids": len(set(ids)), "first_ids": [int(x) for x in ids[:8]]}
+
+
+def sampler_calls(lcr, config: dict, calls: int) -> dict:
+    """`calls` eager lcr_sample calls (T = 0.8, top-k 40, top-p 0.95, one
+    Philox draw each) on one set of seeded N(0, 3) logits of the model's
+    vocabulary, for a profiler's view of the sampler's kernels; the host
+    clock time per call includes the launches."""
+    import ctypes
+    import numpy as np
+    lib = lcr.load_library()
+    V = config["vocab_size"]
+    logits = (np.random.default_rng(1).standard_normal(V) * 3).astype(np.float32)
+    d = lcr.DeviceBuffer.from_array(logits)
+    scratch = lcr.DeviceBuffer(lib.lcr_sample_scratch_floats(V, SAMPLING_TOP_K) * 4)
+    out = lcr.DeviceBuffer(16)
+    draws = lcr.philox_uniforms(SAMPLING_UNIFORM_SEED, calls)
+    ids = []
+    lcr.synchronize()
+    t0 = time.perf_counter()
+    for i in range(calls):
+        lcr.check(lib, lib.lcr_sample(ctypes.c_void_p(out.ptr), ctypes.c_void_p(d.ptr), V, SAMPLING_T,
+                                      SAMPLING_TOP_K, SAMPLING_TOP_P, draws[i], ctypes.c_void_p(scratch.ptr), None),
+                  "sample")
+    lcr.synchronize()
+    seconds = time.perf_counter() - t0
+    ids.append(int(out.to_numpy(np.int32, 1)[0]))
+    return {"calls": calls, "us_per_call_host": seconds * 1e6 / calls, "last_id": ids[-1]}
 
 
 def counters_run(lcr, model_dir: Path, prompt, max_seq: int) -> int:
@@ -322,6 +367,8 @@ def main() -> int:
     ap.add_argument("--sampling", action="store_true",
                     help="only run the config 5 fp16 stochastic-sampling loop and print its JSON")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sampler-calls", type=int, default=0, metavar="N",
+                    help="only run N eager stochastic lcr_sample calls on synthetic logits (for profiling)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the prefill and the timed graph-replayed decode steps, for a kernel trace "
                          "in which every decode kernel is an in-step dispatch")
@@ -338,6 +385,9 @@ def main() -> int:
 
     lcr = load_package()
     config = lcr.llama_config()
+    if args.sampler_calls > 0:
+        print(json.dumps({"sampler_calls": sampler_calls(lcr, config, args.sampler_calls)}))
+        return 0
     if args.sampling:
         # This process loads only the fp16 library.
         if lcr.device_count("fp16") < 1:

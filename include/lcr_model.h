@@ -85,6 +85,15 @@ int lcr_model_set_profiling(lcr_model* model, int enabled);
  * `steps` generated ids and the elapsed GPU time of the loop. */
 int lcr_model_generate_greedy(lcr_model* model, int32_t first_token, int steps,
                               int32_t* out_tokens, double* elapsed_ms);
+/* extension: the reference's sampled host loop (src/main.cu:456-466: decode,
+ * then Model::sample with the next draw) kept on the device. Decodes
+ * first_token, samples with uniforms[0] (temperature > 0, top_k, top_p as
+ * lcr_model_sample), feeds the id to the next step, ...: `steps` decodes,
+ * the `steps` sampled ids written out, the same ids as decode + sample with
+ * the same draws, and the elapsed GPU time of the loop. */
+int lcr_model_generate_sampled(lcr_model* model, int32_t first_token, int steps, float temperature,
+                               int top_k, float top_p, const float* uniforms, int32_t* out_tokens,
+                               double* elapsed_ms);
 /* extension: the split count decode uses at a sequence length. */
 int lcr_model_decode_splits(const lcr_model* model, int seq_len);
 /* extension: times one fused decode kernel in isolation ("qkv", "attention",

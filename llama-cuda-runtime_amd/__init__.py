@@ -171,6 +171,8 @@ SIGNATURES = {
     "lcr_model_tap": (_I, [_P, _I, ctypes.c_char_p, _SZ, ctypes.POINTER(_I), ctypes.POINTER(_I), _P, _SZ]),
     "lcr_model_set_profiling": (_I, [_P, _I]),
     "lcr_model_generate_greedy": (_I, [_P, ctypes.c_int32, _I, _P, ctypes.POINTER(ctypes.c_double)]),
+    "lcr_model_generate_sampled": (_I, [_P, ctypes.c_int32, _I, _F, _I, _F, _P, _P,
+                                        ctypes.POINTER(ctypes.c_double)]),
     "lcr_model_decode_splits": (_I, [_P, _I]),
     "lcr_model_time_decode_kernel": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_double)]),
@@ -518,6 +520,22 @@ class Model:
         check(self.lib, self.lib.lcr_model_generate_greedy(self.handle, int(first_token), int(steps),
                                                            out.ctypes.data, ctypes.byref(ms)),
               "generate_greedy")
+        return out, ms.value
+
+    def generate_sampled(self, first_token: int, steps: int, temperature: float, top_k: int, top_p: float,
+                         uniforms):
+        """The reference's decode + sample loop on the device (uniforms[i] is
+        the draw of the i-th sampled id)."""
+        import numpy as np
+        u = np.ascontiguousarray(np.asarray(uniforms, dtype=np.float32))
+        if u.size < steps:
+            raise LcrError(f"{steps} steps need {steps} draws, got {u.size}")
+        out = np.zeros(steps, dtype=np.int32)
+        ms = ctypes.c_double()
+        check(self.lib, self.lib.lcr_model_generate_sampled(self.handle, int(first_token), int(steps),
+                                                            float(temperature), int(top_k), float(top_p),
+                                                            u.ctypes.data, out.ctypes.data, ctypes.byref(ms)),
+              "generate_sampled")
         return out, ms.value
 
     def time_decode_kernel(self, kernel: str, launches: int = 64):

@@ -187,6 +187,20 @@ extern "C" int lcr_model_generate_greedy(lcr_model* m, int32_t first_token, int 
   });
 }
 
+extern "C" int lcr_model_generate_sampled(lcr_model* m, int32_t first_token, int steps, float temperature,
+                                          int top_k, float top_p, const float* uniforms, int32_t* out_tokens,
+                                          double* elapsed_ms) {
+  CAPI_MODEL(m);
+  CAPI_CHECK(steps >= 0 && (steps == 0 || (out_tokens != nullptr && uniforms != nullptr)),
+             "sampled generation needs one draw per step and an output array");
+  return capi::guarded([&]() -> int {
+    const std::vector<int> ids =
+        M(m).generate_sampled(first_token, steps, temperature, top_k, top_p, uniforms, elapsed_ms);
+    for (int i = 0; i < steps; ++i) out_tokens[i] = ids[static_cast<size_t>(i)];
+    return LCR_OK;
+  });
+}
+
 extern "C" int lcr_model_time_decode_kernel(lcr_model* m, const char* kernel, int launches,
                                             double* avg_ms, double* bytes_per_launch) {
   CAPI_MODEL(m);

@@ -91,4 +91,18 @@ void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t stream, bool with_
 
 int lm_head_blocks(int vocab, int compute_units);
 
+// A sampled step's head: the output head, then the sampler (temperature,
+// top-k, top-p) with draw uniforms[*counter], which writes the id to
+// `sampled`, `next_token` and history[position + 1] and advances the position
+// and the counter. The sampler's scratch is `partials` (sized for both).
+struct SampledHead {
+  float temperature;
+  int top_k;
+  float top_p;
+  const float* uniforms;  // device, one draw per step
+  int32_t* counter;       // device, index of the step's draw
+  int draws;              // entries of `uniforms` (the index is clamped to it)
+};
+void enqueue_decode_head_sampled(const DecodeStepArgs& a, const SampledHead& head, hipStream_t stream);
+
 }  // namespace lcr

@@ -519,6 +519,22 @@ void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
 #undef LCR_LAYER_CASE
 }
 
+void enqueue_decode_head_sampled(const DecodeStepArgs& a, const SampledHead& h, hipStream_t s) {
+  const int blocks = lm_head_blocks(a.vocab, a.compute_units);
+  lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a);
+  HIP_CHECK_LAUNCH();
+  SampleStepState step;
+  step.uniforms = h.uniforms;
+  step.counter = h.counter;
+  step.draws = h.draws;
+  step.next_token = a.next_token;
+  step.history = a.history;
+  step.history_len = a.history_len;
+  step.position = a.position;
+  enqueue_sample_step(a.logits, a.vocab, h.temperature, h.top_k, h.top_p, a.argmax_partials, blocks, a.partials,
+                      a.sampled, step, s);
+}
+
 void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t s, bool with_argmax) {
   const int blocks = lm_head_blocks(a.vocab, a.compute_units);
   lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a);

@@ -4,6 +4,7 @@
 #include <climits>
 
 #include "../capi_util.h"
+#include "../hip_utils.h"
 #include "sampling.h"
 
 namespace lcr {
@@ -50,12 +51,8 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
   return va > vb || (va == vb && ia < ib);
 }
 
-// Loads per thread in flight in the passes over the logits (element i of a
-// batch is base + i * kSampleThreads, so each thread keeps its order).
-constexpr int kSampleBatch = 8;
 // Loads in flight per thread of the sum blocks (one wave per compute unit).
 constexpr int kSumBatch = 32;
-constexpr int kSampleWaves = kSampleThreads / 64;
 
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
@@ -121,163 +118,223 @@ __global__ __launch_bounds__(64) void sample_sum_kernel(float* __restrict__ part
   for (int b = lane; b < kHistogramBins; b += 64) block_hist[blockIdx.x * kHistogramBins + b] = hist[b];
 }
 
-// Steps 1-6 after sample_sum_kernel: the maximum and the total from the
-// partials (the total in the 1024-thread tree of block_sum_1024), the
-// histogram from the blocks' counts, then the cutoff, the compaction, the
-// sort and the walk in one 1024-thread block.
-__global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restrict__ out_id,
-                                                                const float* __restrict__ logits,
-                                                                int vocab, float inv_temperature,
-                                                                int top_k, float top_p,
-                                                                float uniform,
-                                                                const unsigned long long* __restrict__ block_best,
-                                                                int best_blocks,
-                                                                const float* __restrict__ partial_sums,
-                                                                const int* __restrict__ block_hist) {
-  __shared__ float lds32[32];
-  __shared__ int histogram[kHistogramBins];
-  __shared__ int wave_counts[kSampleWaves];
-  __shared__ int shared_cutoff;
-  __shared__ float values[kMaxCandidates];
-  __shared__ int indices[kMaxCandidates];
-  const int t = threadIdx.x;
+// The cutoff bin of step 3 from the summed histogram (wave 0 of a block; the
+// result in *cutoff_out): the number of leading bins whose running count
+// stays <= kMaxCandidates, at least 1. Four bins per lane, in bin order.
+__device__ __forceinline__ void cutoff_from_histogram(const int* __restrict__ block_hist, int* cutoff_out) {
+  static_assert(kHistogramBins == 4 * 64, "four bins per lane");
   const int lane = lane_id();
-  const int wave = t >> 6;
-
-  // 1. Maximum logit; 2. the exponential sum and the histogram, from the
-  // partials of sample_sum_kernel.
-  float max_logit = 0.0f;
-  if (wave == 0) {
-    max_logit = max_from_keys(block_best, best_blocks);
-    if (lane == 0) lds32[0] = max_logit;
-  }
-  for (int b = t; b < kHistogramBins; b += kSampleThreads) {
+  int c[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
     int count = 0;
 #pragma unroll
-    for (int w = 0; w < kSumBlocks; ++w) count += block_hist[w * kHistogramBins + b];
-    histogram[b] = count;
+    for (int w = 0; w < kSumBlocks; ++w) count += block_hist[w * kHistogramBins + 4 * lane + k];
+    c[k] = count;
   }
-  __syncthreads();
-  max_logit = lds32[0];
-  __syncthreads();
-  const float total_sum = block_sum_1024(partial_sums[t], lds32);
+  const int mine = c[0] + c[1] + c[2] + c[3];
+  int before = mine;  // inclusive scan of the lane totals
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int other = __shfl_up(before, o, 64);
+    if (lane >= o) before += other;
+  }
+  before -= mine;
+  int fits = 0;
+  int running = before;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    running += c[k];
+    fits += running <= kMaxCandidates ? 1 : 0;
+  }
+  fits = wave_sum_int(fits);
+  if (lane == 0) *cutoff_out = max(fits, 1);
+}
 
-  // 3. Cutoff bin: the number of leading bins whose running count stays
-  // <= kMaxCandidates (at least 1). Wave 0, four bins per lane, in bin order.
+// Step 4 over many compute units: block b takes logits
+// [b * kCompactSlice, (b + 1) * kCompactSlice) and writes its candidates
+// (scaled value, index) in increasing index order to its own list, and their
+// count. Wave w of the block owns a contiguous quarter of the slice, 64
+// consecutive logits per step; a lane's slot is the candidates of the waves
+// and lanes before it. The lists in block order are the compaction in index
+// order; the final block keeps their first kMaxCandidates.
+constexpr int kCompactThreads = 256;
+constexpr int kCompactSlice = 1024;
+constexpr int kCompactPer = kCompactSlice / kCompactThreads;  // logits per thread
+constexpr int kCompactWaves = kCompactThreads / 64;
+constexpr int kMaxCompactBlocks = 1024;  // vocabularies up to 1M entries
+
+__global__ __launch_bounds__(kCompactThreads) void sample_compact_kernel(
+    float* __restrict__ cand_values, int* __restrict__ cand_indices, int* __restrict__ cand_counts,
+    const float* __restrict__ logits, int vocab, float inv_temperature,
+    const unsigned long long* __restrict__ block_best, int best_blocks, const int* __restrict__ block_hist) {
+  __shared__ int shared_cutoff;
+  __shared__ float shared_max;
+  __shared__ int wave_counts[kCompactWaves];
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int lo = static_cast<int>(blockIdx.x) * kCompactSlice;
+  // The block's logits, requested before the cutoff is known.
+  float v[kCompactPer];
+#pragma unroll
+  for (int k = 0; k < kCompactPer; ++k) {
+    const int i = lo + wave * (kCompactSlice / kCompactWaves) + 64 * k + lane;
+    v[k] = i < vocab ? logits[i] : 0.0f;
+  }
   if (wave == 0) {
-    static_assert(kHistogramBins == 4 * 64, "four bins per lane");
-    int c[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) c[k] = histogram[4 * lane + k];
-    const int mine = c[0] + c[1] + c[2] + c[3];
-    int before = mine;  // inclusive scan of the lane totals
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int other = __shfl_up(before, o, 64);
-      if (lane >= o) before += other;
-    }
-    before -= mine;
-    int fits = 0;
-    int running = before;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      running += c[k];
-      fits += running <= kMaxCandidates ? 1 : 0;
-    }
-    fits = wave_sum_int(fits);
-    if (lane == 0) shared_cutoff = max(fits, 1);
+    const float m = max_from_keys(block_best, best_blocks);
+    if (lane == 0) shared_max = m;
+  } else if (wave == 1) {
+    cutoff_from_histogram(block_hist, &shared_cutoff);
   }
   __syncthreads();
+  const float max_logit = shared_max;
   const int cutoff_bin = shared_cutoff;
-
-  // 4. Ordered compaction. Wave w owns the index range [w * seg, (w + 1) * seg)
-  // and walks it 64 consecutive logits per step (coalesced): it counts its
-  // candidates, takes the exclusive prefix over the waves, then writes them
-  // in index order (a lane's slot is the candidates of the lanes below it).
-  auto is_candidate = [&](float logit, float* scaled_out) {
-    const float scaled = (logit - max_logit) * inv_temperature;
-    const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
-    *scaled_out = scaled;
-    return bin < cutoff_bin;
-  };
-  const int seg = ((vocab + kSampleWaves - 1) / kSampleWaves + 63) / 64 * 64;
-  const int lo = min(vocab, wave * seg);
-  const int hi = min(vocab, lo + seg);
+  bool take[kCompactPer];
+  float scaled[kCompactPer];
   int mine = 0;
-  for (int base = lo; base < hi; base += 64 * kSampleBatch) {
-    float v[kSampleBatch];
 #pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) {
-      const int i = base + 64 * k + lane;
-      v[k] = i < hi ? logits[i] : 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) {
-      float scaled;
-      const bool take = base + 64 * k + lane < hi && is_candidate(v[k], &scaled);
-      mine += __popcll(__ballot(take));
-    }
+  for (int k = 0; k < kCompactPer; ++k) {
+    const int i = lo + wave * (kCompactSlice / kCompactWaves) + 64 * k + lane;
+    scaled[k] = (v[k] - max_logit) * inv_temperature;
+    const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled[k] * (kHistogramBins / 20.0f)));
+    take[k] = i < vocab && bin < cutoff_bin;
+    mine += __popcll(__ballot(take[k]));
   }
   if (lane == 0) wave_counts[wave] = mine;
   __syncthreads();
-  int total_found = 0;
   int slot = 0;
-  for (int w = 0; w < kSampleWaves; ++w) {
-    if (w == wave) slot = total_found;
-    total_found += wave_counts[w];
+  int total = 0;
+  for (int w = 0; w < kCompactWaves; ++w) {
+    if (w == wave) slot = total;
+    total += wave_counts[w];
   }
-  for (int base = lo; base < hi && slot < kMaxCandidates; base += 64 * kSampleBatch) {
-    float v[kSampleBatch];
+  float* values = cand_values + static_cast<size_t>(blockIdx.x) * kCompactSlice;
+  int* indices = cand_indices + static_cast<size_t>(blockIdx.x) * kCompactSlice;
 #pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) {
-      const int i = base + 64 * k + lane;
-      v[k] = i < hi ? logits[i] : 0.0f;
+  for (int k = 0; k < kCompactPer; ++k) {
+    const int i = lo + wave * (kCompactSlice / kCompactWaves) + 64 * k + lane;
+    const unsigned long long mask = __ballot(take[k]);
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+    if (take[k]) {
+      values[slot + below] = scaled[k];
+      indices[slot + below] = i;
     }
-#pragma unroll
-    for (int k = 0; k < kSampleBatch; ++k) {
-      const int i = base + 64 * k + lane;
-      float scaled = 0.0f;
-      const bool take = i < hi && is_candidate(v[k], &scaled);
-      const unsigned long long mask = __ballot(take);
-      const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-      if (take && slot + below < kMaxCandidates) {
-        values[slot + below] = scaled;
-        indices[slot + below] = i;
-      }
-      slot += __popcll(mask);
-    }
+    slot += __popcll(mask);
   }
-  const int found = min(total_found, kMaxCandidates);
-  __syncthreads();
-  for (int i = t; i < kMaxCandidates; i += kSampleThreads) {
-    if (i >= found) {
-      values[i] = -FLT_MAX;
-      indices[i] = INT_MAX;
-    }
-  }
-  __syncthreads();
+  if (threadIdx.x == 0) cand_counts[blockIdx.x] = total;
+}
 
-  // 5. Bitonic sort into (value desc, index asc).
+// One compare-exchange step of the bitonic sort with the element of thread
+// t ^ step: thread t keeps the element that ranks first when it is the lower
+// of the pair in an ascending run (or the upper in a descending one), else
+// the other, which is the swap of the pairwise formulation.
+__device__ __forceinline__ void bitonic_keep(float& v, int& i, float pv, int pi, int t, int span, int step) {
+  const bool keep_first = ((t & step) == 0) == ((t & span) == 0);
+  const bool partner_first = ranks_before(pv, pi, v, i);
+  if (keep_first == partner_first) {
+    v = pv;
+    i = pi;
+  }
+}
+
+// Steps 1-2's totals and 4-6 after sample_compact_kernel, in one 1024-thread
+// block: the maximum is not needed again (the candidates carry their scaled
+// values); the total from the partial sums in the 1024-thread tree of
+// block_sum_1024; the first kMaxCandidates candidates gathered from the
+// blocks' lists in block order; the sort with one element per thread
+// (exchanges between lanes of a wave by shuffles, between waves through LDS);
+// the walk with every exponential computed beforehand, one per thread.
+// With `step` set (a device-resident generation loop), the uniform is
+// step.uniforms[*step.counter], and the id also becomes the next step's input
+// and history[position + 1], and the position and the counter advance (what
+// argmax_step_kernel does for greedy steps).
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restrict__ out_id,
+                                                                int top_k, float top_p, float uniform,
+                                                                const float* __restrict__ partial_sums,
+                                                                const float* __restrict__ cand_values,
+                                                                const int* __restrict__ cand_indices,
+                                                                const int* __restrict__ cand_counts,
+                                                                int compact_blocks, SampleStepState step) {
+  __shared__ float lds32[32];
+  __shared__ int block_start[kMaxCompactBlocks];
+  __shared__ int shared_found;
+  __shared__ float values[kMaxCandidates];
+  __shared__ int indices[kMaxCandidates];
+  __shared__ float weights[kMaxCandidates];
+  const int t = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = t >> 6;
+  static_assert(kSampleThreads == kMaxCandidates, "one candidate per thread");
+
+  const float partial = partial_sums[t];
+
+  // Where each block's list starts in the merged order (wave 0, exclusive
+  // scan over the blocks, 64 at a time).
+  if (wave == 0) {
+    int carry = 0;
+    for (int base = 0; base < compact_blocks; base += 64) {
+      const int b = base + lane;
+      const int count = b < compact_blocks ? cand_counts[b] : 0;
+      int incl = count;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int other = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += other;
+      }
+      if (b < compact_blocks) block_start[b] = carry + incl - count;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) shared_found = min(carry, kMaxCandidates);
+  }
+  const float total_sum = block_sum_1024(partial, lds32);  // its barriers publish the scan
+  const int found = shared_found;
+  // Gather: thread t fetches merged candidate t from the last block whose
+  // list starts at or before t (binary search over the starts), so every
+  // thread's load is in flight at once.
+  float v = -FLT_MAX;
+  int idx = INT_MAX;
+  if (t < found) {
+    int lo_b = 0, hi_b = compact_blocks - 1;
+    while (lo_b < hi_b) {
+      const int mid = (lo_b + hi_b + 1) >> 1;
+      if (block_start[mid] <= t) {
+        lo_b = mid;
+      } else {
+        hi_b = mid - 1;
+      }
+    }
+    const size_t at = static_cast<size_t>(lo_b) * kCompactSlice + static_cast<size_t>(t - block_start[lo_b]);
+    v = cand_values[at];
+    idx = cand_indices[at];
+  }
+
+  // 5. Bitonic sort into (value desc, index asc), one element per thread.
   for (int span = 2; span <= kMaxCandidates; span <<= 1) {
     for (int step = span >> 1; step > 0; step >>= 1) {
-      const int partner = t ^ step;
-      if (partner > t) {
-        const bool first_half = (t & span) == 0;
-        const bool partner_first = ranks_before(values[partner], indices[partner], values[t], indices[t]);
-        const bool swap = first_half ? partner_first : !partner_first;
-        if (swap) {
-          const float tv = values[t];
-          values[t] = values[partner];
-          values[partner] = tv;
-          const int ti = indices[t];
-          indices[t] = indices[partner];
-          indices[partner] = ti;
-        }
+      float pv;
+      int pi;
+      if (step < 64) {
+        pv = __shfl_xor(v, step, 64);
+        pi = __shfl_xor(idx, step, 64);
+      } else {
+        values[t] = v;
+        indices[t] = idx;
+        __syncthreads();
+        pv = values[t ^ step];
+        pi = indices[t ^ step];
+        __syncthreads();
       }
-      __syncthreads();
+      bitonic_keep(v, idx, pv, pi, t, span, step);
     }
   }
+  values[t] = v;
+  indices[t] = idx;
+  // The walk's terms, every one computed once (the same values the walk's
+  // loop would compute in turn).
+  weights[t] = t < found ? lcr_expf(v) : 0.0f;
+  __syncthreads();
 
   // 6. Walk.
   if (t == 0) {
@@ -286,20 +343,29 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
     int keep = 0;
     float kept_mass = 0.0f;
     for (int i = 0; i < limit; ++i) {
-      kept_mass = __builtin_fmaf(lcr_expf(values[i]), inv_total, kept_mass);
+      kept_mass = __builtin_fmaf(weights[i], inv_total, kept_mass);
       ++keep;
       if (top_p < 1.0f && kept_mass >= top_p) break;
     }
     if (keep == 0) keep = 1;
-    const float target = uniform * kept_mass;
+    const int draw = step.counter != nullptr ? min(max(*step.counter, 0), step.draws - 1) : 0;
+    const float u = step.counter != nullptr ? step.uniforms[draw] : uniform;
+    const float target = u * kept_mass;
     int picked = indices[0];
     float running = 0.0f;
     for (int i = 0; i < keep; ++i) {
-      running = __builtin_fmaf(lcr_expf(values[i]), inv_total, running);
+      running = __builtin_fmaf(weights[i], inv_total, running);
       picked = indices[i];
       if (running >= target) break;
     }
     *out_id = picked;
+    if (step.counter != nullptr) {
+      const int pos = *step.position;
+      *step.next_token = picked;
+      if (pos + 1 < step.history_len) step.history[pos + 1] = picked;
+      *step.position = pos + 1;
+      *step.counter = draw + 1;
+    }
   }
 }
 
@@ -309,15 +375,19 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
 using namespace lcr;
 
 // Scratch floats: one 64-bit partial maximum per argmax block, then (for
-// sampling) the 1024 partial exponential sums and the sum blocks' histograms.
+// sampling) the 1024 partial exponential sums, the sum blocks' histograms,
+// and per compaction block its candidate count and its list of (scaled
+// value, index).
 constexpr size_t kScratchKeys = 2 * static_cast<size_t>(kArgmaxBlocks);
 constexpr size_t kScratchSums = kSampleThreads;
 constexpr size_t kScratchHist = static_cast<size_t>(kSumBlocks) * kHistogramBins;
 
+static int compact_blocks_for(int vocab) { return (vocab + kCompactSlice - 1) / kCompactSlice; }
+
 extern "C" size_t lcr_sample_scratch_floats(int vocab, int top_k) {
-  (void)vocab;
   (void)top_k;
-  return kScratchKeys + kScratchSums + kScratchHist;
+  const size_t blocks = static_cast<size_t>(compact_blocks_for(std::max(vocab, 1)));
+  return kScratchKeys + kScratchSums + kScratchHist + blocks * (1 + 2 * static_cast<size_t>(kCompactSlice));
 }
 
 extern "C" int lcr_sample(int32_t* out_id, const float* logits, int vocab, float temperature,
@@ -342,14 +412,54 @@ extern "C" int lcr_sample(int32_t* out_id, const float* logits, int vocab, float
   auto* best = reinterpret_cast<unsigned long long*>(scratch);
   float* sums = scratch + kScratchKeys;
   int* hist = reinterpret_cast<int*>(scratch + kScratchKeys + kScratchSums);
+  const int compact_blocks = compact_blocks_for(vocab);
+  CAPI_CHECK(compact_blocks <= kMaxCompactBlocks,
+             "sampling supports vocabularies up to " << kMaxCompactBlocks * kCompactSlice << " entries, got " << vocab);
+  int* counts = reinterpret_cast<int*>(scratch + kScratchKeys + kScratchSums + kScratchHist);
+  float* cand_values = scratch + kScratchKeys + kScratchSums + kScratchHist + compact_blocks;
+  int* cand_indices = reinterpret_cast<int*>(cand_values + static_cast<size_t>(compact_blocks) * kCompactSlice);
   const int blocks = std::min(kArgmaxBlocks, (vocab + kArgmaxThreads - 1) / kArgmaxThreads);
   const float inv_temperature = 1.0f / temperature;
   argmax_partial_kernel<<<blocks, kArgmaxThreads, 0, s>>>(best, logits, vocab);
   CAPI_LAUNCHED();
   sample_sum_kernel<<<kSumBlocks, 64, 0, s>>>(sums, hist, best, blocks, logits, vocab, inv_temperature);
   CAPI_LAUNCHED();
-  sample_kernel<<<1, kSampleThreads, 0, s>>>(out_id, logits, vocab, inv_temperature, top_k, top_p, uniform, best,
-                                             blocks, sums, hist);
+  sample_compact_kernel<<<compact_blocks, kCompactThreads, 0, s>>>(cand_values, cand_indices, counts, logits, vocab,
+                                                                   inv_temperature, best, blocks, hist);
+  CAPI_LAUNCHED();
+  sample_kernel<<<1, kSampleThreads, 0, s>>>(out_id, top_k, top_p, uniform, sums, cand_values, cand_indices, counts,
+                                             compact_blocks, SampleStepState{});
   CAPI_LAUNCHED();
   return LCR_OK;
 }
+
+namespace lcr {
+
+// The stochastic path after an output head that already wrote its blocks'
+// argmax keys (the fused step's lm_head): steps 2-6 with the step state.
+void enqueue_sample_step(const float* logits, int vocab, float temperature, int top_k, float top_p,
+                         const unsigned long long* block_best, int best_blocks, float* scratch,
+                         int32_t* out_id, const SampleStepState& step, hipStream_t s) {
+  LCR_CHECK(temperature > 0.0f, "a sampled step needs a positive temperature");
+  LCR_CHECK(top_p > 0.0f && top_p <= 1.0f, "top_p must be in (0, 1], got " << top_p);
+  LCR_CHECK(step.counter != nullptr && step.uniforms != nullptr && step.draws > 0,
+            "a sampled step needs its draws on the device");
+  const int compact_blocks = compact_blocks_for(vocab);
+  LCR_CHECK(compact_blocks <= kMaxCompactBlocks, "vocabulary of " << vocab << " entries is too large to sample");
+  float* sums = scratch + kScratchKeys;
+  int* hist = reinterpret_cast<int*>(scratch + kScratchKeys + kScratchSums);
+  int* counts = reinterpret_cast<int*>(scratch + kScratchKeys + kScratchSums + kScratchHist);
+  float* cand_values = scratch + kScratchKeys + kScratchSums + kScratchHist + compact_blocks;
+  int* cand_indices = reinterpret_cast<int*>(cand_values + static_cast<size_t>(compact_blocks) * kCompactSlice);
+  const float inv_temperature = 1.0f / temperature;
+  sample_sum_kernel<<<kSumBlocks, 64, 0, s>>>(sums, hist, block_best, best_blocks, logits, vocab, inv_temperature);
+  HIP_CHECK_LAUNCH();
+  sample_compact_kernel<<<compact_blocks, kCompactThreads, 0, s>>>(cand_values, cand_indices, counts, logits, vocab,
+                                                                   inv_temperature, block_best, best_blocks, hist);
+  HIP_CHECK_LAUNCH();
+  sample_kernel<<<1, kSampleThreads, 0, s>>>(out_id, top_k, top_p, 0.0f, sums, cand_values, cand_indices, counts,
+                                             compact_blocks, step);
+  HIP_CHECK_LAUNCH();
+}
+
+}  // namespace lcr

@@ -9,11 +9,13 @@
 // reduces those and writes the id, so there is nothing to clear between calls.
 //
 // Stochastic: the reference's one-block sampler (sampling.cu:97-224) with its
-// two scheduling-dependent steps made deterministic. Steps 1-2 run on many
-// compute units (the argmax blocks' partial maxima; sixteen one-wave blocks
-// that each run 64 threads of the 1024-thread order below and write their
-// partial sums and bin counts), steps 2's final sum and 3-6 in one
-// 1024-thread block:
+// two scheduling-dependent steps made deterministic, spread over kernels
+// without changing a result: the argmax blocks' partial maxima (step 1);
+// sixteen one-wave blocks that each run 64 threads of the 1024-thread order
+// below and write their partial sums and bin counts (step 2); one block per
+// 1024 logits that finds the cutoff (step 3) and writes its candidates in
+// index order (step 4); one 1024-thread block for step 2's final sum, the
+// first 1024 candidates in block order, the sort and the walk (5-6):
 //  1. max logit (exact), scaled_i = (l_i - max) * inv_temperature;
 //  2. total = sum of exp(scaled_i): thread t (of 1024) adds i = t, t+1024, ...
 //     in order, then a butterfly in each 32-thread group (offsets 16..1), then
@@ -31,6 +33,8 @@
 //     then target = uniform * kept_mass and the first i with
 //     running = fma(exp(v_i), 1/total, running) >= target is the sample.
 #pragma once
+
+#include <hip/hip_runtime.h>
 
 #include "device_common.h"
 
@@ -84,5 +88,25 @@ __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v
 __device__ __forceinline__ int32_t argmax_id(unsigned long long key) {
   return static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull));
 }
+
+// Device state of a sampled generation loop: the draws, the draw counter, and
+// where the id goes besides the output (see sample_kernel). All null for a
+// plain call.
+struct SampleStepState {
+  const float* uniforms = nullptr;   // [steps] draws
+  int32_t* counter = nullptr;        // [1] index of this step's draw
+  int draws = 0;                     // entries of `uniforms`; the index is clamped to them
+  int32_t* next_token = nullptr;     // [1] the next step's input
+  int32_t* history = nullptr;        // [history_len] history[position + 1] = id
+  int history_len = 0;
+  int32_t* position = nullptr;       // [1] advanced by one
+};
+
+// Steps 2-6 of the stochastic path after an output head that wrote its
+// blocks' argmax keys to `block_best` (the fused decode step's lm_head); the
+// scratch is laid out as lcr_sample's (lcr_sample_scratch_floats).
+void enqueue_sample_step(const float* logits, int vocab, float temperature, int top_k, float top_p,
+                         const unsigned long long* block_best, int best_blocks, float* scratch,
+                         int32_t* out_id, const SampleStepState& step, hipStream_t stream);
 
 }  // namespace lcr

@@ -70,6 +70,7 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
 
 Model::~Model() {
   for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
+  for (auto& kv : sampled_graphs_) (void)hipGraphExecDestroy(kv.second);
   graphs_.clear();
   if (stream_ != nullptr) (void)hipStreamSynchronize(stream_);
   if (pinned_state_ != nullptr) (void)hipHostFree(pinned_state_);
@@ -200,6 +201,8 @@ void Model::allocate_arena() {
       kMaxLmHeadBlocks * sizeof(unsigned long long),                  // argmax_partials_
       (static_cast<size_t>(options_.max_seq) + 1) * sizeof(int32_t),  // history_
       gemm_workspace_bytes(),                                         // gemm_workspace_
+      static_cast<size_t>(options_.max_seq) * sizeof(float),          // uniforms_
+      sizeof(int32_t),                                                // draw_counter_
   };
   size_t total = 0;
   for (size_t s : sizes) total = align_up(total, 256) + s;
@@ -222,6 +225,8 @@ void Model::allocate_arena() {
   history_ = arena_.alloc<int32_t>(static_cast<size_t>(options_.max_seq) + 1);
   gemm_workspace_size_ = gemm_workspace_bytes();
   gemm_workspace_ = gemm_workspace_size_ > 0 ? arena_.alloc<float>(gemm_workspace_size_ / sizeof(float)) : nullptr;
+  uniforms_ = arena_.alloc<float>(static_cast<size_t>(options_.max_seq));
+  draw_counter_ = arena_.alloc<int32_t>(1);
   HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
   HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
 }
@@ -411,6 +416,111 @@ const float* Model::decode(int token) {
   stats_.last_decode_ms = timer.elapsed_ms();
   if (profiler_.enabled()) profiler_.collect();
   return logits_;
+}
+
+void Model::clear_sampled_graphs() {
+  for (auto& kv : sampled_graphs_) (void)hipGraphExecDestroy(kv.second);
+  sampled_graphs_.clear();
+}
+
+// One sampled step: the layers as in launch_fused_step, then the head with
+// the sampler instead of the argmax.
+void Model::launch_sampled_step(int seq_len) {
+  const int splits = decode_splits(seq_len);
+  const DecodeStepArgs args = step_args(splits);
+  const SampledHead head{sampled_params_.temperature, sampled_params_.top_k, sampled_params_.top_p, uniforms_,
+                         draw_counter_, options_.max_seq};
+  auto enqueue = [&]() {
+    for (int layer = 0; layer < config_.num_layers; ++layer) {
+      const LayerWeights& lw = layers_[static_cast<size_t>(layer)];
+      LayerDevicePtrs w{lw.input_norm, lw.qkv_proj, lw.o_proj, lw.post_attention_norm,
+                        lw.gate_up_proj, lw.down_proj};
+      enqueue_decode_layer(args, w, kv_cache_->view(layer), layer, stream_);
+    }
+    enqueue_decode_head_sampled(args, head, stream_);
+  };
+  if (!options_.use_graph || synchronous_launches()) {
+    enqueue();
+    return;
+  }
+  auto it = sampled_graphs_.find(splits);
+  if (it == sampled_graphs_.end()) {
+    hipGraph_t graph = nullptr;
+    HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    try {
+      enqueue();
+    } catch (...) {
+      hipGraph_t discard = nullptr;
+      (void)hipStreamEndCapture(stream_, &discard);
+      if (discard != nullptr) (void)hipGraphDestroy(discard);
+      throw;
+    }
+    HIP_CHECK(hipStreamEndCapture(stream_, &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIP_CHECK(status);
+    it = sampled_graphs_.emplace(splits, exec).first;
+  }
+  HIP_CHECK(hipGraphLaunch(it->second, stream_));
+}
+
+std::vector<int> Model::generate_sampled(int first_token, int steps, float temperature, int top_k,
+                                         float top_p, const float* uniforms, double* elapsed_ms) {
+  LCR_CHECK(fused_, "device-side sampled generation needs the fused decode path");
+  LCR_CHECK(steps >= 0, "steps must be non-negative");
+  LCR_CHECK(temperature > 0.0f, "sampled generation needs a positive temperature (greedy: generate_greedy)");
+  LCR_CHECK(top_p > 0.0f && top_p <= 1.0f, "top_p must be in (0, 1], got " << top_p);
+  LCR_CHECK(steps == 0 || uniforms != nullptr, "sampled generation needs one draw per step");
+  LCR_CHECK(first_token >= 0 && first_token < config_.vocab_size,
+            "token id " << first_token << " is outside the vocabulary of " << config_.vocab_size);
+  LCR_CHECK(position_ + steps <= options_.max_seq,
+            "generating " << steps << " tokens at position " << position_
+                          << " exceeds the cache built for " << options_.max_seq);
+  std::vector<int> out(static_cast<size_t>(steps));
+  if (steps == 0) {
+    if (elapsed_ms) *elapsed_ms = 0.0;
+    return out;
+  }
+  const SampledParams params{temperature, top_k, top_p};
+  if (!(params == sampled_params_)) {
+    clear_sampled_graphs();
+    sampled_params_ = params;
+  }
+  const int start = position_;
+  kv_cache_->reserve_length(position_ + steps);
+  HIP_CHECK(hipMemcpy(uniforms_, uniforms, static_cast<size_t>(steps) * sizeof(float), hipMemcpyHostToDevice));
+  // Capture every graph this run needs before timing it (a capture runs its
+  // graph once, which moves the position and the counter: both are reset).
+  HIP_CHECK(hipMemsetAsync(draw_counter_, 0, sizeof(int32_t), stream_));
+  for (int s = 0; s < steps; ++s) {
+    const int splits = decode_splits(start + s + 1);
+    if (options_.use_graph && sampled_graphs_.find(splits) == sampled_graphs_.end()) {
+      write_step_state(first_token);
+      launch_sampled_step(start + s + 1);
+      HIP_CHECK(hipStreamSynchronize(stream_));
+    }
+  }
+  write_step_state(first_token);
+  HIP_CHECK(hipMemsetAsync(draw_counter_, 0, sizeof(int32_t), stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  GpuTimer timer;
+  timer.start(stream_);
+  for (int s = 0; s < steps; ++s) launch_sampled_step(start + s + 1);
+  timer.stop(stream_);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  const double ms = timer.elapsed_ms();
+  if (elapsed_ms) *elapsed_ms = ms;
+  stats_.last_decode_ms = ms / steps;
+  position_ = start + steps;
+  std::vector<int32_t> ids(static_cast<size_t>(steps));
+  HIP_CHECK(hipMemcpy(ids.data(), history_ + start + 1, ids.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+  for (int s = 0; s < steps; ++s) {
+    LCR_CHECK(ids[static_cast<size_t>(s)] >= 0 && ids[static_cast<size_t>(s)] < config_.vocab_size,
+              "sampling produced token id " << ids[static_cast<size_t>(s)] << ", outside the vocabulary");
+    out[static_cast<size_t>(s)] = ids[static_cast<size_t>(s)];
+  }
+  return out;
 }
 
 std::vector<int> Model::generate_greedy(int first_token, int steps, double* elapsed_ms) {

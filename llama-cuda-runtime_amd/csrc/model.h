@@ -113,6 +113,15 @@ class Model {
   // with no host round trip, `steps` decodes in all. Returns the generated ids
   // (the argmax after each step). Needs the fused decode path.
   std::vector<int> generate_greedy(int first_token, int steps, double* elapsed_ms);
+  // Not in the reference. Sampled generation kept on the device, the
+  // reference's host loop (decode(), then sample() with the next draw,
+  // src/main.cu:456-466) without the host: decodes `first_token`, samples
+  // the next with uniforms[0] (temperature, top_k, top_p as sample()), feeds
+  // it to the next step, and so on, `steps` decodes in all. Returns the
+  // sampled ids, the same as decode() + sample() would give with the same
+  // draws. Needs the fused decode path.
+  std::vector<int> generate_sampled(int first_token, int steps, float temperature, int top_k,
+                                    float top_p, const float* uniforms, double* elapsed_ms);
   // Moves the position without running the model (the long-context stress
   // case fills the cache directly). The cache must already hold `position`.
   void set_position(int position);
@@ -183,6 +192,21 @@ class Model {
   int32_t* pinned_state_ = nullptr;  // host {token, position}
 
   std::map<int, hipGraphExec_t> graphs_;  // by split count
+  // Sampled steps' graphs, by split count, for the parameters in
+  // sampled_params_ (other parameters capture them again).
+  std::map<int, hipGraphExec_t> sampled_graphs_;
+  struct SampledParams {
+    float temperature = 0.0f;
+    int top_k = 0;
+    float top_p = 0.0f;
+    bool operator==(const SampledParams& o) const {
+      return temperature == o.temperature && top_k == o.top_k && top_p == o.top_p;
+    }
+  } sampled_params_;
+  float* uniforms_ = nullptr;        // [max_seq] draws of a sampled generation
+  int32_t* draw_counter_ = nullptr;  // [1]
+  void launch_sampled_step(int seq_len);
+  void clear_sampled_graphs();
   hipGraph_t graph_template_ = nullptr;
 
   int position_ = 0;

@@ -98,3 +98,72 @@ def test_fp16_mfma_prefill_then_sampling_matches_oracle_on_exported_cache(lcr, f
     assert len(set(tokens)) > STEPS // 4
     ref.close()
     m.close()
+
+
+def host_loop(m, ptr, steps, uniforms):
+    """The reference's loop (src/main.cu:456-466): sample with the next draw,
+    then decode the sampled id."""
+    ids = []
+    for i in range(steps):
+        tok = m.sample(ptr, T, TOP_K, TOP_P, uniforms[i])
+        ids.append(tok)
+        if i + 1 < steps:
+            ptr = m.decode(tok)
+    return ids
+
+
+@pytest.mark.parametrize("mode", ["graph", "eager", "contiguous"])
+def test_device_sampled_loop_equals_host_loop(lcr, fp16_ckpt, mode):
+    """generate_sampled is the host loop without the host: the first id from
+    the prefill's logits on the host, then 95 decode + sample steps on the
+    device; every id equals the host loop's with the same draws."""
+    cfg = lcr.llama_config()
+    prompt = lcr.synthetic_tokens(80, cfg["vocab_size"], seed=7, variant="fp16")
+    steps = 96
+    uniforms = lcr.philox_uniforms(UNIFORM_SEED + 1, steps)
+    opts = dict(variant="fp16", max_seq=256, paged=0 if mode == "contiguous" else 1, page_size=16,
+                use_graph=0 if mode == "eager" else 1)
+    a = lcr.Model(fp16_ckpt, **opts)
+    want = host_loop(a, a.prefill(prompt), steps, uniforms)
+    a.close()
+    b = lcr.Model(fp16_ckpt, **opts)
+    first = b.sample(b.prefill(prompt), T, TOP_K, TOP_P, uniforms[0])
+    ids, ms = b.generate_sampled(first, steps - 1, T, TOP_K, TOP_P, uniforms[1:])
+    assert [first] + [int(x) for x in ids] == want
+    assert ms > 0 and b.position == len(prompt) + steps - 1
+    # A second call continues from there with new draws, as the host loop would.
+    more = lcr.philox_uniforms(UNIFORM_SEED + 2, 8)
+    ids2, _ = b.generate_sampled(int(ids[-1]), 8, T, TOP_K, TOP_P, more)
+    ptr = b.decode(int(ids2[-1]))
+    assert b.position == len(prompt) + steps + 8
+    b.close()
+    c = lcr.Model(fp16_ckpt, **opts)
+    ptr = c.prefill(prompt)
+    ids_c = host_loop(c, ptr, steps, uniforms)
+    tail = []
+    tok = ids_c[-1]
+    for u in more:
+        tok = c.sample(c.decode(tok), T, TOP_K, TOP_P, u)
+        tail.append(tok)
+    assert [int(x) for x in ids2] == tail
+    c.close()
+
+
+def test_device_sampled_loop_across_split_change(lcr, fp16_ckpt):
+    """A run from 4040 to 4136 positions crosses the change of the decode
+    attention's split count at 4096, so two step graphs are captured during
+    the run; the ids still equal the host loop's."""
+    cfg = lcr.llama_config()
+    prompt = lcr.synthetic_tokens(4040, cfg["vocab_size"], seed=8, variant="fp16")
+    steps = 96
+    uniforms = lcr.philox_uniforms(UNIFORM_SEED + 3, steps)
+    opts = dict(variant="fp16", max_seq=4200, paged=1, page_size=16)
+    a = lcr.Model(fp16_ckpt, **opts)
+    assert a.decode_splits(4040) != a.decode_splits(4136)
+    want = host_loop(a, a.prefill(prompt), steps, uniforms)
+    a.close()
+    b = lcr.Model(fp16_ckpt, **opts)
+    first = b.sample(b.prefill(prompt), T, TOP_K, TOP_P, uniforms[0])
+    ids, _ = b.generate_sampled(first, steps - 1, T, TOP_K, TOP_P, uniforms[1:])
+    assert [first] + [int(x) for x in ids] == want
+    b.close()

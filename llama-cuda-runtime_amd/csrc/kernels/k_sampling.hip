@@ -51,8 +51,6 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
   return va > vb || (va == vb && ia < ib);
 }
 
-// Loads in flight per thread of the sum blocks (one wave per compute unit).
-constexpr int kSumBatch = 32;
 
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
@@ -70,37 +68,55 @@ __device__ __forceinline__ float max_from_keys(const unsigned long long* __restr
   return u32_as_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Step 2 over many compute units: block b (one wave) runs threads
-// 64 b .. 64 b + 63 of the 1024-thread order, each adding exp(scaled_i) for
-// i = t, t + 1024, ... in order, exactly as one 1024-thread block would; the
-// thread's partial sum goes to partial_sums[t] and the block's histogram of
-// bins to block_hist[b][bin] (counts, so their order of addition is free).
+// Step 2 over many compute units: block b runs threads 64 b .. 64 b + 63
+// of the 1024-thread order, each adding exp(scaled_i) for i = t, t + 1024,
+// ... in order, exactly as one 1024-thread block would; the thread's partial
+// sum goes to partial_sums[t] and the block's histogram of bins to
+// block_hist[b][bin] (counts, so their order of addition is free). Four lanes
+// share a thread's chain: lane s of a quad computes the exponentials of terms
+// s, s + 4, s + 8, ... and the quad's first lane adds all of them in term
+// order, each broadcast to it across the quad, so the sum is the chain's, bit
+// for bit, with a quarter of the exponentials per lane.
 constexpr int kSumBlocks = kSampleThreads / 64;
+constexpr int kSumWaves = 4;                 // per block: 64 chains, 4 lanes each
+constexpr int kSumTerms = 8;                 // terms per lane per batch (32 per chain)
 
-__global__ __launch_bounds__(64) void sample_sum_kernel(float* __restrict__ partial_sums, int* __restrict__ block_hist,
-                                                        const unsigned long long* __restrict__ block_best,
-                                                        int best_blocks, const float* __restrict__ logits,
-                                                        int vocab, float inv_temperature) {
+template <int S>
+__device__ __forceinline__ float quad_lane(float v) {
+  constexpr int ctrl = S | (S << 2) | (S << 4) | (S << 6);  // quad_perm [S, S, S, S]
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+__global__ __launch_bounds__(64 * kSumWaves) void sample_sum_kernel(float* __restrict__ partial_sums,
+                                                                    int* __restrict__ block_hist,
+                                                                    const unsigned long long* __restrict__ block_best,
+                                                                    int best_blocks, const float* __restrict__ logits,
+                                                                    int vocab, float inv_temperature) {
   __shared__ int hist[kHistogramBins];
   const int lane = lane_id();
-  const int t = static_cast<int>(blockIdx.x) * 64 + lane;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int sub = lane & 3;
+  const int chain = static_cast<int>(blockIdx.x) * 64 + wave * 16 + (lane >> 2);
   const float max_logit = max_from_keys(block_best, best_blocks);
-  for (int b = lane; b < kHistogramBins; b += 64) hist[b] = 0;
+  for (int b = threadIdx.x; b < kHistogramBins; b += 64 * kSumWaves) hist[b] = 0;
   __syncthreads();
   float local_sum = 0.0f;
   int last_bin = 0;
-  for (int base = t; base < vocab; base += kSumBatch * kSampleThreads) {
-    float v[kSumBatch];
+  // Batch q holds terms 4 kSumTerms q .. 4 kSumTerms (q + 1) - 1 of the
+  // chain; this lane's are those congruent to `sub` mod 4.
+  for (int first = 0; chain + first * kSampleThreads < vocab; first += 4 * kSumTerms) {
+    float e[kSumTerms];
 #pragma unroll
-    for (int k = 0; k < kSumBatch; ++k) {
-      const int i = base + k * kSampleThreads;
-      v[k] = i < vocab ? logits[i] : 0.0f;
+    for (int j = 0; j < kSumTerms; ++j) {
+      const int i = chain + (first + 4 * j + sub) * kSampleThreads;
+      e[j] = i < vocab ? logits[i] : 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < kSumBatch; ++k) {
-      if (base + k * kSampleThreads < vocab) {
-        const float scaled = (v[k] - max_logit) * inv_temperature;
-        local_sum += lcr_expf(scaled);
+    for (int j = 0; j < kSumTerms; ++j) {
+      const int i = chain + (first + 4 * j + sub) * kSampleThreads;
+      const float scaled = (e[j] - max_logit) * inv_temperature;
+      e[j] = lcr_expf(scaled);
+      if (i < vocab) {
         const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
         if (bin == kHistogramBins - 1) {
           ++last_bin;
@@ -109,13 +125,28 @@ __global__ __launch_bounds__(64) void sample_sum_kernel(float* __restrict__ part
         }
       }
     }
+    // In term order: term first + 4 j + s is lane s's e[j].
+#pragma unroll
+    for (int j = 0; j < kSumTerms; ++j) {
+      const float t0 = quad_lane<0>(e[j]);
+      const float t1 = quad_lane<1>(e[j]);
+      const float t2 = quad_lane<2>(e[j]);
+      const float t3 = quad_lane<3>(e[j]);
+      const int k = first + 4 * j;
+      if (chain + k * kSampleThreads < vocab) local_sum += t0;
+      if (chain + (k + 1) * kSampleThreads < vocab) local_sum += t1;
+      if (chain + (k + 2) * kSampleThreads < vocab) local_sum += t2;
+      if (chain + (k + 3) * kSampleThreads < vocab) local_sum += t3;
+    }
   }
   last_bin = wave_sum_int(last_bin);
-  partial_sums[t] = local_sum;
+  if (sub == 0) partial_sums[chain] = local_sum;
   __syncthreads();
-  if (lane == 0) hist[kHistogramBins - 1] += last_bin;
+  if (lane == 0) atomicAdd(&hist[kHistogramBins - 1], last_bin);
   __syncthreads();
-  for (int b = lane; b < kHistogramBins; b += 64) block_hist[blockIdx.x * kHistogramBins + b] = hist[b];
+  for (int b = threadIdx.x; b < kHistogramBins; b += 64 * kSumWaves) {
+    block_hist[blockIdx.x * kHistogramBins + b] = hist[b];
+  }
 }
 
 // The cutoff bin of step 3 from the summed histogram (wave 0 of a block; the
@@ -422,7 +453,7 @@ extern "C" int lcr_sample(int32_t* out_id, const float* logits, int vocab, float
   const float inv_temperature = 1.0f / temperature;
   argmax_partial_kernel<<<blocks, kArgmaxThreads, 0, s>>>(best, logits, vocab);
   CAPI_LAUNCHED();
-  sample_sum_kernel<<<kSumBlocks, 64, 0, s>>>(sums, hist, best, blocks, logits, vocab, inv_temperature);
+  sample_sum_kernel<<<kSumBlocks, 64 * kSumWaves, 0, s>>>(sums, hist, best, blocks, logits, vocab, inv_temperature);
   CAPI_LAUNCHED();
   sample_compact_kernel<<<compact_blocks, kCompactThreads, 0, s>>>(cand_values, cand_indices, counts, logits, vocab,
                                                                    inv_temperature, best, blocks, hist);
@@ -452,7 +483,8 @@ void enqueue_sample_step(const float* logits, int vocab, float temperature, int 
   float* cand_values = scratch + kScratchKeys + kScratchSums + kScratchHist + compact_blocks;
   int* cand_indices = reinterpret_cast<int*>(cand_values + static_cast<size_t>(compact_blocks) * kCompactSlice);
   const float inv_temperature = 1.0f / temperature;
-  sample_sum_kernel<<<kSumBlocks, 64, 0, s>>>(sums, hist, block_best, best_blocks, logits, vocab, inv_temperature);
+  sample_sum_kernel<<<kSumBlocks, 64 * kSumWaves, 0, s>>>(sums, hist, block_best, best_blocks, logits, vocab,
+                                                          inv_temperature);
   HIP_CHECK_LAUNCH();
   sample_compact_kernel<<<compact_blocks, kCompactThreads, 0, s>>>(cand_values, cand_indices, counts, logits, vocab,
                                                                    inv_temperature, block_best, best_blocks, hist);

@@ -482,10 +482,14 @@ __device__ __forceinline__ void wait_stage_landed() {
 //    256-token tiles would leave compute units idle;
 //  - 128 x 128, kWaves = 8: wave tiles of 64 x 32, for projections whose
 //    larger tiles would leave compute units idle (two blocks fit a CU).
-template <int kStages, int kWaves, int BW, int BT, bool kFp32Out>
+// kRK: K per ring stage, 32 (64-byte rows) or 64 (128-byte rows: twice the
+// products per stage barrier). Either way the products run over K in 32-wide
+// MFMA steps in increasing order, so the results are the same bits.
+template <int kStages, int kWaves, int BW, int BT, bool kFp32Out, int kRK = kRingK>
 __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict__ Y, const elem_t* __restrict__ X,
                                                                 const elem_t* __restrict__ W, int T, int N, int K,
                                                                 GemmGrid grid) {
+  static_assert(kRK == 32 || kRK == 64, "ring stages of 32 or 64 K");
   static_assert((BW == 256 && BT == 256 && (kWaves == 4 || kWaves == 8)) ||
                     (BW == 256 && BT == 128 && kWaves == 8) || (BW == 128 && BT == 128 && kWaves == 8),
                 "supported ring tiles: 256 x 256 on 4 or 8 waves, 256 x 128 and 128 x 128 on 8 waves");
@@ -494,9 +498,12 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   constexpr int FW = BW / kWavesW / 16;  // W fragments of 16 rows per wave
   constexpr int FT = BT / kWavesT / 16;      // token fragments of 16 tokens per wave
   constexpr int kRows = BW + BT;
-  constexpr int kStageElems = kRows * kRingK;
-  constexpr int kLoads = kRows / 16 / kWaves;  // 1 KB loads (16 rows) per wave per stage
-  static_assert(kLoads * 16 * kWaves == kRows, "stage rows split evenly over the waves");
+  constexpr int kStageElems = kRows * kRK;
+  constexpr int kLoadRows = 512 / kRK;              // rows of one 1 KB load: 16 or 8
+  constexpr int kLanesPerRow = 64 / kLoadRows;      // 16-byte chunks per row: 4 or 8
+  constexpr int kKSteps = kRK / 32;                 // MFMA k-steps per stage
+  constexpr int kLoads = kRows / kLoadRows / kWaves;  // 1 KB loads per wave per stage
+  static_assert(kLoads * kLoadRows * kWaves == kRows, "stage rows split evenly over the waves");
   static_assert(FW % 2 == 0, "the gated epilogue pairs fragments 2m and 2m + 1");
   __shared__ __attribute__((aligned(1024))) elem_t ring[kStages * kStageElems];
 
@@ -511,22 +518,27 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   const int ww = (wave / kWavesT) * (16 * FW);
   const int wt = (wave % kWavesT) * (16 * FT);
 
+  // Chunk c of row r sits at 16-byte slot c ^ swizzle(r) of the row: for
+  // 64-byte rows (r >> 1) & 3, for 128-byte rows r & 7; fragment reads of 16
+  // consecutive rows are then free of bank conflicts.
+  auto row_swizzle = [](int r) { return kRK == 32 ? ((r >> 1) & 3) : (r & 7); };
   // Load i of a wave fills 1 KB block kWaves * i + wave of the stage: rows
-  // 16 block .. +15, four lanes per row.
+  // kLoadRows block .. + kLoadRows - 1, kLanesPerRow lanes per row; a lane
+  // loads the chunk that belongs in its slot.
   const elem_t* src[kLoads];
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
-    const int row = 16 * (kWaves * i + wave) + (lane >> 2);
-    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    const int row = kLoadRows * (kWaves * i + wave) + lane / kLanesPerRow;
+    const int chunk = (lane % kLanesPerRow) ^ row_swizzle(row);
     src[i] = (row < BW ? W + static_cast<size_t>(weight_row(min(w0 + row, N - 1), grid.ffn)) * K
                            : X + static_cast<size_t>(min(t0 + row - BW, T - 1)) * K) + work.k_first + 8 * chunk;
   }
-  const uint32_t ring_base = lds_address_of(ring) + static_cast<uint32_t>(wave * 16 * kRingK * 2);
+  const uint32_t ring_base = lds_address_of(ring) + static_cast<uint32_t>(wave * 1024);
   auto issue = [&](int s) {
     const uint32_t base = ring_base + static_cast<uint32_t>((s % kStages) * kStageElems * 2);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      load_to_lds16(src[i] + s * kRingK, base + static_cast<uint32_t>(i * kWaves * 16 * kRingK * 2));
+      load_to_lds16(src[i] + s * kRK, base + static_cast<uint32_t>(i * kWaves * 1024));
     }
   };
 
@@ -536,8 +548,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
 #pragma unroll
     for (int j = 0; j < FT; ++j) acc[i][j] = mfma_acc4{0.f, 0.f, 0.f, 0.f};
   }
-  const int swz = 8 * (grp ^ ((col >> 1) & 3));
-  const int stages = work.k_len / kRingK;
+  // 16-byte slot of k-step ks's chunk of this lane's fragment rows (16 rows
+  // from a multiple of 16, so the row's swizzle is that of `col`).
+  auto swz = [&](int ks) { return 8 * ((4 * ks + grp) ^ row_swizzle(col)); };
+  const int stages = work.k_len / kRK;
+  const int ksteps = stages * kKSteps;
   // The next stage's fragments are read during the current stage's products,
   // so LDS reads overlap matrix work: its token fragments into the second of
   // two sets, and each W fragment into the registers of the current one as
@@ -545,22 +560,24 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   // reading stage s + 1, every wave's reads of stage s have returned, and
   // stage s's buffer takes stage s + kStages.
   mfma_in8 aw[FW], bt_a[FT], bt_b[FT];
-  auto read_tokens = [&](int s, mfma_in8 (&bt)[FT]) {
-    const elem_t* base = ring + (s % kStages) * kStageElems;
+  // k-step q: stage q / kKSteps, step q % kKSteps of it.
+  auto read_tokens = [&](int q, mfma_in8 (&bt)[FT]) {
+    const elem_t* base = ring + ((q / kKSteps) % kStages) * kStageElems + swz(q % kKSteps);
 #pragma unroll
-    for (int j = 0; j < FT; ++j) bt[j] = lds_operand(base + (BW + wt + 16 * j + col) * kRingK + swz);
+    for (int j = 0; j < FT; ++j) bt[j] = lds_operand(base + (BW + wt + 16 * j + col) * kRK);
   };
   // Products of the stage whose fragments are in aw / bt, reading stage
   // `next` into aw / bt_next. After the last stage `next` repeats a stage
   // whose loads have all landed, and what is read goes unused.
   auto step = [&](const mfma_in8 (&bt)[FT], mfma_in8 (&bt_next)[FT], int next) {
-    const elem_t* nb = ring + (next % kStages) * kStageElems + (ww + col) * kRingK + swz;
+    const elem_t* nb =
+        ring + ((next / kKSteps) % kStages) * kStageElems + (ww + col) * kRK + swz(next % kKSteps);
     read_tokens(next, bt_next);
 #pragma unroll
     for (int i = 0; i < FW; ++i) {
 #pragma unroll
       for (int j = 0; j < FT; ++j) acc[i][j] = mfma16x16x32(aw[i], bt[j], acc[i][j]);
-      aw[i] = lds_operand(nb + 16 * i * kRingK);
+      aw[i] = lds_operand(nb + 16 * i * kRK);
     }
     // keep that order: the token reads, then per W fragment its products and
     // its replacement's read
@@ -587,13 +604,14 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   advance(0);
   read_tokens(0, bt_a);
   {
-    const elem_t* base = ring + (ww + col) * kRingK + swz;
+    const elem_t* base = ring + (ww + col) * kRK + swz(0);
 #pragma unroll
-    for (int i = 0; i < FW; ++i) aw[i] = lds_operand(base + 16 * i * kRingK);
+    for (int i = 0; i < FW; ++i) aw[i] = lds_operand(base + 16 * i * kRK);
   }
-  for (int s = 0; s < stages; ++s) {
-    if (s + 1 < stages) advance(s + 1);
-    step(bt_a, bt_b, min(s + 1, stages - 1));
+  for (int q = 0; q < ksteps; ++q) {
+    // Reading k-step q + 1's fragments opens a new stage every kKSteps steps.
+    if (q + 1 < ksteps && (q + 1) % kKSteps == 0) advance((q + 1) / kKSteps);
+    step(bt_a, bt_b, min(q + 1, ksteps - 1));
 #pragma unroll
     for (int j = 0; j < FT; ++j) bt_a[j] = bt_b[j];
   }
@@ -606,11 +624,16 @@ constexpr int kRingStages = 4;
 // Fraction of a compute unit's MFMA peak the 256 x 128 ring tile reaches
 // (measured on MI355X; the plan compares it with the other shapes').
 constexpr double kRing256x128Efficiency = 0.30;
-constexpr int kRing256x128Stages = 4;
+// 64 K per stage, three stages (144 KiB of LDS): half the stage barriers of 32
+// K per stage, the same bits; prefill 2.415 -> 2.356 ms at 512 tokens (with
+// the 128 x 128 tile below as well: 2.328 ms, and 6.231 -> 6.115 ms at 2048).
+constexpr int kRing256x128K = 64;
+constexpr int kRing256x128Stages = 3;
 // The 128 x 128 ring tile: o_proj at 2048 tokens (one tile per compute unit)
 // takes 24.2 us, 0.28 of a compute unit's peak, against 34-36 us for the
 // register-staged 128 x 128 kernel.
 constexpr double kRing128x128Efficiency = 0.28;
+constexpr int kRing128x128K = 64;  // 64 K per stage, four stages (128 KiB of LDS)
 constexpr int kRing128x128Stages = 4;
 // Waves per ring block. Eight (two per SIMD) measured faster than four with
 // 128 x 128 wave tiles: 143 against 176 us for T = 2048, N = 16384, K = 2048;
@@ -771,13 +794,16 @@ GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wi
     int bw, bt, stage_k;
     double efficiency;  // fraction of a compute unit's MFMA peak, measured on MI355X
   };
+  // A ring shape needs K in whole ring stages of its depth.
   const bool ring = K % kRingK == 0;
+  const bool ring256x128 = K % kRing256x128K == 0;
+  const bool ring128x128 = K % kRing128x128K == 0;
   const Option options[] = {
       {ring ? GemmShape::kRing256x256 : GemmShape::k256x256, 256, 256, ring ? kRingK : kStageK, ring ? 0.37 : 0.31},
-      {ring ? GemmShape::kRing256x128 : GemmShape::k256x128, 256, 128, ring ? kRingK : kStageK,
-       ring ? kRing256x128Efficiency : 0.23},
-      {ring ? GemmShape::kRing128x128 : GemmShape::k128x128, 128, 128, ring ? kRingK : kStageK,
-       ring ? kRing128x128Efficiency : 0.20}};
+      {ring256x128 ? GemmShape::kRing256x128 : GemmShape::k256x128, 256, 128,
+       ring256x128 ? kRing256x128K : kStageK, ring256x128 ? kRing256x128Efficiency : 0.23},
+      {ring128x128 ? GemmShape::kRing128x128 : GemmShape::k128x128, 128, 128,
+       ring128x128 ? kRing128x128K : kStageK, ring128x128 ? kRing128x128Efficiency : 0.20}};
   constexpr double kCuPeak = 9.8e12;     // bf16 dense flop/s per compute unit
   constexpr double kBandwidth = 5.0e12;  // sustained bytes/s for the partials' round trip
   constexpr double kLaunch = 4e-6;
@@ -818,15 +844,15 @@ void launch_gemm_tiles(void* Y, bool fp32_out, const elem_t* X, const elem_t* W,
   }
 }
 
-template <int BW, int BT, int kWaves, int kStages>
+template <int BW, int BT, int kWaves, int kStages, int kRK = kRingK>
 void launch_gemm_ring(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, int N, int K,
                       const GemmGrid& grid, hipStream_t s) {
   const int units = grid.tiles_t * grid.tiles_w * grid.splits;
   const unsigned blocks = static_cast<unsigned>(((units + 7) / 8) * 8);
   if (fp32_out) {
-    gemm_ring_kernel<kStages, kWaves, BW, BT, true><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
+    gemm_ring_kernel<kStages, kWaves, BW, BT, true, kRK><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
   } else {
-    gemm_ring_kernel<kStages, kWaves, BW, BT, false><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
+    gemm_ring_kernel<kStages, kWaves, BW, BT, false, kRK><<<blocks, 64 * kWaves, 0, s>>>(Y, X, W, T, N, K, grid);
   }
 }
 
@@ -846,10 +872,10 @@ bool run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
       launch_gemm_ring<256, 256, kRingWaves, kRingStages>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
     case GemmShape::kRing256x128:
-      launch_gemm_ring<256, 128, 8, kRing256x128Stages>(Y, fp32_out, X, W, T, N, K, grid, s);
+      launch_gemm_ring<256, 128, 8, kRing256x128Stages, kRing256x128K>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
     case GemmShape::kRing128x128:
-      launch_gemm_ring<128, 128, 8, kRing128x128Stages>(Y, fp32_out, X, W, T, N, K, grid, s);
+      launch_gemm_ring<128, 128, 8, kRing128x128Stages, kRing128x128K>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
     case GemmShape::k256x256:
       launch_gemm_tiles<256, 256, 2, 4>(Y, fp32_out, X, W, T, N, K, grid, s);

@@ -327,6 +327,135 @@ __device__ __forceinline__ void store_gemm_tile(const mfma_acc4 (&acc)[FW][FT], 
   }
 }
 
+// The ring kernel's output through LDS. A fragment's 16 lanes of one group
+// hold 16 consecutive tokens, so a direct store writes 8 or 16 bytes into each
+// of 16 output rows N elements apart; with N = 16384 that ran at about
+// 2 TB/s. Here each wave writes its finished 4-value groups, converted to the
+// output type, into a staged [token][column] tile in the ring (free after the
+// last stage): 16-byte chunk c of staged row r sits at slot c ^ (r & mask), so
+// a fragment's 16 rows land on distinct slots. The block then copies whole
+// 16-byte chunks row by row, each wave store covering 1 KB of consecutive
+// columns. Tiles larger than the ring go in passes of kRowsPerPass tokens.
+// Needs row widths in bytes that are multiples of 16 (the caller checks);
+// chunks past the last column or token are skipped whole.
+template <int kRowBytes, int kRowsPerPass>
+struct StagedTile {
+  static constexpr int kChunks = kRowBytes / 16;
+  static constexpr int kMask = (kChunks < 16 ? kChunks : 16) - 1;
+  char* lds;
+  __device__ __forceinline__ char* slot(int row, int byte) const {
+    return lds + row * kRowBytes + ((((byte >> 4) ^ (row & kMask)) << 4) | (byte & 15));
+  }
+  // Copies staged rows [0, rows) to dst row by row (ld_bytes apart), columns
+  // [0, col_bytes) of each.
+  template <int kThreads>
+  __device__ __forceinline__ void copy_out(char* dst, size_t ld_bytes, int rows, int col_bytes) const {
+    static_assert((kRowsPerPass * kChunks) % kThreads == 0, "whole copy rounds");
+#pragma unroll 4
+    for (int it = 0; it < kRowsPerPass * kChunks / kThreads; ++it) {
+      const int idx = it * kThreads + static_cast<int>(threadIdx.x);
+      const int r = idx / kChunks, c = idx % kChunks;
+      if (r < rows && c * 16 < col_bytes) {
+        const uint4 v = *reinterpret_cast<const uint4*>(lds + r * kRowBytes + ((c ^ (r & kMask)) << 4));
+        *reinterpret_cast<uint4*>(dst + r * ld_bytes + c * 16) = v;
+      }
+    }
+  }
+};
+
+// Whether the ring kernel's epilogue goes through StagedTile: every output
+// but the RoPE one, when the output is 16-byte aligned and its rows are whole
+// 16-byte chunks.
+__device__ __forceinline__ bool staged_store_ok(const GemmGrid& grid, const void* Y, const float* partial,
+                                                bool fp32_out, int N) {
+  if (partial == nullptr && !fp32_out && grid.rope.table != nullptr) return false;
+  const void* out = partial != nullptr ? static_cast<const void*>(partial) : Y;
+  if ((reinterpret_cast<uintptr_t>(out) & 15) != 0) return false;
+  if (grid.ffn > 0 && partial == nullptr) return (grid.ffn & 7) == 0;
+  return (partial != nullptr || fp32_out) ? (N & 3) == 0 : (N & 7) == 0;
+}
+
+// The ring tile's store through LDS (see StagedTile): gated tiles write
+// act[t][f] = SwiGLU of fragments 2m and 2m + 1, split tiles their fp32
+// partial products, others Y in the output type. `lds` holds kLdsBytes.
+template <int BW, int BT, int FW, int FT, int kThreads, int kLdsBytes, bool kFp32Out>
+__device__ __forceinline__ void store_ring_tile_staged(const mfma_acc4 (&acc)[FW][FT], void* Y, float* partial,
+                                                       int T, int N, int ffn, int t0, int w0, int wt, int ww,
+                                                       int col, int grp, char* lds) {
+  const int rows_left = T - t0;
+  if (ffn > 0 && partial == nullptr) {
+    constexpr int kRowBytes = BW / 2 * static_cast<int>(sizeof(elem_t));
+    static_assert(BT * kRowBytes <= kLdsBytes, "gated tile fits the ring");
+    const StagedTile<kRowBytes, BT> tile{lds};
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FT; ++j) {
+      const int r = wt + 16 * j + col;
+#pragma unroll
+      for (int m = 0; m < FW / 2; ++m) {
+        const int fl = (ww + 32 * m) / 2 + 4 * grp;
+        uint2 packed;
+        packed.x = pack_elems(swiglu_rounded(acc[2 * m][j][0], acc[2 * m + 1][j][0]),
+                              swiglu_rounded(acc[2 * m][j][1], acc[2 * m + 1][j][1]));
+        packed.y = pack_elems(swiglu_rounded(acc[2 * m][j][2], acc[2 * m + 1][j][2]),
+                              swiglu_rounded(acc[2 * m][j][3], acc[2 * m + 1][j][3]));
+        *reinterpret_cast<uint2*>(tile.slot(r, fl * static_cast<int>(sizeof(elem_t)))) = packed;
+      }
+    }
+    __syncthreads();
+    const int f0 = w0 / 2;
+    tile.template copy_out<kThreads>(
+        reinterpret_cast<char*>(static_cast<elem_t*>(Y) + static_cast<size_t>(t0) * ffn + f0),
+        static_cast<size_t>(ffn) * sizeof(elem_t), rows_left, (ffn - f0) * static_cast<int>(sizeof(elem_t)));
+    return;
+  }
+  if (kFp32Out || partial != nullptr) {
+    constexpr int kRowBytes = BW * 4;
+    constexpr int kRowsPerPass = (BT * kRowBytes <= kLdsBytes) ? BT : kLdsBytes / kRowBytes;
+    static_assert(kRowsPerPass % 16 == 0 && BT % kRowsPerPass == 0, "passes of whole fragments");
+    const StagedTile<kRowBytes, kRowsPerPass> tile{lds};
+    float* out = partial != nullptr ? partial : static_cast<float*>(Y);
+#pragma unroll
+    for (int pass = 0; pass < BT / kRowsPerPass; ++pass) {
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < FT; ++j) {
+        const int r = wt + 16 * j + col - pass * kRowsPerPass;
+        if (wt + 16 * j < pass * kRowsPerPass || wt + 16 * j >= (pass + 1) * kRowsPerPass) continue;
+#pragma unroll
+        for (int i = 0; i < FW; ++i) {
+          *reinterpret_cast<float4*>(tile.slot(r, (ww + 16 * i + 4 * grp) * 4)) =
+              float4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        }
+      }
+      __syncthreads();
+      const int first = t0 + pass * kRowsPerPass;
+      tile.template copy_out<kThreads>(reinterpret_cast<char*>(out + static_cast<size_t>(first) * N + w0),
+                                       static_cast<size_t>(N) * 4, T - first, (N - w0) * 4);
+    }
+    return;
+  }
+  constexpr int kRowBytes = BW * static_cast<int>(sizeof(elem_t));
+  static_assert(BT * kRowBytes <= kLdsBytes, "tile fits the ring");
+  const StagedTile<kRowBytes, BT> tile{lds};
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < FT; ++j) {
+    const int r = wt + 16 * j + col;
+#pragma unroll
+    for (int i = 0; i < FW; ++i) {
+      uint2 packed;
+      packed.x = pack_elems(acc[i][j][0], acc[i][j][1]);
+      packed.y = pack_elems(acc[i][j][2], acc[i][j][3]);
+      *reinterpret_cast<uint2*>(tile.slot(r, (ww + 16 * i + 4 * grp) * static_cast<int>(sizeof(elem_t)))) = packed;
+    }
+  }
+  __syncthreads();
+  tile.template copy_out<kThreads>(
+      reinterpret_cast<char*>(static_cast<elem_t*>(Y) + static_cast<size_t>(t0) * N + w0),
+      static_cast<size_t>(N) * sizeof(elem_t), rows_left, (N - w0) * static_cast<int>(sizeof(elem_t)));
+}
+
 // Block tile BW x BT (W rows x tokens) over kWavesW x kWavesT waves; each
 // wave owns a (BW / kWavesW) x (BT / kWavesT) piece. Operands go global ->
 // registers -> LDS, a stage of 64 K ahead, through two LDS buffers.
@@ -573,6 +702,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
     const elem_t* nb =
         ring + ((next / kKSteps) % kStages) * kStageElems + (ww + col) * kRK + swz(next % kKSteps);
     read_tokens(next, bt_next);
+    // The wave holds issue priority over its SIMD's other wave while it runs
+    // its products, so that wave's loads and LDS reads issue in the matrix
+    // pipe's gaps instead of the two waves trading products (same bits;
+    // 256 x 128 tiles 4-5 % faster).
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int i = 0; i < FW; ++i) {
 #pragma unroll
@@ -587,6 +721,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
       __builtin_amdgcn_sched_group_barrier(0x008, FT, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
   // Before reading stage `next`: this wave's loads of it have landed (at most
   // the loads of the stages issued after it remain) and its earlier fragment
@@ -617,6 +752,12 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   }
 
   float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
+  if (staged_store_ok(grid, Y, partial, kFp32Out, N)) {
+    store_ring_tile_staged<BW, BT, FW, FT, 64 * kWaves, kStages * kStageElems * static_cast<int>(sizeof(elem_t)),
+                           kFp32Out>(acc, Y, partial, T, N, grid.ffn, t0, w0, wt, ww, col, grp,
+                                     reinterpret_cast<char*>(ring));
+    return;
+  }
   store_gemm_tile<FW, FT, kFp32Out>(acc, Y, partial, T, N, t0 + wt, w0 + ww, col, grp, grid);
 }
 

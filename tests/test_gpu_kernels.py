@@ -376,6 +376,10 @@ GEMM_CASES = [
     # 128 x 128 ring tiles: o_proj at 2048 tokens (one tile per compute unit),
     # ragged tokens and rows, and a split K
     (2048, 2048, 2048), (1500, 1000, 1024), (512, 3072, 2048),
+    # the LDS-staged epilogue: N % 8 == 4 (16-bit rows of whole 16-byte
+    # chunks no longer, so those stores go direct; fp32 rows still staged),
+    # and N ending mid-tile on 256 x 256 tiles
+    (600, 1004, 2048), (1100, 5000, 1024),
 ]
 
 
@@ -410,6 +414,21 @@ def test_gemm_mfma(gpu, orc, T, N, K):
         assert np.array_equal(runs[0], runs[1])
         got = runs[0] if fp32_out else to_f32(runs[0])
         expect_close(np.asarray(got).reshape(T, N), exp, tol, f"gemm_ws {T}x{N}x{K} ({ws_bytes} B workspace)")
+
+
+@pytest.mark.parametrize("fp32_out", [0, 1])
+def test_gemm_rejects_misaligned_output(gpu, fp32_out):
+    """The epilogue writes 16-byte chunks: an output 8 bytes past a 16-byte
+    boundary is an argument error, and the buffer is left as it was."""
+    lib = gpu
+    T, N, K = 70, 4096, 256
+    r = rng(T + N + K + fp32_out)
+    Xd, Wd = dev(random_elems(r, (T, K))), dev(random_elems(r, (N, K), 0.02))
+    dtype, esize = (np.float32, 4) if fp32_out else (np.uint16, 2)
+    shifted = zeros_dev(T * N + 8 // esize, dtype)
+    assert lib.lcr_gemm(ctypes.c_void_p(shifted.ptr + 8), fp32_out, p(Xd), p(Wd), T, N, K, NULL) != 0
+    assert b"16-byte aligned" in lib.lcr_last_error_message()
+    assert not host(shifted, dtype).any()
 
 
 def test_gemm_workspace_plans(gpu):

@@ -460,7 +460,7 @@ def main() -> int:
 
     # Per-kernel timing (dominant kernel first), live, on the model's stream.
     kernels = {}
-    for name in ("gate_up", "down", "lm_head", "qkv", "o_proj", "attention"):
+    for name in ("gate_up", "down", "lm_head", "qkv", "o_proj", "attention", "argmax"):
         ms, nbytes = model.time_decode_kernel(name, args.kernel_launches)
         kernels[name] = {"avg_us": ms * 1000.0, "bytes_per_launch": nbytes,
                          "gbs": nbytes / (ms / 1000.0) / 1e9}
@@ -513,6 +513,11 @@ def main() -> int:
         "decode_frac_of_peak": achieved_gbs / HBM_PEAK_GBS,
         "bytes_per_token": bytes_per_token,
         "roofline_tok_s": HBM_PEAK_GBS * 1e9 / bytes_per_token,
+        # ms/token as the reference defines it (decode() only, sampling
+        # excluded, src/main.cu:464): the timed step less its argmax kernel,
+        # timed alone; ms_per_step includes it.
+        "ms_per_token_excluding_sampling": ms_per_step - kernels["argmax"]["avg_us"] / 1000.0,
+        "ms_per_token_including_sampling": ms_per_step,
         "host_loop_ms_per_token": host_ms_per_token,
         "prefill_ms": prefill_ms,
         "prefill_tok_s": T / (prefill_ms / 1000.0),

@@ -97,7 +97,8 @@ int lcr_model_generate_sampled(lcr_model* model, int32_t first_token, int steps,
 /* extension: the split count decode uses at a sequence length. */
 int lcr_model_decode_splits(const lcr_model* model, int seq_len);
 /* extension: times one fused decode kernel in isolation ("qkv", "attention",
- * "o_proj", "gate_up", "down", "lm_head") over `launches` launches on the
+ * "o_proj", "gate_up", "down", "lm_head", or "argmax": the reduction of the
+ * head's per-block keys to the id alone) over `launches` launches on the
  * model's stream, each between its own pair of hipEvents, cycling through the
  * layers; returns the mean duration (ms) and the algorithmic bytes per launch.
  * Call after a prefill or decode. The kernels write their usual outputs (the

@@ -88,6 +88,9 @@ void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
 // Enqueues the output head and the argmax (which also advances the position;
 // leave it out only to time the head alone).
 void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t stream, bool with_argmax = true);
+// The argmax alone: the reduction of the output head's per-block keys to the
+// id, which also advances the position (timing only).
+void enqueue_decode_argmax(const DecodeStepArgs& a, hipStream_t stream);
 
 int lm_head_blocks(int vocab, int compute_units);
 

@@ -535,6 +535,11 @@ void enqueue_decode_head_sampled(const DecodeStepArgs& a, const SampledHead& h, 
                       a.sampled, step, s);
 }
 
+void enqueue_decode_argmax(const DecodeStepArgs& a, hipStream_t s) {
+  argmax_step_kernel<<<1, kThreads, 0, s>>>(a, lm_head_blocks(a.vocab, a.compute_units));
+  HIP_CHECK_LAUNCH();
+}
+
 void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t s, bool with_argmax) {
   const int blocks = lm_head_blocks(a.vocab, a.compute_units);
   lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a);

@@ -574,6 +574,7 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
   const double e = sizeof(elem_t);
   const int seq_len = position_;  // attention reads the positions present
   unsigned mask = 0;
+  bool argmax_only = false;
   double bytes = 0.0;
   if (kernel == "qkv") {
     mask = kDecodeQkv;
@@ -592,6 +593,9 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
     bytes = H * F * e + F * e + 2 * H * 4;
   } else if (kernel == "lm_head") {
     bytes = V * H * e + H * e + H * 4 + V * 4;
+  } else if (kernel == "argmax") {
+    argmax_only = true;
+    bytes = 8.0 * lm_head_blocks(config_.vocab_size, multiprocessors_) + 3 * 4;
   } else {
     LCR_FAIL("unknown decode kernel \"" << kernel << "\"");
   }
@@ -607,7 +611,9 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
   auto enqueue = [&]() {
     for (int i = 0; i < launches; ++i) {
       const int layer = i % config_.num_layers;
-      if (mask == 0) {
+      if (argmax_only) {
+        enqueue_decode_argmax(args, stream_);
+      } else if (mask == 0) {
         enqueue_decode_head(args, stream_, false);
       } else {
         const LayerWeights& lw = layers_[static_cast<size_t>(layer)];

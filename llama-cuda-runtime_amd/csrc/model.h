@@ -134,7 +134,8 @@ class Model {
   // model's stream, cycling through the layers so each launch streams
   // different weights, each bracketed by its own pair of hipEvents. Returns
   // the mean launch duration in ms and the algorithmic bytes one launch moves.
-  // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head".
+  // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", or
+  // "argmax" (the reduction of the head's per-block keys to the id alone).
   double time_decode_kernel(const std::string& kernel, int launches, double* bytes_per_launch);
 
  private:

@@ -221,3 +221,19 @@ def test_model_errors(lcr, small_ckpt):
         m.decode(1)
     with pytest.raises(lcr.LcrError, match=r"top_p must be in \(0, 1\]"):
         m.sample(0, 1.0, 0, 2.0, 0.5)
+
+
+def test_time_decode_kernel(lcr, small_ckpt):
+    """Each fused decode kernel, timed alone from a graph of back-to-back
+    launches, reports a positive mean time and the algorithmic bytes of one
+    launch (the o_proj figure: its weights, its input row, the residual read
+    and written); an unknown kernel is an argument error."""
+    m = lcr.Model(small_ckpt, max_seq=64)
+    m.prefill(list(range(1, 9)))
+    for name in ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax"):
+        ms, nbytes = m.time_decode_kernel(name, 8)
+        assert ms > 0.0 and nbytes > 0.0, name
+    assert m.time_decode_kernel("o_proj", 4)[1] == 2048 * 2048 * 2 + 2048 * 2 + 2 * 2048 * 4
+    with pytest.raises(lcr.LcrError, match="unknown decode kernel"):
+        m.time_decode_kernel("softmax", 4)
+    m.close()

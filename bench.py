@@ -330,6 +330,76 @@ def sampler_calls(lcr, config: dict, calls: int) -> dict:
     return {"calls": calls, "us_per_call_host": seconds * 1e6 / calls, "last_id": ids[-1]}
 
 
+PROJECTION_SHAPES = [("gate_up", 16384, 2048), ("down", 2048, 8192), ("qkv", 3072, 2048), ("o_proj", 2048, 2048)]
+
+
+def gemm_vs_hipblaslt(lcr, tokens=(2048, 512), rounds: int = 3, reps: int = 30) -> list:
+    """The model's four projection shapes at config 4's token counts:
+    lcr_gemm_ws (16-bit output, the workspace's plan) against torch.matmul
+    (hipBLASLt) into the same output, both on the default stream, timed with
+    hipEvents around `reps` back-to-back calls, best of `rounds`. Warm: one
+    weight matrix, resident in the 256 MB Infinity Cache after the first call;
+    cold: enough weight copies (cycled) to exceed 512 MB, as a prefill meets
+    each layer's weights. torch is only the library under comparison here."""
+    import ctypes
+    import torch
+    lib = lcr.load_library()
+    lib.lcr_gemm_workspace_bytes.restype = ctypes.c_size_t
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    warm = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16, generator=gen)
+    for _ in range(50):  # clocks up before the first measurement
+        warm @ warm
+    torch.cuda.synchronize()
+    del warm
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps * 1000.0
+
+    out = []
+    for cold in (False, True):
+        for T in tokens:
+            for name, N, K in PROJECTION_SHAPES:
+                X = (torch.randn(T, K, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+                copies = -(-512 * 2**20 // (N * K * 2)) if cold else 1
+                Ws = [(torch.randn(N, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+                Y = torch.empty(T, N, device=dev, dtype=torch.bfloat16)
+                ws_bytes = lib.lcr_gemm_workspace_bytes(T, N, K)
+                ws = torch.empty(max(ws_bytes, 16) // 4 + 4, device=dev, dtype=torch.float32)
+                turn = [0, 0]
+
+                def ours():
+                    W = Ws[turn[0] % copies]
+                    turn[0] += 1
+                    lcr.check(lib, lib.lcr_gemm_ws(ctypes.c_void_p(Y.data_ptr()), 0, ctypes.c_void_p(X.data_ptr()),
+                                                   ctypes.c_void_p(W.data_ptr()), T, N, K,
+                                                   ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws_bytes), None),
+                              "gemm_ws")
+
+                def library():
+                    W = Ws[turn[1] % copies]
+                    turn[1] += 1
+                    torch.matmul(X, W.t(), out=Y)
+
+                ours_us = min(timed(ours) for _ in range(rounds))
+                lib_us = min(timed(library) for _ in range(rounds))
+                out.append({"shape": name, "T": T, "N": N, "K": K, "weights": "cold" if cold else "warm",
+                            "lcr_us": round(ours_us, 1), "hipblaslt_us": round(lib_us, 1),
+                            "ratio": round(ours_us / lib_us, 3),
+                            "lcr_tflops": round(2.0 * T * N * K / (ours_us * 1e-6) / 1e12, 1)})
+                del Ws, X, Y, ws
+    return out
+
+
 def counters_run(lcr, model_dir: Path, prompt, max_seq: int) -> int:
     """Eager work for a rocprofv3 --pmc pass: every fused decode kernel is a
     separate dispatch, plus a 256 MiB device-to-device copy whose counter
@@ -367,6 +437,8 @@ def main() -> int:
     ap.add_argument("--sampling", action="store_true",
                     help="only run the config 5 fp16 stochastic-sampling loop and print its JSON")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemm-vs-hipblaslt", action="store_true",
+                    help="only the projection GEMMs against torch.matmul (hipBLASLt) at 512 and 2048 tokens")
     ap.add_argument("--sampler-calls", type=int, default=0, metavar="N",
                     help="only run N eager stochastic lcr_sample calls on synthetic logits (for profiling)")
     ap.add_argument("--decode-only", action="store_true",
@@ -387,6 +459,10 @@ def main() -> int:
     config = lcr.llama_config()
     if args.sampler_calls > 0:
         print(json.dumps({"sampler_calls": sampler_calls(lcr, config, args.sampler_calls)}))
+        return 0
+    if args.gemm_vs_hipblaslt:
+        for row in gemm_vs_hipblaslt(lcr):
+            print(json.dumps({"gemm_vs_hipblaslt": row}), flush=True)
         return 0
     if args.sampling:
         # This process loads only the fp16 library.

@@ -363,16 +363,84 @@ struct StagedTile {
   }
 };
 
-// Whether the ring kernel's epilogue goes through StagedTile: every output
-// but the RoPE one, when the output is 16-byte aligned and its rows are whole
-// 16-byte chunks.
+// Whether the ring kernel's epilogue goes through StagedTile: when every
+// destination is 16-byte aligned and its rows are whole 16-byte chunks.
 __device__ __forceinline__ bool staged_store_ok(const GemmGrid& grid, const void* Y, const float* partial,
                                                 bool fp32_out, int N) {
-  if (partial == nullptr && !fp32_out && grid.rope.table != nullptr) return false;
+  if (partial == nullptr && !fp32_out && grid.rope.table != nullptr) {
+    // The RoPE epilogue writes 16-byte chunks of query rows and cache rows.
+    const KvCacheView& v = grid.rope.view;
+    return ((reinterpret_cast<uintptr_t>(grid.rope.q_heads) | reinterpret_cast<uintptr_t>(v.keys) |
+             reinterpret_cast<uintptr_t>(v.values)) & 15) == 0 &&
+           (v.page_stride & 7) == 0 && (v.head_stride & 7) == 0;
+  }
   const void* out = partial != nullptr ? static_cast<const void*>(partial) : Y;
   if ((reinterpret_cast<uintptr_t>(out) & 15) != 0) return false;
   if (grid.ffn > 0 && partial == nullptr) return (grid.ffn & 7) == 0;
   return (partial != nullptr || fp32_out) ? (N & 3) == 0 : (N & 7) == 0;
+}
+
+// The RoPE epilogue from a staged tile of 16-bit projection outputs (already
+// rounded, as the unfused path rounds the q/k/v buffer): thread item (token
+// row, group of eight pairs i .. i + 7) loads that position's eight (cos, sin)
+// once and serves every head of the tile with them, rotating a query or key
+// head's pairs (i, i + half) into q_heads or the keys, or copying a value
+// head's; each write is a 16-byte chunk. The same arithmetic as
+// emit_rope_quad, so the same bits.
+template <int kHd, bool kPaged, int BW, int BT, int kThreads, class Tile>
+__device__ __forceinline__ void rope_copy_out(const Tile& tile, const GemmRope& r, int T, int N, int t0, int w0) {
+  constexpr int kHalf = kHd / 2;
+  constexpr int kGroups = kHalf / 8;
+  constexpr int kHeads = BW / kHd;
+  constexpr int kItems = BT * kGroups;
+  static_assert(BW % kHd == 0 && kItems % kThreads == 0, "whole heads per tile, whole item rounds");
+  const int kv_dim = r.view.num_kv_heads * kHd;
+#pragma unroll
+  for (int it = 0; it < kItems / kThreads; ++it) {
+    const int item = it * kThreads + static_cast<int>(threadIdx.x);
+    const int row = item / kGroups;
+    const int i = 8 * (item % kGroups);
+    const int t = t0 + row;
+    if (t >= T) continue;
+    const int position = r.start_position + t;
+    const float4* cs4 = reinterpret_cast<const float4*>(r.table + static_cast<size_t>(position) * kHalf + i);
+    float2 c[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 w = cs4[q];
+      c[2 * q] = make_float2(w.x, w.y);
+      c[2 * q + 1] = make_float2(w.z, w.w);
+    }
+#pragma unroll
+    for (int hb = 0; hb < kHeads; ++hb) {
+      const int row0 = w0 + hb * kHd;
+      if (row0 >= N) break;
+      const vec16 lo_v = *reinterpret_cast<const vec16*>(tile.slot(row, (hb * kHd + i) * 2));
+      const vec16 hi_v = *reinterpret_cast<const vec16*>(tile.slot(row, (hb * kHd + kHalf + i) * 2));
+      if (row0 >= r.q_dim + kv_dim) {
+        elem_t* dst = r.view.values + r.view.offset<kPaged>((row0 - r.q_dim - kv_dim) / kHd, position) + i;
+        store16(dst, lo_v);
+        store16(dst + kHalf, hi_v);
+        continue;
+      }
+      float lo[8], hi[8];
+      unpack8(lo_v, lo);
+      unpack8(hi_v, hi);
+      vec16 a, b;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float2 r0 = rope_rotate(lo[2 * v], hi[2 * v], c[2 * v]);
+        const float2 r1 = rope_rotate(lo[2 * v + 1], hi[2 * v + 1], c[2 * v + 1]);
+        a.w[v] = pack_elems(r0.x, r1.x);
+        b.w[v] = pack_elems(r0.y, r1.y);
+      }
+      elem_t* dst = row0 < r.q_dim
+                        ? r.q_heads + (static_cast<size_t>(row0 / kHd) * T + t) * kHd + i
+                        : r.view.keys + r.view.offset<kPaged>((row0 - r.q_dim) / kHd, position) + i;
+      store16(dst, a);
+      store16(dst + kHalf, b);
+    }
+  }
 }
 
 // The ring tile's store through LDS (see StagedTile): gated tiles write
@@ -380,8 +448,9 @@ __device__ __forceinline__ bool staged_store_ok(const GemmGrid& grid, const void
 // partial products, others Y in the output type. `lds` holds kLdsBytes.
 template <int BW, int BT, int FW, int FT, int kThreads, int kLdsBytes, bool kFp32Out>
 __device__ __forceinline__ void store_ring_tile_staged(const mfma_acc4 (&acc)[FW][FT], void* Y, float* partial,
-                                                       int T, int N, int ffn, int t0, int w0, int wt, int ww,
-                                                       int col, int grp, char* lds) {
+                                                       int T, int N, const GemmGrid& grid, int t0, int w0, int wt,
+                                                       int ww, int col, int grp, char* lds) {
+  const int ffn = grid.ffn;
   const int rows_left = T - t0;
   if (ffn > 0 && partial == nullptr) {
     constexpr int kRowBytes = BW / 2 * static_cast<int>(sizeof(elem_t));
@@ -451,6 +520,23 @@ __device__ __forceinline__ void store_ring_tile_staged(const mfma_acc4 (&acc)[FW
     }
   }
   __syncthreads();
+  if constexpr (!kFp32Out) {
+    if (grid.rope.table != nullptr) {
+      const GemmRope& r = grid.rope;
+      if (r.view.head_dim == 64) {
+        if (r.paged) {
+          rope_copy_out<64, true, BW, BT, kThreads>(tile, r, T, N, t0, w0);
+        } else {
+          rope_copy_out<64, false, BW, BT, kThreads>(tile, r, T, N, t0, w0);
+        }
+      } else if (r.paged) {
+        rope_copy_out<128, true, BW, BT, kThreads>(tile, r, T, N, t0, w0);
+      } else {
+        rope_copy_out<128, false, BW, BT, kThreads>(tile, r, T, N, t0, w0);
+      }
+      return;
+    }
+  }
   tile.template copy_out<kThreads>(
       reinterpret_cast<char*>(static_cast<elem_t*>(Y) + static_cast<size_t>(t0) * N + w0),
       static_cast<size_t>(N) * sizeof(elem_t), rows_left, (N - w0) * static_cast<int>(sizeof(elem_t)));
@@ -754,7 +840,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
   float* partial = grid.partial != nullptr ? grid.partial + static_cast<size_t>(work.split) * T * N : nullptr;
   if (staged_store_ok(grid, Y, partial, kFp32Out, N)) {
     store_ring_tile_staged<BW, BT, FW, FT, 64 * kWaves, kStages * kStageElems * static_cast<int>(sizeof(elem_t)),
-                           kFp32Out>(acc, Y, partial, T, N, grid.ffn, t0, w0, wt, ww, col, grp,
+                           kFp32Out>(acc, Y, partial, T, N, grid, t0, w0, wt, ww, col, grp,
                                      reinterpret_cast<char*>(ring));
     return;
   }

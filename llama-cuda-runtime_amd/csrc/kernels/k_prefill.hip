@@ -1164,16 +1164,6 @@ constexpr int kFlashThreads = 512;
 constexpr int kFlashKeys = 64;      // keys per tile; two tiles are staged per step
 constexpr int kKeyGroups = 2;
 
-// Slot of key k (0..63) of a tile in the transposed value rows: the order in
-// which a wave's S^T accumulators hand keys to the P operand. MFMA k-slot
-// 8g + j of a 32-key step holds key 4g + j (j < 4) or 16 + 4g + (j - 4).
-__device__ __forceinline__ int value_slot(int k) {
-  return (k & 32) | (((k & 15) >> 2) << 3) | ((k & 16) >> 2) | (k & 3);
-}
-// 16-byte group swizzle of transposed value row d: staging writes are at most
-// two-way bank conflicted and the operand reads are conflict free.
-__device__ __forceinline__ int value_swizzle(int d) { return ((d >> 3) ^ (d >> 1)) & 7; }
-
 // Key rows are head_dim elements with 16-byte chunk c at position
 // c ^ key_swizzle(key), so the fragment reads of 16 consecutive keys are free
 // of bank conflicts (measured on MI355X for 128-byte rows; 256-byte rows
@@ -1183,13 +1173,27 @@ __device__ __forceinline__ int key_swizzle(int key) {
   return kHeadDim == 64 ? (key & 7) : (key & 15);
 }
 
+// Value rows are kept as they are in the cache (key-major) with chunk c at
+// c ^ value_swizzle(key). The P.V operand is assembled by transposing reads
+// (ds_read_b64_tr_b16): in each 16-lane group, lane 4k + q names 8 bytes (4
+// dims) of one key row and lane 4q + c receives dim c of those 8 bytes from
+// the rows named by lanes 4k + q, k = 0..3. One read covers 16 rows x 32
+// bytes; with an even swizzle that takes each value twice over the rows of
+// one bank half, every bank serves the same number of dwords.
+template <int kHeadDim>
+__device__ __forceinline__ int value_swizzle(int key) {
+  return kHeadDim == 64 ? (key & 6) : ((key & 7) << 1);
+}
+
 template <int kHeadDim, int kRows>
 struct FlashShared {
   static constexpr int kKeyPitch = kHeadDim;
-  elem_t keys[2][kKeyGroups * kFlashKeys * kKeyPitch];           // two tiles per buffer
-  elem_t values_t[2][kKeyGroups][kHeadDim * kFlashKeys];
-  float stats[kFlashThreads / 64][kRows][2];                       // per wave: row max, row sum
+  elem_t keys[2][kKeyGroups * kFlashKeys * kKeyPitch];    // two tiles per buffer
+  elem_t values[2][kKeyGroups * kFlashKeys * kHeadDim];   // the same keys' values
+  float stats[kFlashThreads / 64][kRows][2];              // per wave: row max, row sum
 };
+
+typedef short lds_v4i16 __attribute__((ext_vector_type(4)));
 
 template <bool kPaged, int kHeadDim, int kRF>
 __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_prefill_kernel(
@@ -1199,12 +1203,13 @@ __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_p
   constexpr int kSteps = kHeadDim / 32;                   // MFMA k-steps over head_dim
   constexpr int kDFrags = kHeadDim / 16;                  // output fragments over head_dim
   constexpr int kPairKeys = kKeyGroups * kFlashKeys;      // keys staged per step
-  constexpr int kChunks = kPairKeys * kHeadDim / 8;       // 16-byte chunks of K (or V) per step
-  constexpr int kPer = kChunks / kFlashThreads;
   constexpr int kKeyPitch = FlashShared<kHeadDim, kRows>::kKeyPitch;
-  static_assert(kChunks % kFlashThreads == 0, "a step must split evenly over the block");
+  constexpr int kRowChunks = kHeadDim / 8;                // 16-byte chunks per key row
+  constexpr int kLoadRows = 64 / kRowChunks;              // rows of one 1 KiB direct load
+  constexpr int kWaveLoads = kPairKeys / kLoadRows / (kFlashThreads / 64);  // per wave, K or V
+  static_assert(kWaveLoads * kLoadRows * (kFlashThreads / 64) == kPairKeys, "a step splits over the waves");
   static_assert(kKeyGroups * 4 == kFlashThreads / 64, "one wave per (head, key group)");
-  __shared__ __attribute__((aligned(16))) FlashShared<kHeadDim, kRows> sh;
+  __shared__ __attribute__((aligned(1024))) FlashShared<kHeadDim, kRows> sh;
 
   // XCD-aware order: XCD x (block id mod 8) takes the contiguous run of units
   // [x * per, (x + 1) * per) of the kv-head-major order, so one XCD's L2 holds
@@ -1217,7 +1222,7 @@ __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_p
   if (u >= units) return;  // the whole block: no barrier has been met
   const int kv = u / row_blocks;
   const int r0 = (row_blocks - 1 - u % row_blocks) * kRows;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = lane_id();
   const int col = lane & 15;
   const int grp = lane >> 4;
@@ -1246,50 +1251,47 @@ __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_p
     }
   }
 
-  // Step `step` stages tiles 2 step and 2 step + 1: keys 128 step .. +127. A
-  // thread moves the same 16-byte chunk of two consecutive keys (even key
-  // first), whose transposed values sit in adjacent slots and go to LDS as
-  // 32-bit pairs.
-  constexpr int kPairs = kPer / 2;
-  static_assert(kPer % 2 == 0, "chunks move in key pairs");
-  vec16 kreg[kPer], vreg[kPer];
-  auto fetch = [&](int step, bool with_values) {
+  // Step `step` stages tiles 2 step and 2 step + 1 (keys 128 step .. +127)
+  // by direct global-to-LDS loads, no registers between: load n of a wave
+  // fills rows kLoadRows (8 n + wave) .. + kLoadRows - 1, lane i writing slot
+  // i % kRowChunks of row i / kRowChunks, so the lane loads the chunk whose
+  // swizzled position that slot is. Keys past the last position repeat it (the
+  // scores mask them).
+  const int load_row = lane / kRowChunks;
+  const int load_slot = lane % kRowChunks;
+  auto issue = [&](int step, int buf, bool with_values) {
 #pragma unroll
-    for (int c = 0; c < kPairs; ++c) {
-      const int pair = c * kFlashThreads + threadIdx.x;
-      const int key = 2 * (pair / (kHeadDim / 8));
-      const int d0 = (pair % (kHeadDim / 8)) * 8;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const size_t at = view.offset<kPaged>(kv, min(step * kPairKeys + key + e, last_key)) + d0;
-        kreg[2 * c + e] = load16(view.keys + at);
-        if (with_values) vreg[2 * c + e] = load16(view.values + at);
+    for (int n = 0; n < kWaveLoads; ++n) {
+      const int block_row = kLoadRows * (8 * n + wave);
+      const int row = block_row + load_row;
+      const size_t at = view.offset<kPaged>(kv, min(step * kPairKeys + row, last_key));
+      load_to_lds16(view.keys + at + 8 * (load_slot ^ key_swizzle<kHeadDim>(row)),
+                    lds_address_of(&sh.keys[buf][block_row * kKeyPitch]));
+      if (with_values) {
+        load_to_lds16(view.values + at + 8 * (load_slot ^ value_swizzle<kHeadDim>(row)),
+                      lds_address_of(&sh.values[buf][block_row * kHeadDim]));
       }
     }
   };
-  auto deposit = [&](int buf, bool with_values) {
-#pragma unroll
-    for (int c = 0; c < kPairs; ++c) {
-      const int pair = c * kFlashThreads + threadIdx.x;
-      const int key = 2 * (pair / (kHeadDim / 8));
-      const int d0 = (pair % (kHeadDim / 8)) * 8;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        store16(&sh.keys[buf][(key + e) * kKeyPitch + (((d0 >> 3) ^ key_swizzle<kHeadDim>(key + e)) << 3)],
-                kreg[2 * c + e]);
-      }
-      if (!with_values) continue;
-      const int slot = value_slot(key & (kFlashKeys - 1));  // even; key + 1 takes slot + 1
-      elem_t* vt = sh.values_t[buf][key / kFlashKeys];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int d = d0 + j;
-        const uint32_t lo = (vreg[2 * c].w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-        const uint32_t hi = (vreg[2 * c + 1].w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(&vt[d * kFlashKeys + ((((slot >> 3) ^ value_swizzle(d)) << 3) | (slot & 7))]) =
-            lo | (hi << 16);
-      }
-    }
+  // The A operand of O^T += V^T . P^T for dims 16 df .. + 15 and the 32 keys
+  // of half `half` of this wave's tile, in the order the P^T fragments hold
+  // them: k-slot 8 grp + j is key 32 half + 4 grp + j (j < 4) or
+  // 32 half + 16 + 4 grp + (j - 4). Two transposing reads, one per group of
+  // four keys; this lane names row 4 grp + col / 4 (+ 16) at dims
+  // 16 df + 4 (col % 4) .. + 3.
+  auto value_operand = [&](const elem_t* tile, int half, int df) {
+    typedef __attribute__((address_space(3))) lds_v4i16* lds_v4i16_ptr;
+    const int r0 = 32 * half + 4 * grp + (col >> 2);
+    const int c = 2 * df + ((col & 3) >> 1);
+    const int within = (col & 1) * 4;
+    const int r1 = r0 + 16;
+    const elem_t* p0 = tile + r0 * kHeadDim + ((c ^ value_swizzle<kHeadDim>(r0)) << 3) + within;
+    const elem_t* p1 = tile + r1 * kHeadDim + ((c ^ value_swizzle<kHeadDim>(r1)) << 3) + within;
+    const lds_v4i16 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(p0));
+    const lds_v4i16 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(p1));
+    typedef short v8i16 __attribute__((ext_vector_type(8)));
+    const v8i16 both = __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(mfma_in8, both);
   };
   // Scores q . k of this wave's tile of a staged step, transposed:
   // s[rf][kf][v] is row 16rf + col against key 16kf + 4grp + v of tile
@@ -1334,12 +1336,13 @@ __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_p
     m[rf] = -__builtin_huge_valf();
     l[rf] = 0.0f;
   }
-  fetch(0, false);
-  deposit(0, false);
+  issue(0, 0, false);
+  wait_stage_landed<0>();
   __syncthreads();
   for (int step = 0; step < steps; ++step) {
     const int buf = step & 1;
-    if (step + 1 < steps) fetch(step + 1, false);
+    // buf ^ 1 was last read in the previous step, before its closing barrier
+    if (step + 1 < steps) issue(step + 1, buf ^ 1, false);
     const int tile = kKeyGroups * step + kg;
     if (active && tile < tiles) {
       mfma_acc4 s[kRF][4];
@@ -1371,7 +1374,7 @@ __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_p
         m[rf] = m_new;
       }
     }
-    if (step + 1 < steps) deposit(buf ^ 1, false);
+    wait_stage_landed<0>();
     __syncthreads();
   }
   // Merge the two key groups, group 0 first: M = max(m0, m1),
@@ -1411,17 +1414,17 @@ __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_p
 #pragma unroll
     for (int df = 0; df < kDFrags; ++df) o[rf][df] = mfma_acc4{0.f, 0.f, 0.f, 0.f};
   }
-  fetch(0, true);
-  deposit(0, true);
+  issue(0, 0, true);
+  wait_stage_landed<0>();
   __syncthreads();
   for (int step = 0; step < steps; ++step) {
     const int buf = step & 1;
-    if (step + 1 < steps) fetch(step + 1, true);
+    if (step + 1 < steps) issue(step + 1, buf ^ 1, true);
     const int tile = kKeyGroups * step + kg;
     if (active && tile < tiles) {
       mfma_acc4 s[kRF][4];
       scores(buf, tile, s);
-      const elem_t* vt = sh.values_t[buf][kg];
+      const elem_t* vt = &sh.values[buf][kg * kFlashKeys * kHeadDim];
 #pragma unroll
       for (int rf = 0; rf < kRF; ++rf) {
         uint32_t pk[4][2];
@@ -1441,14 +1444,12 @@ __global__ __launch_bounds__(kFlashThreads, kHeadDim == 64 ? 4 : 2) void flash_p
           const mfma_in8 b = as_operand(pw);
 #pragma unroll
           for (int df = 0; df < kDFrags; ++df) {
-            const int d = df * 16 + col;
-            const mfma_in8 a = lds_operand(&vt[d * kFlashKeys + (((half * 4 + grp) ^ value_swizzle(d)) << 3)]);
-            o[rf][df] = mfma16x16x32(a, b, o[rf][df]);
+            o[rf][df] = mfma16x16x32(value_operand(vt, half, df), b, o[rf][df]);
           }
         }
       }
     }
-    if (step + 1 < steps) deposit(buf ^ 1, true);
+    wait_stage_landed<0>();
     __syncthreads();
   }
 

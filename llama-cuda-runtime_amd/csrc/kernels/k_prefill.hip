@@ -224,11 +224,15 @@ __device__ __forceinline__ void store_rope_tile(const mfma_acc4 (&acc)[FW][FT], 
 template <int FW, int FT>
 __device__ __forceinline__ void store_rope_heads(const mfma_acc4 (&acc)[FW][FT], const GemmRope& r, int T, int N,
                                                  int t_base, int w_base, int col, int grp) {
+  // Waves whose rows are not whole heads (the 192-row tile) always take the
+  // staged epilogue; the planner gives them no other case.
   if (r.view.head_dim == 64) {
-    if (r.paged) {
-      store_rope_tile<FW, FT, 2, true>(acc, r, T, N, t_base, w_base, col, grp);
-    } else {
-      store_rope_tile<FW, FT, 2, false>(acc, r, T, N, t_base, w_base, col, grp);
+    if constexpr (FW % 4 == 0) {
+      if (r.paged) {
+        store_rope_tile<FW, FT, 2, true>(acc, r, T, N, t_base, w_base, col, grp);
+      } else {
+        store_rope_tile<FW, FT, 2, false>(acc, r, T, N, t_base, w_base, col, grp);
+      }
     }
   } else if constexpr (FW % 8 == 0) {
     if (r.paged) {
@@ -341,7 +345,9 @@ __device__ __forceinline__ void store_gemm_tile(const mfma_acc4 (&acc)[FW][FT], 
 template <int kRowBytes, int kRowsPerPass>
 struct StagedTile {
   static constexpr int kChunks = kRowBytes / 16;
-  static constexpr int kMask = (kChunks < 16 ? kChunks : 16) - 1;
+  // XOR inside aligned groups of 16, 8 or 4 chunks (the largest that divides
+  // the row), so the swizzle stays a permutation of the row's chunks.
+  static constexpr int kMask = (kChunks % 16 == 0 ? 16 : kChunks % 8 == 0 ? 8 : 4) - 1;
   char* lds;
   __device__ __forceinline__ char* slot(int row, int byte) const {
     return lds + row * kRowBytes + ((((byte >> 4) ^ (row & kMask)) << 4) | (byte & 15));
@@ -529,10 +535,12 @@ __device__ __forceinline__ void store_ring_tile_staged(const mfma_acc4 (&acc)[FW
         } else {
           rope_copy_out<64, false, BW, BT, kThreads>(tile, r, T, N, t0, w0);
         }
-      } else if (r.paged) {
-        rope_copy_out<128, true, BW, BT, kThreads>(tile, r, T, N, t0, w0);
-      } else {
-        rope_copy_out<128, false, BW, BT, kThreads>(tile, r, T, N, t0, w0);
+      } else if constexpr (BW % 128 == 0) {  // the planner keeps 128-row heads off other tiles
+        if (r.paged) {
+          rope_copy_out<128, true, BW, BT, kThreads>(tile, r, T, N, t0, w0);
+        } else {
+          rope_copy_out<128, false, BW, BT, kThreads>(tile, r, T, N, t0, w0);
+        }
       }
       return;
     }
@@ -695,6 +703,8 @@ __device__ __forceinline__ void wait_stage_landed() {
 //    256 fp32 accumulators in the accumulation registers);
 //  - 256 x 128, kWaves = 8: wave tiles of 64 x 64, for token counts whose
 //    256-token tiles would leave compute units idle;
+//  - 192 x 128, kWaves = 8: wave tiles of 96 x 32 (three 64-row heads per
+//    block tile), so 3072 q/k/v rows and 2048 tokens make exactly 256 tiles;
 //  - 128 x 128, kWaves = 8: wave tiles of 64 x 32, for projections whose
 //    larger tiles would leave compute units idle (two blocks fit a CU).
 // kRK: K per ring stage, 32 (64-byte rows) or 64 (128-byte rows: twice the
@@ -706,9 +716,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_ring_kernel(void* __restrict
                                                                 GemmGrid grid) {
   static_assert(kRK == 32 || kRK == 64, "ring stages of 32 or 64 K");
   static_assert((BW == 256 && BT == 256 && (kWaves == 4 || kWaves == 8)) ||
-                    (BW == 256 && BT == 128 && kWaves == 8) || (BW == 128 && BT == 128 && kWaves == 8),
-                "supported ring tiles: 256 x 256 on 4 or 8 waves, 256 x 128 and 128 x 128 on 8 waves");
-  constexpr int kWavesW = (BW == 128 || BT == 256) ? 2 : 4;  // waves along W; the rest split the tokens
+                    ((BW == 256 || BW == 192 || BW == 128) && BT == 128 && kWaves == 8),
+                "supported ring tiles: 256 x 256 on 4 or 8 waves, 256 x 128, 192 x 128 and 128 x 128 on 8 waves");
+  // waves along W; the rest split the tokens
+  constexpr int kWavesW = (BW == 128 || BW == 192 || BT == 256) ? 2 : 4;
   constexpr int kWavesT = kWaves / kWavesW;
   constexpr int FW = BW / kWavesW / 16;  // W fragments of 16 rows per wave
   constexpr int FT = BT / kWavesT / 16;      // token fragments of 16 tokens per wave
@@ -860,6 +871,10 @@ constexpr int kRing256x128Stages = 3;
 // takes 24.2 us, 0.28 of a compute unit's peak, against 34-36 us for the
 // register-staged 128 x 128 kernel.
 constexpr double kRing128x128Efficiency = 0.28;
+// The 192 x 128 ring tile: three stages of 64 K (120 KiB of LDS).
+constexpr double kRing192x128Efficiency = 0.29;
+constexpr int kRing192x128K = 64;
+constexpr int kRing192x128Stages = 3;
 constexpr int kRing128x128K = 64;  // 64 K per stage, four stages (128 KiB of LDS)
 constexpr int kRing128x128Stages = 4;
 // Waves per ring block. Eight (two per SIMD) measured faster than four with
@@ -997,7 +1012,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(void* __restrict__ Y, 
   }
 }
 
-enum class GemmShape { kRing256x256, kRing256x128, kRing128x128, k256x256, k256x128, k128x128 };
+enum class GemmShape { kRing256x256, kRing256x128, kRing192x128, kRing128x128, k256x256, k256x128, k128x128 };
 
 struct GemmPlan {
   GemmShape shape;
@@ -1014,8 +1029,10 @@ struct GemmPlan {
 // partials' round trip through memory plus a launch. Each slice keeps at
 // least 256 K and is a whole number of the shape's K stages. With
 // wide_waves, an unsplit plan uses only shapes whose waves own 128 W rows
-// (the RoPE epilogue for 128-row heads).
-GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wide_waves = false) {
+// (the RoPE epilogue for 128-row heads). Without narrow_ok, no unsplit plan
+// uses the 192-row tile (its RoPE epilogue needs the staged store).
+GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wide_waves = false,
+                   bool narrow_ok = true) {
   struct Option {
     GemmShape shape;
     int bw, bt, stage_k;
@@ -1025,18 +1042,22 @@ GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wi
   const bool ring = K % kRingK == 0;
   const bool ring256x128 = K % kRing256x128K == 0;
   const bool ring128x128 = K % kRing128x128K == 0;
+  const bool ring192x128 = K % kRing192x128K == 0;
   const Option options[] = {
       {ring ? GemmShape::kRing256x256 : GemmShape::k256x256, 256, 256, ring ? kRingK : kStageK, ring ? 0.37 : 0.31},
       {ring256x128 ? GemmShape::kRing256x128 : GemmShape::k256x128, 256, 128,
        ring256x128 ? kRing256x128K : kStageK, ring256x128 ? kRing256x128Efficiency : 0.23},
       {ring128x128 ? GemmShape::kRing128x128 : GemmShape::k128x128, 128, 128,
-       ring128x128 ? kRing128x128K : kStageK, ring128x128 ? kRing128x128Efficiency : 0.20}};
+       ring128x128 ? kRing128x128K : kStageK, ring128x128 ? kRing128x128Efficiency : 0.20},
+      // ring only: the register-staged kernel has no 192-row tile
+      {GemmShape::kRing192x128, 192, 128, kRing192x128K, ring192x128 ? kRing192x128Efficiency : 0.0}};
   constexpr double kCuPeak = 9.8e12;     // bf16 dense flop/s per compute unit
   constexpr double kBandwidth = 5.0e12;  // sustained bytes/s for the partials' round trip
   constexpr double kLaunch = 4e-6;
   GemmPlan best{GemmShape::k128x128, 128, 128, 1, K, 0};
   double best_time = -1.0;
   for (const Option& o : options) {
+    if (o.efficiency <= 0.0) continue;
     const long long tiles = static_cast<long long>((N + o.bw - 1) / o.bw) * ((T + o.bt - 1) / o.bt);
     for (int splits = 1; splits <= 16; splits *= 2) {
       if (splits > 1 && tiles * (splits / 2) >= cus) break;  // already enough units
@@ -1044,6 +1065,7 @@ GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wi
       if (splits > 1 && k_chunk < 256) break;
       const int used = (K + k_chunk - 1) / k_chunk;
       if (wide_waves && used == 1 && o.bt != 256) continue;
+      if (!narrow_ok && used == 1 && o.bw == 192) continue;
       const size_t bytes = used > 1 ? static_cast<size_t>(used) * T * N * sizeof(float) : 0;
       if (bytes > workspace_bytes) break;
       const long long rounds = (tiles * used + cus - 1) / cus;
@@ -1089,8 +1111,15 @@ bool run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
               size_t workspace_bytes, int ffn, hipStream_t s, const GemmRope* rope = nullptr,
               const GemmNorm* norm = nullptr) {
   const bool wide_waves = rope != nullptr && rope->view.head_dim == 128;
-  const GemmPlan plan =
-      plan_gemm(T, N, K, device_compute_units(), workspace != nullptr ? workspace_bytes : 0, wide_waves);
+  // The staged RoPE epilogue's conditions (staged_store_ok), known here.
+  const bool narrow_ok =
+      rope == nullptr ||
+      (rope->view.head_dim == 64 &&
+       ((reinterpret_cast<uintptr_t>(rope->q_heads) | reinterpret_cast<uintptr_t>(rope->view.keys) |
+         reinterpret_cast<uintptr_t>(rope->view.values)) & 15u) == 0 &&
+       rope->view.page_stride % 8 == 0 && rope->view.head_stride % 8 == 0);
+  const GemmPlan plan = plan_gemm(T, N, K, device_compute_units(), workspace != nullptr ? workspace_bytes : 0,
+                                  wide_waves, narrow_ok);
   GemmGrid grid{(T + plan.bt - 1) / plan.bt, (N + plan.bw - 1) / plan.bw, plan.splits, plan.k_chunk,
                 plan.splits > 1 ? static_cast<float*>(workspace) : nullptr, ffn,
                 rope != nullptr ? *rope : GemmRope{}};
@@ -1103,6 +1132,9 @@ bool run_gemm(void* Y, bool fp32_out, const elem_t* X, const elem_t* W, int T, i
       break;
     case GemmShape::kRing128x128:
       launch_gemm_ring<128, 128, 8, kRing128x128Stages, kRing128x128K>(Y, fp32_out, X, W, T, N, K, grid, s);
+      break;
+    case GemmShape::kRing192x128:
+      launch_gemm_ring<192, 128, 8, kRing192x128Stages, kRing192x128K>(Y, fp32_out, X, W, T, N, K, grid, s);
       break;
     case GemmShape::k256x256:
       launch_gemm_tiles<256, 256, 2, 4>(Y, fp32_out, X, W, T, N, K, grid, s);

@@ -380,6 +380,9 @@ GEMM_CASES = [
     # chunks no longer, so those stores go direct; fp32 rows still staged),
     # and N ending mid-tile on 256 x 256 tiles
     (600, 1004, 2048), (1100, 5000, 1024),
+    # 192 x 128 ring tiles: q/k/v rows at 2048 tokens (256 tiles), and rows
+    # and tokens that end mid-tile
+    (2000, 3000, 2048),
 ]
 
 
@@ -517,7 +520,7 @@ def test_rope_table_matches_oracle(gpu, orc):
 
 QKV_ROPE_CASES = [
     # (T, num_heads, kv_heads, head_dim, K, start, paged): the Llama-3.2-1B
-    # projection at 2048 tokens (unsplit 256 x 128 ring tiles) and at 512
+    # projection at 2048 tokens (unsplit 192 x 128 ring tiles) and at 512
     # (K split, rotated in the reduction), a chunk continuing at a later
     # position, ragged token counts, N = 640 (a tile past the last head), one
     # token, and 128-wide heads (256 x 256 tiles when unsplit)
@@ -528,6 +531,9 @@ QKV_ROPE_CASES = [
     (1, 4, 2, 64, 256, 3, False),
     (300, 16, 4, 128, 1024, 7, True),
     (130, 8, 8, 128, 512, 0, False),
+    # 192-row tiles (three heads each): 3072 rows over 1900 tokens (the last
+    # token tile ragged) after 100 cached positions, paged
+    (1900, 32, 8, 64, 2048, 100, True),
 ]
 
 

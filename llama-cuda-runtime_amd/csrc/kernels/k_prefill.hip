@@ -1029,8 +1029,9 @@ struct GemmPlan {
 // partials' round trip through memory plus a launch. Each slice keeps at
 // least 256 K and is a whole number of the shape's K stages. With
 // wide_waves, an unsplit plan uses only shapes whose waves own 128 W rows
-// (the RoPE epilogue for 128-row heads). Without narrow_ok, no unsplit plan
-// uses the 192-row tile (its RoPE epilogue needs the staged store).
+// (the RoPE epilogue for 128-row heads). The 192-row tile is for unsplit
+// plans, and without narrow_ok for none (its RoPE epilogue needs the staged
+// store).
 GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wide_waves = false,
                    bool narrow_ok = true) {
   struct Option {
@@ -1065,7 +1066,9 @@ GemmPlan plan_gemm(int T, int N, int K, int cus, size_t workspace_bytes, bool wi
       if (splits > 1 && k_chunk < 256) break;
       const int used = (K + k_chunk - 1) / k_chunk;
       if (wide_waves && used == 1 && o.bt != 256) continue;
-      if (!narrow_ok && used == 1 && o.bw == 192) continue;
+      // 192-row tiles unsplit only: split four ways for q/k/v at 512 tokens
+      // they measured slower than 128 x 128 tiles split in two
+      if (o.bw == 192 && (used > 1 || !narrow_ok)) continue;
       const size_t bytes = used > 1 ? static_cast<size_t>(used) * T * N * sizeof(float) : 0;
       if (bytes > workspace_bytes) break;
       const long long rounds = (tiles * used + cus - 1) / cus;

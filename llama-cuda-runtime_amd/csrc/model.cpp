@@ -156,9 +156,9 @@ void Model::load_weights(const SafetensorsArchive& archive) {
 }
 
 // The split-K workspace the prefill projections use: the largest the GEMM
-// plans ask for over the four projection shapes at chunk lengths from the
-// maximum chunk down by halves (a chunk between two of these gets the plan
-// that fits).
+// plans ask for over the four projection shapes at every chunk length up to
+// the maximum chunk, so each chunk gets its preferred plan (a few thousand
+// plan evaluations of a few dozen operations each, once per model).
 size_t Model::gemm_workspace_bytes() const {
   const int hidden = config_.hidden_size;
   const int ffn = config_.intermediate_size;
@@ -167,7 +167,7 @@ size_t Model::gemm_workspace_bytes() const {
                             {2 * ffn, hidden},
                             {hidden, ffn}};
   size_t bytes = 0;
-  for (int T = max_tokens_; T >= 2; T /= 2) {
+  for (int T = 2; T <= max_tokens_; ++T) {
     for (const auto& s : shapes) bytes = std::max(bytes, lcr_gemm_workspace_bytes(T, s[0], s[1]));
   }
   return align_up(bytes, 256);

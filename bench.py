@@ -447,6 +447,9 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="with --decode-only: enqueue each step's kernels directly instead of replaying the "
                          "captured graph (the kernels and their order are the same)")
+    ap.add_argument("--no-exchange", action="store_true",
+                    help="run the decode step's q/k/v projection and attention as two kernels instead of "
+                         "the exchange grid (for comparison)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -488,7 +491,8 @@ def main() -> int:
         print(json.dumps({"long_context": long_context(lcr, model_dir, config, args.long_context)}))
         return 0
     t0 = time.perf_counter()
-    model = lcr.Model(model_dir, max_seq=args.max_seq, use_graph=0 if args.eager else 1)
+    model = lcr.Model(model_dir, max_seq=args.max_seq, use_graph=0 if args.eager else 1,
+                      decode_exchange=0 if args.no_exchange else 1)
     load_s = time.perf_counter() - t0
     st = model.stats()
     assert st.fused == 1, "the benchmark measures the fused decode step"
@@ -536,11 +540,14 @@ def main() -> int:
 
     # Per-kernel timing (dominant kernel first), live, on the model's stream.
     kernels = {}
-    for name in ("gate_up", "down", "lm_head", "qkv", "o_proj", "attention", "argmax"):
+    for name in ("gate_up", "down", "lm_head", "qkv_attention", "qkv", "o_proj", "attention", "argmax"):
         ms, nbytes = model.time_decode_kernel(name, args.kernel_launches)
         kernels[name] = {"avg_us": ms * 1000.0, "bytes_per_launch": nbytes,
                          "gbs": nbytes / (ms / 1000.0) / 1e9}
     dom = kernels["gate_up"]
+    exchange_enabled, exchange_failed = model.exchange_status()
+    if exchange_failed:
+        raise RuntimeError("an exchange wait of the timed decode steps gave up")
 
     # Prefill MFMA figures for the 128-token prompt.
     T = args.prompt
@@ -611,6 +618,7 @@ def main() -> int:
             "bytes_per_launch": dom["bytes_per_launch"],
         },
         "kernels": kernels,
+        "decode_exchange": exchange_enabled,
         **extra,
         "cpu_baseline": cpu,
         "oracle_greedy_parity": parity,

@@ -96,6 +96,9 @@ class ModelOptions(ctypes.Structure):
         ("fused_decode", ctypes.c_int),
         ("use_graph", ctypes.c_int),
         ("prefill_via_decode", ctypes.c_int),
+        ("decode_exchange", ctypes.c_int),
+        ("exchange_spins", ctypes.c_int),
+        ("exchange_test_unwritten", ctypes.c_int),
     ]
 
 
@@ -170,6 +173,8 @@ SIGNATURES = {
     "lcr_model_tap_count": (_I, [_P]),
     "lcr_model_tap": (_I, [_P, _I, ctypes.c_char_p, _SZ, ctypes.POINTER(_I), ctypes.POINTER(_I), _P, _SZ]),
     "lcr_model_set_profiling": (_I, [_P, _I]),
+    "lcr_model_exchange_status": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "lcr_model_exchange_clear": (_I, [_P]),
     "lcr_model_generate_greedy": (_I, [_P, ctypes.c_int32, _I, _P, ctypes.POINTER(ctypes.c_double)]),
     "lcr_model_generate_sampled": (_I, [_P, ctypes.c_int32, _I, _F, _I, _F, _P, _P,
                                         ctypes.POINTER(ctypes.c_double)]),
@@ -537,6 +542,17 @@ class Model:
                                                             u.ctypes.data, out.ctypes.data, ctypes.byref(ms)),
               "generate_sampled")
         return out, ms.value
+
+    def exchange_status(self):
+        """(enabled, status): whether decode steps run q/k/v and attention as one
+        exchange grid, and whether an exchange wait of a past step gave up."""
+        enabled, status = ctypes.c_int(), ctypes.c_int()
+        check(self.lib, self.lib.lcr_model_exchange_status(self.handle, ctypes.byref(enabled),
+                                                           ctypes.byref(status)), "exchange_status")
+        return bool(enabled.value), int(status.value)
+
+    def exchange_clear(self):
+        check(self.lib, self.lib.lcr_model_exchange_clear(self.handle), "exchange_clear")
 
     def time_decode_kernel(self, kernel: str, launches: int = 64):
         ms, nbytes = ctypes.c_double(), ctypes.c_double()

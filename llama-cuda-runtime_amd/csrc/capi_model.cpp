@@ -38,6 +38,9 @@ extern "C" void lcr_model_default_options(lcr_model_options* o) {
   o->fused_decode = 1;
   o->use_graph = 1;
   o->prefill_via_decode = 0;
+  o->decode_exchange = 1;
+  o->exchange_spins = 1 << 20;
+  o->exchange_test_unwritten = 0;
 }
 
 extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* options,
@@ -58,6 +61,9 @@ extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* 
     opt.fused_decode = o.fused_decode != 0;
     opt.use_graph = o.use_graph != 0;
     opt.prefill_via_decode = o.prefill_via_decode != 0;
+    opt.decode_exchange = o.decode_exchange != 0;
+    opt.exchange_spins = o.exchange_spins > 0 ? o.exchange_spins : (1 << 20);
+    opt.exchange_test_unwritten = o.exchange_test_unwritten != 0;
     auto handle = std::make_unique<lcr_model>();
     handle->impl = std::make_unique<Model>(model_dir, opt);
     *out = handle.release();
@@ -66,6 +72,24 @@ extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* 
 }
 
 extern "C" void lcr_model_destroy(lcr_model* model) { delete model; }
+
+extern "C" int lcr_model_exchange_status(const lcr_model* m, int* enabled, int* status) {
+  CAPI_MODEL(m);
+  CAPI_CHECK(enabled != nullptr && status != nullptr, "output pointers needed");
+  return capi::guarded([&]() -> int {
+    *enabled = m->impl->decode_exchange() ? 1 : 0;
+    *status = m->impl->exchange_status();
+    return LCR_OK;
+  });
+}
+
+extern "C" int lcr_model_exchange_clear(lcr_model* m) {
+  CAPI_MODEL(m);
+  return capi::guarded([&]() -> int {
+    m->impl->clear_exchange();
+    return LCR_OK;
+  });
+}
 
 extern "C" int lcr_model_prefill(lcr_model* m, const int32_t* tokens, int count,
                                  const float** logits) {

@@ -51,6 +51,7 @@
 
 #include "../kv_cache.h"
 #include "device_common.h"
+#include "exchange.h"
 
 namespace lcr {
 
@@ -86,6 +87,19 @@ struct AttnShared {
   // Paged layout: the 16-byte-chunk index of position begin + i of the
   // block's range (chunk 0 of that position's key and value rows).
   uint32_t chunks[kPaged ? kAttnPositionTable : 1];
+};
+
+// What a block that runs inside the q/k/v projection's grid takes from it
+// (exchange.h): its query head and the key and value of the new position as
+// 3 * head_dim exchange words (query, key, value), plus LDS for them once
+// taken.
+template <int kHeadDim>
+struct AttnExchange {
+  unsigned long long* words;     // [3][kHeadDim]
+  int spins;
+  int* status;
+  float* q_lds;                  // [kHeadDim] LDS
+  elem_t* kv_lds;                // [2][kHeadDim] LDS, 16-byte aligned
 };
 
 // Step 3's reduce-scatter: at offset O the lane keeps the half of its N values
@@ -133,14 +147,22 @@ using attn_flag = std::integral_constant<bool, B>;
 // issued after a tile's keys would hold the next tile's requests until those
 // keys were in. Tiles whose 64 positions are all in range skip the masking
 // selects.
-template <bool kPaged, int kHeadDim, int kHeads>
+//
+// kExchange (one head, one split): the block runs inside the q/k/v
+// projection's grid. Its query and the new position's key and value are not
+// in memory yet; it issues its first tiles' cache loads, then takes them from
+// exchange words (`x`), and uses the taken key and value in place of the
+// cache's for position seq_len - 1. The arithmetic is unchanged.
+template <bool kPaged, int kHeadDim, int kHeads, bool kExchange = false>
 __device__ __forceinline__ void decode_attention_block(
     AttnShared<kPaged, kHeadDim, kHeads>& sh, elem_t* __restrict__ out,
     float* __restrict__ partials, const elem_t* __restrict__ q, const KvCacheView& view,
-    int kv_head, int head0, int split, int splits, int seq_len, float scale) {
+    int kv_head, int head0, int split, int splits, int seq_len, float scale,
+    const AttnExchange<kHeadDim>* x = nullptr) {
   constexpr int P = kHeadDim / 8;   // chunks per position
   constexpr int Q = 64 / P;         // positions per load instruction
   constexpr int G = kHeads;
+  static_assert(!kExchange || (kHeads == 1 && P <= 8), "exchange blocks serve one head");
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) >> 6;
   const int j = lane % P;
@@ -178,13 +200,59 @@ __device__ __forceinline__ void decode_attention_block(
   if constexpr (kPaged) fill_table(0);
 
   float qv[G][8];
+  if constexpr (!kExchange) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const vec16 raw = load16(q + static_cast<size_t>(head0 + g) * kHeadDim + 8 * j);
-    unpack8(raw, qv[g]);
+    for (int g = 0; g < G; ++g) {
+      const vec16 raw = load16(q + static_cast<size_t>(head0 + g) * kHeadDim + 8 * j);
+      unpack8(raw, qv[g]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qv[g][e] *= scale;
+      for (int e = 0; e < 8; ++e) qv[g][e] *= scale;
+    }
   }
+  // kExchange: wave 0 takes the query and the new key and value from the
+  // exchange words into LDS; after the barrier every lane reads its query
+  // chunk. Every wave calls this exactly once, after its first tile's loads.
+  auto exchange_wait = [&]() {
+    if constexpr (kExchange) {
+      static_assert(kHeadDim % 64 == 0, "exchange blocks take whole waves of words");
+      constexpr int N = 3 * kHeadDim / 64;
+      if (wave == 0) {
+        float vals[N];
+        exchange_take<N>(x->words, vals, x->spins, x->status);
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+          const int i = lane + 64 * k;  // word i: query, key, value in turn
+          if (i < kHeadDim) {
+            x->q_lds[i] = vals[k];
+          } else {
+            x->kv_lds[i - kHeadDim] = float_to_elem(vals[k]);
+          }
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[0][e] = x->q_lds[8 * j + e] * scale;
+    }
+  };
+  // kExchange: position seq_len - 1 (index length - 1 of the one split) comes
+  // from the exchange, not from the cache, whose copy its producer may not
+  // have written yet: the lanes holding it overwrite their chunk of the tile
+  // that contains it (the last tile of the range, the last one its wave
+  // processes, so no later load of that wave is still in flight).
+  auto patch_new = [&](int tile, vec16 (&kr)[P], vec16 (&vr)[P]) {
+    if constexpr (kExchange) {
+      const int idx = length - 1;
+      if (tile != idx / kAttnTile) return;
+      const int in_tile = idx % kAttnTile;
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        if (i * Q + a == in_tile) {
+          kr[i] = load16(x->kv_lds + 8 * j);
+          vr[i] = load16(x->kv_lds + kHeadDim + 8 * j);
+        }
+      }
+    }
+  };
 
   float m[G], l_lane[G], acc[G][8];
 #pragma unroll
@@ -358,7 +426,10 @@ __device__ __forceinline__ void decode_attention_block(
   // them for its tile), so they keep one set and refill the keys as soon as
   // the scores are taken and the values as soon as they are used.
   auto run_tiles = [&](int first_tile, int last_tile, int window) {
-    if (first_tile + wave >= last_tile) return;
+    if (first_tile + wave >= last_tile) {
+      if (window == 0) exchange_wait();
+      return;
+    }
     if constexpr (G <= 2 && P <= 8) {
       auto process = [&](int tile, const vec16 (&kr)[P], const vec16 (&vr)[P]) {
         const int count = tile_count(tile);
@@ -382,6 +453,7 @@ __device__ __forceinline__ void decode_attention_block(
       tile_chunks(tile, window, o);
       load_chunks(view.keys, o, ka);
       load_chunks(view.values, o, va);
+      bool first = window == 0;
       while (true) {
         const int t1 = tile + kAttnWaves;
         const bool more1 = t1 < last_tile;
@@ -390,6 +462,11 @@ __device__ __forceinline__ void decode_attention_block(
           load_chunks(view.keys, o, kb);
           load_chunks(view.values, o, vb);
         }
+        if (first) {
+          exchange_wait();
+          first = false;
+        }
+        patch_new(tile, ka, va);
         process(tile, ka, va);
         if (!more1) break;
         const int t2 = t1 + kAttnWaves;
@@ -399,6 +476,7 @@ __device__ __forceinline__ void decode_attention_block(
           load_chunks(view.keys, o, ka);
           load_chunks(view.values, o, va);
         }
+        patch_new(t1, kb, vb);
         process(t1, kb, vb);
         if (!more2) break;
         tile = t2;

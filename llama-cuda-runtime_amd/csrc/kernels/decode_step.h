@@ -64,10 +64,24 @@ struct DecodeStepArgs {
   bool paged;
   int splits;
   int compute_units;         // of the device: sizes the output head's grid
+  // In-grid exchange (exchange.h): when set and splits == 1, the q/k/v
+  // projection and the attention run as one grid. Words: [num_heads][3][head_dim].
+  unsigned long long* exchange;
+  int* exchange_status;      // [1] raised by a wait that gave up
+  int exchange_spins;        // polls before a wait gives up
+  int exchange_read_offset;  // added to the words the attention blocks read (0; tests)
 };
 
 // True when the fused kernels are compiled for this geometry.
 bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads, int head_dim);
+// True when the q/k/v + attention exchange grid is compiled for this geometry
+// and all its blocks fit on the device at once.
+bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, bool paged, int compute_units);
+// Exchange words the step needs (3 * num_heads * head_dim) plus the same
+// again, never written, for the tests of the give-up path.
+inline size_t decode_exchange_words(int num_heads, int head_dim) {
+  return 6 * static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim);
+}
 
 // The five kernels of a layer, as bits of a selection mask.
 enum DecodeKernel : unsigned {

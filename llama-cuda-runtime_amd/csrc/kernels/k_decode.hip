@@ -6,6 +6,7 @@
 #include "../hip_utils.h"
 #include "attention_decode.h"
 #include "decode_step.h"
+#include "exchange.h"
 #include "gemv_core.h"
 #include "row_norm.h"
 #include "sampling.h"
@@ -48,10 +49,12 @@ struct NormInput {
 };
 
 // `load_chunk(c, out8)` yields the 8 floats of chunk c of v.
+// Threads from kThreads on (blocks of more than kThreads threads) take no part.
 template <int NCH, typename LoadChunk>
 __device__ __forceinline__ void norm_load(NormInput<NCH>& in, LoadChunk load_chunk,
                                           const elem_t* __restrict__ w) {
   const int t = threadIdx.x;
+  if (t >= kThreads) return;
 #pragma unroll
   for (int c = 0; c < NormInput<NCH>::kPer; ++c) {
     const int chunk = t + c * kThreads;
@@ -61,23 +64,28 @@ __device__ __forceinline__ void norm_load(NormInput<NCH>& in, LoadChunk load_chu
 }
 
 // Finishes the norm into `xs` (all threads; two barriers, the first inside
-// the sum of squares; `scratch` is used once per kernel). When `resid_out` is
-// set, the thread also stores its v chunks there (layer 0 seeding the
-// residual sum with the embedding row).
+// the sum of squares; `scratch` is used once per kernel and holds one float
+// per 32 threads of the block). When `resid_out` is set, the thread also
+// stores its v chunks there (layer 0 seeding the residual sum with the
+// embedding row). Threads from kThreads on contribute nothing.
 template <int NCH>
 __device__ __forceinline__ void norm_finish(elem_t* xs, const NormInput<NCH>& in, float eps,
                                             float* scratch, float* resid_out) {
   constexpr int H = NCH * 512;
   const int t = threadIdx.x;
+  const bool active = t < kThreads;
   float s = 0.0f;
+  if (active) {
 #pragma unroll
-  for (int c = 0; c < NormInput<NCH>::kPer; ++c) {
+    for (int c = 0; c < NormInput<NCH>::kPer; ++c) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s = __builtin_fmaf(in.v[c][j], in.v[c][j], s);
+      for (int j = 0; j < 8; ++j) s = __builtin_fmaf(in.v[c][j], in.v[c][j], s);
+    }
   }
   const float scale = norm_scale(block_norm_total_once(s, scratch), H, eps);
 #pragma unroll
   for (int c = 0; c < NormInput<NCH>::kPer; ++c) {
+    if (!active) break;
     const int chunk = t + c * kThreads;
     const float* v = in.v[c];
     if (resid_out != nullptr) {
@@ -120,27 +128,37 @@ __device__ __forceinline__ void load_resid_chunk(const float* resid, int chunk, 
 // 1. QKV projection + RoPE + KV append
 // ---------------------------------------------------------------------------
 
-// A block serves 2 * kQkvRowsPerWave rotation pairs (i, i + head_dim / 2) of
-// one head: waves 0 and 1 take the first rows of the pairs, waves 2 and 3 the
-// second ones, kQkvRowsPerWave rows each.
-template <int NCH, int HD, bool kPaged>
-__global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, LayerDevicePtrs w,
-                                                            KvCacheView view, int layer) {
+// LDS of a q/k/v block with `PAIRS` rotation pairs.
+template <int NCH, int PAIRS>
+struct QkvShared {
+  __attribute__((aligned(16))) elem_t xs[NCH * 512];
+  float scratch[16];
+  float rowv[2 * PAIRS];
+};
+
+// Block `block` of the q/k/v projection, with WAVES waves of RW rows each.
+// It serves PAIRS = WAVES / 2 * RW rotation pairs (i, i + head_dim / 2) of one
+// head: the first WAVES / 2 waves take the first rows of the pairs, the others
+// the second ones. With kPublish the rotated query and key values and the
+// value rows also go out as exchange words (exchange.h) for the attention
+// blocks of the same grid, 3 * HD words per query head h: its query at
+// x[3 h HD + i], and the key and value of its kv head at x[3 h HD + HD + i]
+// and x[3 h HD + 2 HD + i] (a kv head's once for each of its G query heads).
+template <int NCH, int HD, bool kPaged, int WAVES, int RW, int G, bool kPublish>
+__device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDevicePtrs& w,
+                                          const KvCacheView& view, int layer, int block,
+                                          QkvShared<NCH, WAVES / 2 * RW>& sh) {
   constexpr int H = NCH * 512;
   constexpr int HALF = HD / 2;
-  constexpr int RW = kQkvRowsPerWave;
-  constexpr int PAIRS = 2 * RW;  // rotation pairs per block
+  constexpr int PAIRS = WAVES / 2 * RW;  // rotation pairs per block
   constexpr int BLOCKS_PER_HEAD = HALF / PAIRS;
   static_assert(HALF % PAIRS == 0, "head_dim / 2 must be a multiple of the pairs per block");
-  __shared__ __attribute__((aligned(16))) elem_t xs[H];
-  __shared__ float scratch[9];
-  __shared__ float rowv[2 * PAIRS];
 
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
-  const int head = blockIdx.x / BLOCKS_PER_HEAD;
-  const int i0 = (blockIdx.x % BLOCKS_PER_HEAD) * PAIRS;
-  const int r0 = i0 + (wave & 1) * RW + ((wave >> 1) ? HALF : 0);  // row within the head
+  const int head = block / BLOCKS_PER_HEAD;
+  const int i0 = (block % BLOCKS_PER_HEAD) * PAIRS;
+  const int r0 = i0 + (wave % (WAVES / 2)) * RW + ((wave / (WAVES / 2)) ? HALF : 0);  // row within the head
 
   // Everything the prologue and epilogue read is requested before the weight
   // tile, so its latency hides under the stream: the position, the rotation
@@ -166,40 +184,75 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, La
     tile.load(rows, lane);
   }
 
-  norm_finish<NCH>(xs, nin, a.eps, scratch, (layer == 0 && blockIdx.x == 0) ? a.resid : nullptr);
+  norm_finish<NCH>(sh.xs, nin, a.eps, sh.scratch, (layer == 0 && block == 0) ? a.resid : nullptr);
 
   vec16 xv[NCH];
-  load_x_lds<NCH>(xv, xs, lane);
+  load_x_lds<NCH>(xv, sh.xs, lane);
   float out[RW];
   tile.dot(out, xv);
   if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < RW; ++r) rowv[wave * RW + r] = elem_to_float(float_to_elem(out[r]));
+    for (int r = 0; r < RW; ++r) sh.rowv[wave * RW + r] = elem_to_float(float_to_elem(out[r]));
   }
   __syncthreads();
 
   if (static_cast<int>(threadIdx.x) < PAIRS) {
     const int k = threadIdx.x;
     const int i = i0 + k;
-    const float lo = rowv[k];
-    const float hi = rowv[PAIRS + k];
+    const float lo = sh.rowv[k];
+    const float hi = sh.rowv[PAIRS + k];
+    unsigned long long* xw = a.exchange;
     if (head < a.num_heads + a.num_kv_heads) {
       const float ra = lo * rot.x - hi * rot.y;
       const float rb = hi * rot.x + lo * rot.y;
+      const elem_t ea = float_to_elem(ra);
+      const elem_t eb = float_to_elem(rb);
       if (head < a.num_heads) {
-        a.q[head * HD + i] = float_to_elem(ra);
-        a.q[head * HD + i + HALF] = float_to_elem(rb);
+        a.q[head * HD + i] = ea;
+        a.q[head * HD + i + HALF] = eb;
+        if constexpr (kPublish) {
+          unsigned long long* dst = xw + static_cast<size_t>(3 * head) * HD;
+          exchange_put(dst + i, elem_to_float(ea));
+          exchange_put(dst + i + HALF, elem_to_float(eb));
+        }
       } else {
-        const size_t off = view.offset<kPaged>(head - a.num_heads, pos);
-        view.keys[off + i] = float_to_elem(ra);
-        view.keys[off + i + HALF] = float_to_elem(rb);
+        const int kvh = head - a.num_heads;
+        const size_t off = view.offset<kPaged>(kvh, pos);
+        view.keys[off + i] = ea;
+        view.keys[off + i + HALF] = eb;
+        if constexpr (kPublish) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            unsigned long long* dst = xw + static_cast<size_t>(3 * (kvh * G + g) + 1) * HD;
+            exchange_put(dst + i, elem_to_float(ea));
+            exchange_put(dst + i + HALF, elem_to_float(eb));
+          }
+        }
       }
     } else {
-      const size_t off = view.offset<kPaged>(head - a.num_heads - a.num_kv_heads, pos);
-      view.values[off + i] = float_to_elem(lo);
-      view.values[off + i + HALF] = float_to_elem(hi);
+      const int kvh = head - a.num_heads - a.num_kv_heads;
+      const size_t off = view.offset<kPaged>(kvh, pos);
+      const elem_t ea = float_to_elem(lo);
+      const elem_t eb = float_to_elem(hi);
+      view.values[off + i] = ea;
+      view.values[off + i + HALF] = eb;
+      if constexpr (kPublish) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          unsigned long long* dst = xw + static_cast<size_t>(3 * (kvh * G + g) + 2) * HD;
+          exchange_put(dst + i, elem_to_float(ea));
+          exchange_put(dst + i + HALF, elem_to_float(eb));
+        }
+      }
     }
   }
+}
+
+template <int NCH, int HD, bool kPaged>
+__global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, LayerDevicePtrs w,
+                                                            KvCacheView view, int layer) {
+  __shared__ QkvShared<NCH, kWaves / 2 * kQkvRowsPerWave> sh;
+  qkv_block<NCH, HD, kPaged, kWaves, kQkvRowsPerWave, 1, false>(a, w, view, layer, blockIdx.x, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -254,6 +307,56 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStep
   if (split >= splits) return;
   decode_attention_block<kPaged, HD, kHeads>(sh, a.attn, a.partials, a.q, view, kv_head,
                                              kv_head * G + g * kHeads, split, splits, seq_len, scale);
+}
+
+// q/k/v projection and single-split attention in one grid (exchange.h). The
+// first qkv_blocks blocks are the projection (kAttnWaves waves of
+// kQkvRowsPerWave rows, 16 rows per block) and publish what they compute; the
+// last num_heads blocks are the attention, one query head each, numbered as
+// attention_step_kernel numbers them (qkv_blocks is a multiple of the eight
+// XCDs, so each kv head's blocks still share one XCD). An attention block
+// issues its first cache tiles while the projection streams its weights, then
+// takes its query and the new key and value from the exchange words. Same
+// arithmetic, same bits as qkv_rope_kernel followed by attention_step_kernel.
+template <int NCH, int HD, bool kPaged>
+struct ExchangeStepShared {
+  union {
+    QkvShared<NCH, kAttnWaves / 2 * kQkvRowsPerWave> qkv;
+    struct {
+      AttnShared<kPaged, HD, 1> attn;
+      float q[HD];
+      __attribute__((aligned(16))) elem_t kv[2 * HD];
+    } at;
+  };
+};
+
+template <int NCH, int HD, bool kPaged, int G>
+__global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepArgs a, LayerDevicePtrs w,
+                                                                     KvCacheView view, int layer,
+                                                                     int qkv_blocks, float scale) {
+  __shared__ ExchangeStepShared<NCH, HD, kPaged> sh;
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < qkv_blocks) {
+    qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, true>(a, w, view, layer, b, sh.qkv);
+    return;
+  }
+  int unit, g = 0;
+  if (G > 1) {
+    attention_block_coords(b - qkv_blocks, a.num_kv_heads, G, &unit, &g);
+  } else {
+    unit = b - qkv_blocks;
+  }
+  const int kv_head = unit;
+  const int head = kv_head * G + g;
+  AttnExchange<HD> x;
+  x.words = a.exchange + a.exchange_read_offset + static_cast<size_t>(3 * head) * HD;
+  x.spins = a.exchange_spins;
+  x.status = a.exchange_status;
+  x.q_lds = sh.at.q;
+  x.kv_lds = sh.at.kv;
+  const int seq_len = *a.position + 1;
+  decode_attention_block<kPaged, HD, 1, true>(sh.at.attn, a.attn, a.partials, nullptr, view, kv_head, head,
+                                              0, 1, seq_len, scale, &x);
 }
 
 // Split merge (splits > 1 only), one kMergeThreads-thread block per query head.
@@ -441,9 +544,17 @@ __global__ __launch_bounds__(kThreads) void argmax_step_kernel(DecodeStepArgs a,
 template <int NCH, int NCH_F, int HD, bool kPaged, int G>
 void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, const KvCacheView& view,
                          int layer, hipStream_t s, unsigned mask) {
+  const int qkv_rows = (a.num_heads + 2 * a.num_kv_heads) * HD;
+  if (a.exchange != nullptr && a.splits == 1 && (mask & kDecodeQkv) && (mask & kDecodeAttention)) {
+    const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
+    const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
+    qkv_attention_kernel<NCH, HD, kPaged, G>
+        <<<qkv_blocks + a.num_heads, kAttnThreads, 0, s>>>(a, w, view, layer, qkv_blocks, scale);
+    HIP_CHECK_LAUNCH();
+    mask &= ~(kDecodeQkv | kDecodeAttention);
+  }
   if (mask & kDecodeQkv) {
-    const int qkv_rows = (a.num_heads + 2 * a.num_kv_heads) * HD;
-    qkv_rope_kernel<NCH, HD, kPaged><<<qkv_rows / (4 * kQkvRowsPerWave), kThreads, 0, s>>>(a, w, view, layer);
+    qkv_rope_kernel<NCH, HD, kPaged><<<qkv_rows / (kWaves * kQkvRowsPerWave), kThreads, 0, s>>>(a, w, view, layer);
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeAttention) {
@@ -484,6 +595,33 @@ bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads,
   if (num_heads * head_dim != hidden) return false;  // o_proj input width == hidden
   const int g = num_heads / num_kv_heads;
   return g == 1 || g == 2 || g == 4 || g == 8;
+}
+
+bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, bool paged, int compute_units) {
+  if (head_dim != 64 || num_kv_heads <= 0) return false;
+  const int g = num_heads / num_kv_heads;
+  const int qkv_rows = (num_heads + 2 * num_kv_heads) * head_dim;
+  if (qkv_rows % (kAttnWaves * kQkvRowsPerWave) != 0) return false;
+  const int blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave) + num_heads;
+  if ((blocks - num_heads) % 8 != 0) return false;  // the attention blocks' XCD numbering
+  int per_cu = 0;
+  const void* fn = nullptr;
+#define LCR_EXCHANGE_FN(G_)                                                                           \
+  case G_:                                                                                            \
+    fn = paged ? reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, true, G_>)                \
+               : reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, false, G_>);             \
+    break;
+  switch (g) {
+    LCR_EXCHANGE_FN(1)
+    LCR_EXCHANGE_FN(2)
+    LCR_EXCHANGE_FN(4)
+    LCR_EXCHANGE_FN(8)
+    default:
+      return false;
+  }
+#undef LCR_EXCHANGE_FN
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kAttnThreads, 0) != hipSuccess) return false;
+  return static_cast<long>(per_cu) * compute_units >= blocks;
 }
 
 // One block per compute unit, each taking the same number of row groups

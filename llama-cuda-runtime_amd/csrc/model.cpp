@@ -53,6 +53,9 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
            decode_step_supported(config_.hidden_size, config_.intermediate_size,
                                  config_.num_heads, config_.num_kv_heads, config_.head_dim) &&
            config_.vocab_size > 0;
+  exchange_enabled_ = fused_ && options_.decode_exchange &&
+                      decode_exchange_fits(config_.num_heads, config_.num_kv_heads, config_.head_dim,
+                                           options_.kv_layout == KvLayout::kPaged, multiprocessors_);
 
   // The table serves the fused decode step and the prefill q/k/v projection
   // with RoPE in its epilogue.
@@ -203,6 +206,8 @@ void Model::allocate_arena() {
       gemm_workspace_bytes(),                                         // gemm_workspace_
       static_cast<size_t>(options_.max_seq) * sizeof(float),          // uniforms_
       sizeof(int32_t),                                                // draw_counter_
+      decode_exchange_words(config_.num_heads, config_.head_dim) * sizeof(unsigned long long),  // exchange_words_
+      sizeof(int),                                                    // exchange_status_
   };
   size_t total = 0;
   for (size_t s : sizes) total = align_up(total, 256) + s;
@@ -227,6 +232,9 @@ void Model::allocate_arena() {
   gemm_workspace_ = gemm_workspace_size_ > 0 ? arena_.alloc<float>(gemm_workspace_size_ / sizeof(float)) : nullptr;
   uniforms_ = arena_.alloc<float>(static_cast<size_t>(options_.max_seq));
   draw_counter_ = arena_.alloc<int32_t>(1);
+  exchange_words_ = arena_.alloc<unsigned long long>(decode_exchange_words(config_.num_heads, config_.head_dim));
+  exchange_status_ = arena_.alloc<int>(1);
+  clear_exchange();
   HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
   HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
 }
@@ -351,7 +359,28 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.paged = options_.kv_layout == KvLayout::kPaged;
   a.splits = splits;
   a.compute_units = multiprocessors_;
+  a.exchange = exchange_enabled_ ? exchange_words_ : nullptr;
+  a.exchange_status = exchange_status_;
+  a.exchange_spins = std::max(1, options_.exchange_spins);
+  a.exchange_read_offset = options_.exchange_test_unwritten
+                               ? static_cast<int>(decode_exchange_words(config_.num_heads, config_.head_dim) / 2)
+                               : 0;
   return a;
+}
+
+int Model::exchange_status() const {
+  int status = 0;
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipMemcpy(&status, exchange_status_, sizeof(int), hipMemcpyDeviceToHost));
+  return status;
+}
+
+void Model::clear_exchange() {
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipMemset(exchange_words_, 0,
+                      decode_exchange_words(config_.num_heads, config_.head_dim) * sizeof(unsigned long long)));
+  HIP_CHECK(hipMemset(exchange_status_, 0, sizeof(int)));
+  HIP_CHECK(hipDeviceSynchronize());
 }
 
 void Model::launch_fused_step(int seq_len) {
@@ -515,6 +544,10 @@ std::vector<int> Model::generate_sampled(int first_token, int steps, float tempe
   position_ = start + steps;
   std::vector<int32_t> ids(static_cast<size_t>(steps));
   HIP_CHECK(hipMemcpy(ids.data(), history_ + start + 1, ids.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+  if (exchange_enabled_ && exchange_status() != 0) {
+    clear_exchange();
+    LCR_FAIL("a decode step's in-grid exchange wait gave up; its results are not valid");
+  }
   for (int s = 0; s < steps; ++s) {
     LCR_CHECK(ids[static_cast<size_t>(s)] >= 0 && ids[static_cast<size_t>(s)] < config_.vocab_size,
               "sampling produced token id " << ids[static_cast<size_t>(s)] << ", outside the vocabulary");
@@ -560,6 +593,10 @@ std::vector<int> Model::generate_greedy(int first_token, int steps, double* elap
   std::vector<int32_t> ids(static_cast<size_t>(steps));
   HIP_CHECK(hipMemcpy(ids.data(), history_ + start + 1, static_cast<size_t>(steps) * sizeof(int32_t),
                       hipMemcpyDeviceToHost));
+  if (exchange_enabled_ && exchange_status() != 0) {
+    clear_exchange();
+    LCR_FAIL("a decode step's in-grid exchange wait gave up; its results are not valid");
+  }
   for (int s = 0; s < steps; ++s) out[static_cast<size_t>(s)] = ids[static_cast<size_t>(s)];
   return out;
 }
@@ -579,6 +616,10 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
   if (kernel == "qkv") {
     mask = kDecodeQkv;
     bytes = (qd + 2 * kvd) * H * e + H * e + H * 4 + (qd + 2 * kvd) * e;
+  } else if (kernel == "qkv_attention") {
+    // The exchange grid when the step uses it, else the two kernels.
+    mask = kDecodeQkv | kDecodeAttention;
+    bytes = (qd + 2 * kvd) * H * e + H * e + H * 4 + (qd + 2 * kvd) * e + 2.0 * kvd * seq_len * e + qd * e;
   } else if (kernel == "attention") {
     mask = kDecodeAttention;
     bytes = 2.0 * kvd * seq_len * e + qd * e + qd * e;

@@ -64,6 +64,12 @@ class Model {
     bool fused_decode = true;        // fused kernels when the geometry has them
     bool use_graph = true;           // replay the fused step from a hipGraph
     bool prefill_via_decode = false; // run prompts token by token through decode
+    // The decode step's q/k/v projection and single-split attention in one
+    // grid, handing the query and the new key and value over in-grid
+    // exchange words (kernels/exchange.h), when the device holds the grid.
+    bool decode_exchange = true;
+    int exchange_spins = 1 << 20;         // polls before an exchange wait gives up
+    bool exchange_test_unwritten = false; // tests: waits read words no block writes
   };
 
   // Prompt chunks shorter than this run token by token through the decode
@@ -137,6 +143,13 @@ class Model {
   // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", or
   // "argmax" (the reduction of the head's per-block keys to the id alone).
   double time_decode_kernel(const std::string& kernel, int launches, double* bytes_per_launch);
+  // Whether the decode step runs q/k/v and attention as one exchange grid.
+  bool decode_exchange() const { return exchange_enabled_; }
+  // Non-zero when an exchange wait of a past step gave up (its results are
+  // then not to be trusted); reading it synchronizes the stream.
+  int exchange_status() const;
+  // Clears the exchange words and the status (after a wait gave up).
+  void clear_exchange();
 
  private:
   void load_weights(const SafetensorsArchive& archive);
@@ -190,6 +203,9 @@ class Model {
   int32_t* position_dev_ = nullptr;
   unsigned long long* argmax_partials_ = nullptr;
   int32_t* history_ = nullptr;    // [max_seq + 1]
+  unsigned long long* exchange_words_ = nullptr;  // decode_exchange_words(...)
+  int* exchange_status_ = nullptr;
+  bool exchange_enabled_ = false;
   int32_t* pinned_state_ = nullptr;  // host {token, position}
 
   std::map<int, hipGraphExec_t> graphs_;  // by split count

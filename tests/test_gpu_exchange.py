@@ -1,0 +1,125 @@
+"""The decode step's q/k/v projection and single-split attention as one grid
+(kernels/exchange.h, qkv_attention_kernel): the attention blocks take their
+query and the new position's key and value from in-grid exchange words.
+
+  - the grid is used on the Llama-3.2-1B geometry, both cache layouts;
+  - its logits equal the oracle's and the two-kernel step's bit for bit, from
+    the first position on (a one-token prompt: the new key is the only one)
+    and across the 64-position tile boundaries, graph-replayed and eager;
+  - groups of 4 and 8 query heads per kv head (groups of 1 and 2 have more
+    q/k/v rows than one grid of one block per compute unit holds, and keep
+    the two-kernel step);
+  - a wait that finds no writer gives up after its poll limit, raises the
+    status (generate_greedy then fails with a message), and leaves no wave
+    spinning: the failure is forced from the host by pointing the waits at
+    words no block writes, so every kernel still exits normally.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import expect_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(num_hidden_layers=2, vocab_size=4096)
+
+
+@pytest.fixture(scope="module")
+def small_ckpt(lcr, tmp_path_factory):
+    d = tmp_path_factory.mktemp("exchange_model")
+    return lcr.write_synthetic_checkpoint(d, lcr.llama_config(**SMALL))
+
+
+def greedy_logits(m, prompt, steps):
+    """Logits of the prompt's last token and of `steps` greedy decode steps."""
+    out = [m.logits(m.prefill(prompt))]
+    for _ in range(steps):
+        out.append(m.logits(m.decode(int(np.argmax(out[-1])))))
+    return out
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_exchange_grid_is_used(lcr, small_ckpt, paged):
+    m = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1)
+    enabled, status = m.exchange_status()
+    assert enabled and status == 0
+    off = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1, decode_exchange=0)
+    assert off.exchange_status() == (False, 0)
+
+
+@pytest.mark.parametrize("graph", [1, 0])
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("prompt_len", [1, 63, 64, 130])
+def test_exchange_equals_oracle_and_two_kernel_step(lcr, small_ckpt, paged, graph, prompt_len):
+    """Prompts of 1, 63, 64 and 130 tokens put the new position first in the
+    cache, last in a full tile, first in a new tile and in a later wave's tile."""
+    kw = dict(max_seq=256, paged=int(paged), use_graph=graph, prefill_via_decode=1)
+    m = lcr.Model(small_ckpt, **kw)
+    ref = lcr.Model(small_ckpt, decode_exchange=0, **kw)
+    o = oracle.OracleModel(small_ckpt, max_seq=256, paged=paged, multiprocessors=m.stats().multiprocessors)
+    prompt = lcr.synthetic_tokens(prompt_len, m.vocab, seed=prompt_len)
+    got = greedy_logits(m, prompt, 3)
+    two = greedy_logits(ref, prompt, 3)
+    lo = [o.prefill(prompt, use_decode_path=True)]
+    for _ in range(3):
+        lo.append(o.decode(oracle.argmax(lo[-1])))
+    for s, (g, t, e) in enumerate(zip(got, two, lo)):
+        expect_bits_equal(g.view(np.uint32), t.view(np.uint32), f"step {s}: exchange vs two kernels")
+        expect_bits_equal(g.view(np.uint32), e.view(np.uint32), f"step {s}: exchange vs oracle")
+    assert m.exchange_status() == (True, 0)
+
+
+@pytest.mark.parametrize("kv_heads", [32, 16, 8, 4])
+@pytest.mark.parametrize("paged", [False, True])
+def test_exchange_group_sizes(lcr, tmp_path_factory, kv_heads, paged):
+    d = tmp_path_factory.mktemp(f"exchange_group_{kv_heads}")
+    ckpt = lcr.write_synthetic_checkpoint(d, lcr.llama_config(num_key_value_heads=kv_heads, **SMALL))
+    m = lcr.Model(ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1)
+    # The grid runs one 512-thread block per compute unit: 16 q/k/v rows per
+    # block plus one block per query head must fit (groups of 4 and 8 do on
+    # 256 compute units; groups of 1 and 2 keep the two-kernel step).
+    blocks = (32 + 2 * kv_heads) * 64 // 16 + 32
+    assert m.exchange_status() == (blocks <= m.stats().multiprocessors, 0)
+    o = oracle.OracleModel(ckpt, max_seq=256, paged=paged, multiprocessors=m.stats().multiprocessors)
+    prompt = lcr.synthetic_tokens(70, m.vocab, seed=kv_heads)
+    got = greedy_logits(m, prompt, 3)
+    lo = [o.prefill(prompt, use_decode_path=True)]
+    for _ in range(3):
+        lo.append(o.decode(oracle.argmax(lo[-1])))
+    for s, (g, e) in enumerate(zip(got, lo)):
+        expect_bits_equal(g.view(np.uint32), e.view(np.uint32), f"group {32 // kv_heads} step {s}")
+
+
+def test_exchange_generate_greedy_matches_oracle(lcr, small_ckpt):
+    m = lcr.Model(small_ckpt, max_seq=256, prefill_via_decode=1)
+    o = oracle.OracleModel(small_ckpt, max_seq=256, multiprocessors=m.stats().multiprocessors)
+    prompt = lcr.synthetic_tokens(20, m.vocab, seed=5)
+    first = oracle.argmax(m.logits(m.prefill(prompt)))
+    ids, _ = m.generate_greedy(first, 40)
+    tok = oracle.argmax(o.prefill(prompt, use_decode_path=True))
+    assert tok == first
+    expected = []
+    for _ in range(40):
+        tok = oracle.argmax(o.decode(tok))
+        expected.append(tok)
+    assert list(ids) == expected
+    assert m.exchange_status() == (True, 0)
+
+
+def test_exchange_wait_gives_up(lcr, small_ckpt):
+    """Waits pointed at words no block writes: each gives up after four polls
+    and raises the status; the steps still finish (their logits are not
+    valid), generate_greedy reports the failure, and clearing resets the
+    status."""
+    m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=1, exchange_spins=4, exchange_test_unwritten=1)
+    prompt = lcr.synthetic_tokens(5, m.vocab, seed=3)
+    m.prefill(prompt)
+    enabled, status = m.exchange_status()
+    assert enabled and status == 1
+    m.exchange_clear()
+    assert m.exchange_status() == (True, 0)
+    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+        m.generate_greedy(1, 4)
+    assert m.exchange_status() == (True, 0)  # the failure cleared it

@@ -540,7 +540,8 @@ def main() -> int:
 
     # Per-kernel timing (dominant kernel first), live, on the model's stream.
     kernels = {}
-    for name in ("gate_up", "down", "lm_head", "qkv_attention", "qkv", "o_proj", "attention", "argmax"):
+    for name in ("gate_up", "down", "lm_head", "qkv_attention_oproj", "qkv_attention", "qkv", "o_proj", "attention",
+                 "argmax"):
         ms, nbytes = model.time_decode_kernel(name, args.kernel_launches)
         kernels[name] = {"avg_us": ms * 1000.0, "bytes_per_launch": nbytes,
                          "gbs": nbytes / (ms / 1000.0) / 1e9}

@@ -38,6 +38,7 @@ typedef struct lcr_model_options {
   int decode_exchange;  /* extension: q/k/v projection and single-split attention of the
                            decode step in one grid, exchanging the query and the new key
                            and value in-grid (default 1; used when the device holds the grid) */
+  int exchange_oproj;   /* extension: the o_proj projection joins that grid too (default 1) */
   int exchange_spins;   /* extension: polls before an exchange wait gives up (default 1 << 20) */
   int exchange_test_unwritten; /* tests only: exchange waits read words no block writes (default 0) */
 } lcr_model_options;
@@ -85,9 +86,9 @@ int lcr_model_tap(const lcr_model* model, int index, char* name, size_t name_cap
 /* Per-stage profile of eager (unfused) passes (src/profiler.h). */
 int lcr_model_set_profiling(lcr_model* model, int enabled);
 
-/* extension: whether decode steps run the exchange grid (*enabled), and whether an
- * exchange wait of a past step gave up (*status non-zero: those results are not valid).
- * Synchronizes the model's stream. */
+/* extension: which exchange grid decode steps run (*enabled: 0 none, 1 q/k/v and attention,
+ * 2 q/k/v, attention and o_proj), and whether an exchange wait of a past step gave up
+ * (*status non-zero: those results are not valid). Synchronizes the model's stream. */
 int lcr_model_exchange_status(const lcr_model* model, int* enabled, int* status);
 /* extension: clears the exchange words and status (after a wait gave up). */
 int lcr_model_exchange_clear(lcr_model* model);

@@ -97,6 +97,7 @@ class ModelOptions(ctypes.Structure):
         ("use_graph", ctypes.c_int),
         ("prefill_via_decode", ctypes.c_int),
         ("decode_exchange", ctypes.c_int),
+        ("exchange_oproj", ctypes.c_int),
         ("exchange_spins", ctypes.c_int),
         ("exchange_test_unwritten", ctypes.c_int),
     ]
@@ -544,12 +545,13 @@ class Model:
         return out, ms.value
 
     def exchange_status(self):
-        """(enabled, status): whether decode steps run q/k/v and attention as one
-        exchange grid, and whether an exchange wait of a past step gave up."""
+        """(grid, status): which exchange grid decode steps run (0 none, 1 q/k/v
+        and attention, 2 with o_proj too), and whether an exchange wait of a
+        past step gave up."""
         enabled, status = ctypes.c_int(), ctypes.c_int()
         check(self.lib, self.lib.lcr_model_exchange_status(self.handle, ctypes.byref(enabled),
                                                            ctypes.byref(status)), "exchange_status")
-        return bool(enabled.value), int(status.value)
+        return int(enabled.value), int(status.value)
 
     def exchange_clear(self):
         check(self.lib, self.lib.lcr_model_exchange_clear(self.handle), "exchange_clear")

@@ -39,6 +39,7 @@ extern "C" void lcr_model_default_options(lcr_model_options* o) {
   o->use_graph = 1;
   o->prefill_via_decode = 0;
   o->decode_exchange = 1;
+  o->exchange_oproj = 1;
   o->exchange_spins = 1 << 20;
   o->exchange_test_unwritten = 0;
 }
@@ -62,6 +63,7 @@ extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* 
     opt.use_graph = o.use_graph != 0;
     opt.prefill_via_decode = o.prefill_via_decode != 0;
     opt.decode_exchange = o.decode_exchange != 0;
+    opt.exchange_oproj = o.exchange_oproj != 0;
     opt.exchange_spins = o.exchange_spins > 0 ? o.exchange_spins : (1 << 20);
     opt.exchange_test_unwritten = o.exchange_test_unwritten != 0;
     auto handle = std::make_unique<lcr_model>();
@@ -77,7 +79,7 @@ extern "C" int lcr_model_exchange_status(const lcr_model* m, int* enabled, int* 
   CAPI_MODEL(m);
   CAPI_CHECK(enabled != nullptr && status != nullptr, "output pointers needed");
   return capi::guarded([&]() -> int {
-    *enabled = m->impl->decode_exchange() ? 1 : 0;
+    *enabled = m->impl->decode_exchange() ? (m->impl->exchange_oproj() ? 2 : 1) : 0;
     *status = m->impl->exchange_status();
     return LCR_OK;
   });

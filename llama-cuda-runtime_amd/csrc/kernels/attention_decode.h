@@ -100,6 +100,11 @@ struct AttnExchange {
   int* status;
   float* q_lds;                  // [kHeadDim] LDS
   elem_t* kv_lds;                // [2][kHeadDim] LDS, 16-byte aligned
+  // When set, the head's output also goes out as broadcast words, two
+  // elements each (element 2i in the low half), tagged `tag`, at
+  // out_words[(head * kHeadDim) / 2 + i]: for the o_proj blocks of the grid.
+  unsigned long long* out_words;
+  uint32_t tag;
 };
 
 // Step 3's reduce-scatter: at offset O the lane keeps the half of its N values
@@ -576,7 +581,18 @@ __device__ __forceinline__ void decode_attention_block(
     }
     const int head = head0 + g;
     if (splits == 1) {
-      out[static_cast<size_t>(head) * kHeadDim + d] = float_to_elem(merged * (1.0f / tl));
+      const elem_t e = float_to_elem(merged * (1.0f / tl));
+      out[static_cast<size_t>(head) * kHeadDim + d] = e;
+      if constexpr (kExchange) {
+        // kHeadDim is a multiple of 64, so a lane and its odd neighbour hold
+        // outputs d and d + 1 of the same wave.
+        const uint32_t bits = e.bits;
+        const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1));
+        if (x->out_words != nullptr && (d & 1) == 0) {
+          exchange_put_tagged(x->out_words + (static_cast<size_t>(head) * kHeadDim + d) / 2, x->tag,
+                              bits | (next << 16));
+        }
+      }
     } else {
       float* slot = partials + (static_cast<size_t>(head) * splits + split) * (kPartialHeader + kHeadDim);
       if (d == 0) {

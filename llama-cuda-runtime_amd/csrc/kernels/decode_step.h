@@ -65,23 +65,31 @@ struct DecodeStepArgs {
   int splits;
   int compute_units;         // of the device: sizes the output head's grid
   // In-grid exchange (exchange.h): when set and splits == 1, the q/k/v
-  // projection and the attention run as one grid. Words: [num_heads][3][head_dim].
+  // projection and the attention run as one grid (with exchange_oproj, the
+  // o_proj projection too). Words (X = num_heads * head_dim): [0, 3X) the
+  // query, key and value hand-over, [num_heads][3][head_dim]; [3X, 3.5X) the
+  // attention output, two elements per word; [3.5X, 7X) never written.
   unsigned long long* exchange;
+  bool exchange_oproj;
   int* exchange_status;      // [1] raised by a wait that gave up
   int exchange_spins;        // polls before a wait gives up
-  int exchange_read_offset;  // added to the words the attention blocks read (0; tests)
+  int exchange_read_offset;  // added to every word the grid reads (0; 3.5X in tests of the give-up path)
+  uint32_t* epoch;           // [1] steps completed; advanced by the step's last kernel
 };
 
 // True when the fused kernels are compiled for this geometry.
 bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads, int head_dim);
 // True when the q/k/v + attention exchange grid is compiled for this geometry
 // and all its blocks fit on the device at once.
-bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, bool paged, int compute_units);
-// Exchange words the step needs (3 * num_heads * head_dim) plus the same
-// again, never written, for the tests of the give-up path.
+bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, int hidden, bool paged,
+                          int compute_units, bool with_oproj);
+// Exchange words of the step (see DecodeStepArgs::exchange).
 inline size_t decode_exchange_words(int num_heads, int head_dim) {
-  return 6 * static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim);
+  return 7 * static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim);
 }
+// Launches of one graph that exchange words through the same buffer
+// (enqueue_decode_layer's tag_slot is below this).
+constexpr int kExchangeTagSlots = 1024;
 
 // The five kernels of a layer, as bits of a selection mask.
 enum DecodeKernel : unsigned {
@@ -96,9 +104,12 @@ enum DecodeKernel : unsigned {
 // Enqueues one layer's kernels (qkv+rope+kv, attention, o_proj+residual,
 // gate_up+swiglu, down+residual); `mask` selects a subset (for timing one
 // kernel in isolation).
+// `tag_slot` (default: the layer) tells launches of one graph apart for the
+// exchange grid's broadcast words; graphs that launch one layer more than
+// once give each launch its own slot, below kExchangeTagSlots.
 void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
                           const KvCacheView& view, int layer, hipStream_t stream,
-                          unsigned mask = kDecodeAll);
+                          unsigned mask = kDecodeAll, int tag_slot = -1);
 // Enqueues the output head and the argmax (which also advances the position;
 // leave it out only to time the head alone).
 void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t stream, bool with_argmax = true);

@@ -100,4 +100,53 @@ __device__ __forceinline__ void exchange_take(unsigned long long* words, float (
   }
 }
 
+// Broadcast words: one writer, any number of readers, never cleared. A word
+// is (tag << 32 | 32-bit payload); a reader waits for the tag of the current
+// launch, which the writer and every reader derive alike (a step counter that
+// only grows, and the launch's place in its graph), so a word left by an
+// earlier launch never passes for a current one.
+__device__ __forceinline__ void exchange_put_tagged(unsigned long long* word, uint32_t tag, uint32_t payload) {
+  __hip_atomic_store(word, (static_cast<unsigned long long>(tag) << 32) | payload, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One wave waits for N words per lane (word lane + 64 k of `words`) to carry
+// `tag`, two polls in flight as in exchange_take, at most `spins` polls;
+// returns the payloads.
+template <int N>
+__device__ __forceinline__ void exchange_wait_tagged(unsigned long long* words, uint32_t tag, uint32_t (&out)[N],
+                                                     int spins, int* status) {
+  const int lane = static_cast<int>(threadIdx.x & 63u);
+  unsigned long long a[N], b[N];
+  auto poll = [&](unsigned long long (&w)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) w[k] = exchange_peek(words + lane + 64 * k);
+  };
+  auto all_current = [&](const unsigned long long (&w)[N]) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) ok = ok && static_cast<uint32_t>(w[k] >> 32) == tag;
+    return __all(ok) != 0;
+  };
+  poll(a);
+  int polls = 0;
+  while (true) {
+    poll(b);
+    if (all_current(a)) break;
+    poll(a);
+    if (all_current(b)) {
+#pragma unroll
+      for (int k = 0; k < N; ++k) a[k] = b[k];
+      break;
+    }
+    polls += 2;
+    if (polls >= spins) {
+      if (lane == 0) exchange_give_up(status);
+      break;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) out[k] = static_cast<uint32_t>(a[k]);
+}
+
 }  // namespace lcr

@@ -21,6 +21,7 @@ constexpr int kLmHeadRows = 2;  // rows per wave per group
 constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
 constexpr int kDownWaves = 1;   // waves (rows) per down block
 constexpr int kQkvRowsPerWave = 2;   // rows per qkv wave
+constexpr int kOProjRowsPerWave = 2; // rows per wave of the exchange grid's o_proj blocks
 constexpr int kGateUpActsPerWave = 1;  // activations (gate + up row pairs) per gate_up wave
 // Query heads per block in the long-context attention launch (with fewer
 // than G, the heads of one kv head are spread over G / kLongContextHeads
@@ -144,10 +145,15 @@ struct QkvShared {
 // blocks of the same grid, 3 * HD words per query head h: its query at
 // x[3 h HD + i], and the key and value of its kv head at x[3 h HD + HD + i]
 // and x[3 h HD + 2 HD + i] (a kv head's once for each of its G query heads).
+//
+// At layer 0 block 0 also seeds the residual sum with the embedding row,
+// unless `seed` is false (the exchange grid with o_proj blocks, which read
+// the embedding row themselves: a seed written from one XCD's L2 and joins
+// written from others could be written back in either order).
 template <int NCH, int HD, bool kPaged, int WAVES, int RW, int G, bool kPublish>
 __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDevicePtrs& w,
                                           const KvCacheView& view, int layer, int block,
-                                          QkvShared<NCH, WAVES / 2 * RW>& sh) {
+                                          QkvShared<NCH, WAVES / 2 * RW>& sh, bool seed = true) {
   constexpr int H = NCH * 512;
   constexpr int HALF = HD / 2;
   constexpr int PAIRS = WAVES / 2 * RW;  // rotation pairs per block
@@ -184,7 +190,7 @@ __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDe
     tile.load(rows, lane);
   }
 
-  norm_finish<NCH>(sh.xs, nin, a.eps, sh.scratch, (layer == 0 && block == 0) ? a.resid : nullptr);
+  norm_finish<NCH>(sh.xs, nin, a.eps, sh.scratch, (seed && layer == 0 && block == 0) ? a.resid : nullptr);
 
   vec16 xv[NCH];
   load_x_lds<NCH>(xv, sh.xs, lane);
@@ -327,18 +333,89 @@ struct ExchangeStepShared {
       float q[HD];
       __attribute__((aligned(16))) elem_t kv[2 * HD];
     } at;
+    __attribute__((aligned(16))) elem_t ox[NCH * 512];  // o_proj blocks: the attention output
   };
 };
 
-template <int NCH, int HD, bool kPaged, int G>
+// Block `ob` of the o_proj projection inside the exchange grid: kAttnWaves
+// waves of kOProjRowsPerWave rows. Its weight rows and residual entries are
+// requested first; then each wave waits for its share of the attention
+// output's broadcast words (two elements per word), the block assembles the
+// whole vector in LDS, and finishes as proj_residual_kernel does (same
+// products in the same order, same residual join).
+//
+// At layer 0 (`first`) the residual sum before the join is the embedding row,
+// read from the embedding (the q/k/v blocks of this grid do not seed it).
+template <int NCH>
+__device__ __forceinline__ void oproj_block(const DecodeStepArgs& a, const elem_t* __restrict__ W,
+                                            unsigned long long* words, uint32_t tag, int ob, elem_t* xs,
+                                            bool first) {
+  constexpr int K = NCH * 512;
+  constexpr int RW = kOProjRowsPerWave;
+  constexpr int PER = K / 2 / kAttnThreads;  // words per lane
+  static_assert(PER * 2 * kAttnThreads == K, "the block's lanes take the words evenly");
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int row0 = (ob * kAttnWaves + wave) * RW;
+  GemvTile<RW, NCH> tile;
+  {
+    const elem_t* rows[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) rows[r] = W + static_cast<size_t>(row0 + r) * K;
+    tile.load(rows, lane);
+  }
+  float vold[RW];
+  const elem_t* erow = a.embedding + static_cast<size_t>(*a.token) * a.hidden;
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    vold[r] = first ? elem_to_float(erow[row0 + r]) : a.resid[row0 + r];
+    hold_value(vold[r]);
+  }
+  uint32_t payload[PER];
+  exchange_wait_tagged<PER>(words + wave * 64 * PER, tag, payload, a.exchange_spins, a.exchange_status);
+  uint32_t* xs32 = reinterpret_cast<uint32_t*>(xs);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) xs32[wave * 64 * PER + lane + 64 * k] = payload[k];
+  __syncthreads();
+  vec16 xv[NCH];
+  load_x_lds<NCH>(xv, xs, lane);
+  float out[RW];
+  tile.dot(out, xv);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const float proj = elem_to_float(float_to_elem(out[r]));
+      const float xold = elem_to_float(float_to_elem(vold[r]));
+      a.resid[row0 + r] = xold + proj;
+    }
+  }
+}
+
+//
+// kOProj: the o_proj projection with its residual join joins the grid as its
+// last hidden / (kAttnWaves * kOProjRowsPerWave) blocks (oproj_block), fed
+// by the attention blocks' broadcast words. Their tag is
+// epoch * kExchangeTagSlots + tag_slot + 1: `tag_slot` is the launch's place
+// in its graph (the layer in a decode step), `epoch` the count of completed
+// steps, which only grows.
+template <int NCH, int HD, bool kPaged, int G, bool kOProj>
 __global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepArgs a, LayerDevicePtrs w,
                                                                      KvCacheView view, int layer,
-                                                                     int qkv_blocks, float scale) {
+                                                                     int qkv_blocks, float scale, int tag_slot) {
   __shared__ ExchangeStepShared<NCH, HD, kPaged> sh;
   const int b = static_cast<int>(blockIdx.x);
   if (b < qkv_blocks) {
-    qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, true>(a, w, view, layer, b, sh.qkv);
+    qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, true>(a, w, view, layer, b, sh.qkv, !kOProj);
     return;
+  }
+  const size_t broadcast = 3 * static_cast<size_t>(a.num_heads) * HD;  // first broadcast word
+  const uint32_t tag = (*a.epoch) * static_cast<uint32_t>(kExchangeTagSlots) + static_cast<uint32_t>(tag_slot) + 1u;
+  if constexpr (kOProj) {
+    if (b >= qkv_blocks + a.num_heads) {
+      oproj_block<NCH>(a, w.o, a.exchange + a.exchange_read_offset + broadcast, tag, b - qkv_blocks - a.num_heads,
+                       sh.ox, layer == 0);
+      return;
+    }
   }
   int unit, g = 0;
   if (G > 1) {
@@ -354,6 +431,8 @@ __global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepA
   x.status = a.exchange_status;
   x.q_lds = sh.at.q;
   x.kv_lds = sh.at.kv;
+  x.out_words = kOProj ? a.exchange + broadcast : nullptr;
+  x.tag = tag;
   const int seq_len = *a.position + 1;
   decode_attention_block<kPaged, HD, 1, true>(sh.at.attn, a.attn, a.partials, nullptr, view, kv_head, head,
                                               0, 1, seq_len, scale, &x);
@@ -538,18 +617,26 @@ __global__ __launch_bounds__(kThreads) void argmax_step_kernel(DecodeStepArgs a,
     *a.next_token = id;
     if (pos + 1 < a.history_len) a.history[pos + 1] = id;
     *a.position = pos + 1;
+    if (a.epoch != nullptr) *a.epoch = *a.epoch + 1u;
   }
 }
 
 template <int NCH, int NCH_F, int HD, bool kPaged, int G>
 void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, const KvCacheView& view,
-                         int layer, hipStream_t s, unsigned mask) {
+                         int layer, hipStream_t s, unsigned mask, int tag_slot) {
   const int qkv_rows = (a.num_heads + 2 * a.num_kv_heads) * HD;
   if (a.exchange != nullptr && a.splits == 1 && (mask & kDecodeQkv) && (mask & kDecodeAttention)) {
     const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
     const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
-    qkv_attention_kernel<NCH, HD, kPaged, G>
-        <<<qkv_blocks + a.num_heads, kAttnThreads, 0, s>>>(a, w, view, layer, qkv_blocks, scale);
+    if (a.exchange_oproj && (mask & kDecodeOProj)) {
+      const int oproj_blocks = a.hidden / (kAttnWaves * kOProjRowsPerWave);
+      qkv_attention_kernel<NCH, HD, kPaged, G, true><<<qkv_blocks + a.num_heads + oproj_blocks, kAttnThreads, 0, s>>>(
+          a, w, view, layer, qkv_blocks, scale, tag_slot);
+      mask &= ~kDecodeOProj;
+    } else {
+      qkv_attention_kernel<NCH, HD, kPaged, G, false>
+          <<<qkv_blocks + a.num_heads, kAttnThreads, 0, s>>>(a, w, view, layer, qkv_blocks, scale, tag_slot);
+    }
     HIP_CHECK_LAUNCH();
     mask &= ~(kDecodeQkv | kDecodeAttention);
   }
@@ -597,19 +684,30 @@ bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads,
   return g == 1 || g == 2 || g == 4 || g == 8;
 }
 
-bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, bool paged, int compute_units) {
+// The q/k/v + attention grid must fit on the device at once. With o_proj
+// blocks (with_oproj) it need not: the blocks that wait (attention and
+// o_proj) must leave room for at least one more block, so a block that never
+// waits (q/k/v) can always run and every wait is eventually served.
+bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, int hidden, bool paged,
+                          int compute_units, bool with_oproj) {
   if (head_dim != 64 || num_kv_heads <= 0) return false;
   const int g = num_heads / num_kv_heads;
   const int qkv_rows = (num_heads + 2 * num_kv_heads) * head_dim;
   if (qkv_rows % (kAttnWaves * kQkvRowsPerWave) != 0) return false;
-  const int blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave) + num_heads;
-  if ((blocks - num_heads) % 8 != 0) return false;  // the attention blocks' XCD numbering
+  const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
+  if (qkv_blocks % 8 != 0) return false;  // the attention blocks' XCD numbering
+  if (with_oproj && (hidden % (kAttnWaves * kOProjRowsPerWave) != 0 || num_heads * head_dim != 2048)) return false;
   int per_cu = 0;
   const void* fn = nullptr;
-#define LCR_EXCHANGE_FN(G_)                                                                           \
-  case G_:                                                                                            \
-    fn = paged ? reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, true, G_>)                \
-               : reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, false, G_>);             \
+#define LCR_EXCHANGE_FN(G_)                                                                                    \
+  case G_:                                                                                                     \
+    if (with_oproj) {                                                                                          \
+      fn = paged ? reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, true, G_, true>)                 \
+                 : reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, false, G_, true>);              \
+    } else {                                                                                                   \
+      fn = paged ? reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, true, G_, false>)                \
+                 : reinterpret_cast<const void*>(&qkv_attention_kernel<4, 64, false, G_, false>);             \
+    }                                                                                                          \
     break;
   switch (g) {
     LCR_EXCHANGE_FN(1)
@@ -621,7 +719,10 @@ bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, bool pa
   }
 #undef LCR_EXCHANGE_FN
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kAttnThreads, 0) != hipSuccess) return false;
-  return static_cast<long>(per_cu) * compute_units >= blocks;
+  const long slots = static_cast<long>(per_cu) * compute_units;
+  if (!with_oproj) return slots >= qkv_blocks + num_heads;
+  const int waiting = num_heads + hidden / (kAttnWaves * kOProjRowsPerWave);
+  return slots >= qkv_blocks + num_heads && slots > waiting;
 }
 
 // One block per compute unit, each taking the same number of row groups
@@ -636,15 +737,17 @@ int lm_head_blocks(int vocab, int compute_units) {
 }
 
 void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
-                          const KvCacheView& view, int layer, hipStream_t s, unsigned mask) {
+                          const KvCacheView& view, int layer, hipStream_t s, unsigned mask, int tag_slot) {
   const int g = a.num_heads / a.num_kv_heads;
-#define LCR_LAYER_CASE(G_)                                                          \
-  case G_:                                                                          \
-    if (a.paged) {                                                                  \
-      enqueue_layer_typed<4, 16, 64, true, G_>(a, w, view, layer, s, mask);         \
-    } else {                                                                        \
-      enqueue_layer_typed<4, 16, 64, false, G_>(a, w, view, layer, s, mask);        \
-    }                                                                               \
+  if (tag_slot < 0) tag_slot = layer;
+  LCR_CHECK(tag_slot < kExchangeTagSlots, "exchange tag slot " << tag_slot << " out of range");
+#define LCR_LAYER_CASE(G_)                                                                \
+  case G_:                                                                                \
+    if (a.paged) {                                                                        \
+      enqueue_layer_typed<4, 16, 64, true, G_>(a, w, view, layer, s, mask, tag_slot);     \
+    } else {                                                                              \
+      enqueue_layer_typed<4, 16, 64, false, G_>(a, w, view, layer, s, mask, tag_slot);    \
+    }                                                                                     \
     return;
   switch (g) {
     LCR_LAYER_CASE(1)
@@ -669,6 +772,7 @@ void enqueue_decode_head_sampled(const DecodeStepArgs& a, const SampledHead& h, 
   step.history = a.history;
   step.history_len = a.history_len;
   step.position = a.position;
+  step.epoch = a.epoch;
   enqueue_sample_step(a.logits, a.vocab, h.temperature, h.top_k, h.top_p, a.argmax_partials, blocks, a.partials,
                       a.sampled, step, s);
 }

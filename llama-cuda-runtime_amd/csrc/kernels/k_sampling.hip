@@ -396,6 +396,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
       if (pos + 1 < step.history_len) step.history[pos + 1] = picked;
       *step.position = pos + 1;
       *step.counter = draw + 1;
+      if (step.epoch != nullptr) *step.epoch = *step.epoch + 1u;
     }
   }
 }

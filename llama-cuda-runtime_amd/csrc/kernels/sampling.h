@@ -100,6 +100,7 @@ struct SampleStepState {
   int32_t* history = nullptr;        // [history_len] history[position + 1] = id
   int history_len = 0;
   int32_t* position = nullptr;       // [1] advanced by one
+  uint32_t* epoch = nullptr;         // [1] advanced by one (the decode step's step counter)
 };
 
 // Steps 2-6 of the stochastic path after an output head that wrote its

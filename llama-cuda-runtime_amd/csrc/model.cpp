@@ -53,9 +53,15 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
            decode_step_supported(config_.hidden_size, config_.intermediate_size,
                                  config_.num_heads, config_.num_kv_heads, config_.head_dim) &&
            config_.vocab_size > 0;
-  exchange_enabled_ = fused_ && options_.decode_exchange &&
+  {
+    const bool paged = options_.kv_layout == KvLayout::kPaged;
+    exchange_enabled_ = fused_ && options_.decode_exchange &&
+                        decode_exchange_fits(config_.num_heads, config_.num_kv_heads, config_.head_dim,
+                                             config_.hidden_size, paged, multiprocessors_, false);
+    exchange_oproj_ = exchange_enabled_ && options_.exchange_oproj &&
                       decode_exchange_fits(config_.num_heads, config_.num_kv_heads, config_.head_dim,
-                                           options_.kv_layout == KvLayout::kPaged, multiprocessors_);
+                                           config_.hidden_size, paged, multiprocessors_, true);
+  }
 
   // The table serves the fused decode step and the prefill q/k/v projection
   // with RoPE in its epilogue.
@@ -208,6 +214,7 @@ void Model::allocate_arena() {
       sizeof(int32_t),                                                // draw_counter_
       decode_exchange_words(config_.num_heads, config_.head_dim) * sizeof(unsigned long long),  // exchange_words_
       sizeof(int),                                                    // exchange_status_
+      sizeof(uint32_t),                                               // epoch_
   };
   size_t total = 0;
   for (size_t s : sizes) total = align_up(total, 256) + s;
@@ -234,6 +241,8 @@ void Model::allocate_arena() {
   draw_counter_ = arena_.alloc<int32_t>(1);
   exchange_words_ = arena_.alloc<unsigned long long>(decode_exchange_words(config_.num_heads, config_.head_dim));
   exchange_status_ = arena_.alloc<int>(1);
+  epoch_ = arena_.alloc<uint32_t>(1);
+  HIP_CHECK(hipMemset(epoch_, 0, sizeof(uint32_t)));
   clear_exchange();
   HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
   HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
@@ -360,11 +369,13 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.splits = splits;
   a.compute_units = multiprocessors_;
   a.exchange = exchange_enabled_ ? exchange_words_ : nullptr;
+  a.exchange_oproj = exchange_oproj_;
   a.exchange_status = exchange_status_;
   a.exchange_spins = std::max(1, options_.exchange_spins);
   a.exchange_read_offset = options_.exchange_test_unwritten
                                ? static_cast<int>(decode_exchange_words(config_.num_heads, config_.head_dim) / 2)
                                : 0;
+  a.epoch = epoch_;
   return a;
 }
 
@@ -373,6 +384,14 @@ int Model::exchange_status() const {
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipMemcpy(&status, exchange_status_, sizeof(int), hipMemcpyDeviceToHost));
   return status;
+}
+
+void Model::advance_epoch() {
+  uint32_t epoch = 0;
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipMemcpy(&epoch, epoch_, sizeof(uint32_t), hipMemcpyDeviceToHost));
+  epoch += 1;
+  HIP_CHECK(hipMemcpy(epoch_, &epoch, sizeof(uint32_t), hipMemcpyHostToDevice));
 }
 
 void Model::clear_exchange() {
@@ -617,9 +636,16 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
     mask = kDecodeQkv;
     bytes = (qd + 2 * kvd) * H * e + H * e + H * 4 + (qd + 2 * kvd) * e;
   } else if (kernel == "qkv_attention") {
-    // The exchange grid when the step uses it, else the two kernels.
+    // The exchange grid of q/k/v and attention when the step uses it, else
+    // the two kernels.
     mask = kDecodeQkv | kDecodeAttention;
     bytes = (qd + 2 * kvd) * H * e + H * e + H * 4 + (qd + 2 * kvd) * e + 2.0 * kvd * seq_len * e + qd * e;
+  } else if (kernel == "qkv_attention_oproj") {
+    // The exchange grid of q/k/v, attention and o_proj when the step uses
+    // it, else what runs in its place.
+    mask = kDecodeQkv | kDecodeAttention | kDecodeOProj;
+    bytes = (qd + 2 * kvd) * H * e + H * e + H * 4 + (qd + 2 * kvd) * e + 2.0 * kvd * seq_len * e + qd * e +
+            H * qd * e + 2 * H * 4;
   } else if (kernel == "attention") {
     mask = kDecodeAttention;
     bytes = 2.0 * kvd * seq_len * e + qd * e + qd * e;
@@ -660,7 +686,7 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
         const LayerWeights& lw = layers_[static_cast<size_t>(layer)];
         LayerDevicePtrs w{lw.input_norm, lw.qkv_proj, lw.o_proj, lw.post_attention_norm,
                           lw.gate_up_proj, lw.down_proj};
-        enqueue_decode_layer(args, w, kv_cache_->view(layer), layer, stream_, mask);
+        enqueue_decode_layer(args, w, kv_cache_->view(layer), layer, stream_, mask, i);
       }
     }
   };
@@ -683,6 +709,9 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
   HIP_CHECK(hipEventCreate(&start));
   HIP_CHECK(hipEventCreate(&stop));
   HIP_CHECK(hipGraphLaunch(exec, stream_));  // warm-up replay
+  // A new epoch for the timed replay, so no exchange word of the warm-up
+  // replay passes for one of its own.
+  advance_epoch();
   HIP_CHECK(hipEventRecord(start, stream_));
   HIP_CHECK(hipGraphLaunch(exec, stream_));
   HIP_CHECK(hipEventRecord(stop, stream_));

@@ -68,6 +68,7 @@ class Model {
     // grid, handing the query and the new key and value over in-grid
     // exchange words (kernels/exchange.h), when the device holds the grid.
     bool decode_exchange = true;
+    bool exchange_oproj = true;           // and the o_proj projection in the same grid
     int exchange_spins = 1 << 20;         // polls before an exchange wait gives up
     bool exchange_test_unwritten = false; // tests: waits read words no block writes
   };
@@ -140,8 +141,10 @@ class Model {
   // model's stream, cycling through the layers so each launch streams
   // different weights, each bracketed by its own pair of hipEvents. Returns
   // the mean launch duration in ms and the algorithmic bytes one launch moves.
-  // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", or
-  // "argmax" (the reduction of the head's per-block keys to the id alone).
+  // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head",
+  // "argmax" (the reduction of the head's per-block keys to the id alone),
+  // "qkv_attention" or "qkv_attention_oproj" (the exchange grids, or the
+  // kernels that run in their place).
   double time_decode_kernel(const std::string& kernel, int launches, double* bytes_per_launch);
   // Whether the decode step runs q/k/v and attention as one exchange grid.
   bool decode_exchange() const { return exchange_enabled_; }
@@ -150,6 +153,8 @@ class Model {
   int exchange_status() const;
   // Clears the exchange words and the status (after a wait gave up).
   void clear_exchange();
+  // Whether o_proj runs in the exchange grid too.
+  bool exchange_oproj() const { return exchange_oproj_; }
 
  private:
   void load_weights(const SafetensorsArchive& archive);
@@ -164,6 +169,7 @@ class Model {
   void enqueue_fused_step();
   void launch_fused_step(int seq_len);
   DecodeStepArgs step_args(int splits) const;
+  void advance_epoch();
 
   ModelConfig config_;
   Options options_;
@@ -206,6 +212,8 @@ class Model {
   unsigned long long* exchange_words_ = nullptr;  // decode_exchange_words(...)
   int* exchange_status_ = nullptr;
   bool exchange_enabled_ = false;
+  bool exchange_oproj_ = false;
+  uint32_t* epoch_ = nullptr;     // [1] decode steps completed (exchange tags)
   int32_t* pinned_state_ = nullptr;  // host {token, position}
 
   std::map<int, hipGraphExec_t> graphs_;  // by split count

@@ -1,9 +1,11 @@
-"""The decode step's q/k/v projection and single-split attention as one grid
-(kernels/exchange.h, qkv_attention_kernel): the attention blocks take their
-query and the new position's key and value from in-grid exchange words.
+"""The decode step's q/k/v projection, single-split attention and o_proj as
+one grid (kernels/exchange.h, qkv_attention_kernel): the attention blocks take
+their query and the new position's key and value from in-grid exchange words,
+and the o_proj blocks the attention output from tagged broadcast words.
 
-  - the grid is used on the Llama-3.2-1B geometry, both cache layouts;
-  - its logits equal the oracle's and the two-kernel step's bit for bit, from
+  - the grid is used on the Llama-3.2-1B geometry, both cache layouts, with
+    o_proj (grid 2) unless asked for without it (grid 1);
+  - its logits equal the oracle's and the separate kernels' bit for bit, from
     the first position on (a one-token prompt: the new key is the only one)
     and across the 64-position tile boundaries, graph-replayed and eager;
   - groups of 4 and 8 query heads per kv head (groups of 1 and 2 have more
@@ -43,10 +45,11 @@ def greedy_logits(m, prompt, steps):
 @pytest.mark.parametrize("paged", [False, True])
 def test_exchange_grid_is_used(lcr, small_ckpt, paged):
     m = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1)
-    enabled, status = m.exchange_status()
-    assert enabled and status == 0
+    assert m.exchange_status() == (2, 0)
+    one = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1, exchange_oproj=0)
+    assert one.exchange_status() == (1, 0)
     off = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1, decode_exchange=0)
-    assert off.exchange_status() == (False, 0)
+    assert off.exchange_status() == (0, 0)
 
 
 @pytest.mark.parametrize("graph", [1, 0])
@@ -57,18 +60,22 @@ def test_exchange_equals_oracle_and_two_kernel_step(lcr, small_ckpt, paged, grap
     cache, last in a full tile, first in a new tile and in a later wave's tile."""
     kw = dict(max_seq=256, paged=int(paged), use_graph=graph, prefill_via_decode=1)
     m = lcr.Model(small_ckpt, **kw)
+    one = lcr.Model(small_ckpt, exchange_oproj=0, **kw)
     ref = lcr.Model(small_ckpt, decode_exchange=0, **kw)
     o = oracle.OracleModel(small_ckpt, max_seq=256, paged=paged, multiprocessors=m.stats().multiprocessors)
     prompt = lcr.synthetic_tokens(prompt_len, m.vocab, seed=prompt_len)
     got = greedy_logits(m, prompt, 3)
-    two = greedy_logits(ref, prompt, 3)
+    got1 = greedy_logits(one, prompt, 3)
+    sep = greedy_logits(ref, prompt, 3)
     lo = [o.prefill(prompt, use_decode_path=True)]
     for _ in range(3):
         lo.append(o.decode(oracle.argmax(lo[-1])))
-    for s, (g, t, e) in enumerate(zip(got, two, lo)):
-        expect_bits_equal(g.view(np.uint32), t.view(np.uint32), f"step {s}: exchange vs two kernels")
-        expect_bits_equal(g.view(np.uint32), e.view(np.uint32), f"step {s}: exchange vs oracle")
-    assert m.exchange_status() == (True, 0)
+    for s, (g, g1, t, e) in enumerate(zip(got, got1, sep, lo)):
+        expect_bits_equal(g.view(np.uint32), e.view(np.uint32), f"step {s}: grid 2 vs oracle")
+        expect_bits_equal(g1.view(np.uint32), e.view(np.uint32), f"step {s}: grid 1 vs oracle")
+        expect_bits_equal(t.view(np.uint32), e.view(np.uint32), f"step {s}: separate kernels vs oracle")
+    assert m.exchange_status() == (2, 0)
+    assert one.exchange_status() == (1, 0)
 
 
 @pytest.mark.parametrize("kv_heads", [32, 16, 8, 4])
@@ -81,7 +88,7 @@ def test_exchange_group_sizes(lcr, tmp_path_factory, kv_heads, paged):
     # block plus one block per query head must fit (groups of 4 and 8 do on
     # 256 compute units; groups of 1 and 2 keep the two-kernel step).
     blocks = (32 + 2 * kv_heads) * 64 // 16 + 32
-    assert m.exchange_status() == (blocks <= m.stats().multiprocessors, 0)
+    assert m.exchange_status() == (2 if blocks <= m.stats().multiprocessors else 0, 0)
     o = oracle.OracleModel(ckpt, max_seq=256, paged=paged, multiprocessors=m.stats().multiprocessors)
     prompt = lcr.synthetic_tokens(70, m.vocab, seed=kv_heads)
     got = greedy_logits(m, prompt, 3)
@@ -105,21 +112,47 @@ def test_exchange_generate_greedy_matches_oracle(lcr, small_ckpt):
         tok = oracle.argmax(o.decode(tok))
         expected.append(tok)
     assert list(ids) == expected
-    assert m.exchange_status() == (True, 0)
+    assert m.exchange_status() == (2, 0)
 
 
-def test_exchange_wait_gives_up(lcr, small_ckpt):
+@pytest.mark.parametrize("oproj", [1, 0])
+def test_exchange_wait_gives_up(lcr, small_ckpt, oproj):
     """Waits pointed at words no block writes: each gives up after four polls
     and raises the status; the steps still finish (their logits are not
     valid), generate_greedy reports the failure, and clearing resets the
     status."""
-    m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=1, exchange_spins=4, exchange_test_unwritten=1)
+    m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=1, exchange_spins=4, exchange_test_unwritten=1,
+                  exchange_oproj=oproj)
+    grid = 2 if oproj else 1
     prompt = lcr.synthetic_tokens(5, m.vocab, seed=3)
     m.prefill(prompt)
-    enabled, status = m.exchange_status()
-    assert enabled and status == 1
+    assert m.exchange_status() == (grid, 1)
     m.exchange_clear()
-    assert m.exchange_status() == (True, 0)
+    assert m.exchange_status() == (grid, 0)
     with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
         m.generate_greedy(1, 4)
-    assert m.exchange_status() == (True, 0)  # the failure cleared it
+    assert m.exchange_status() == (grid, 0)  # the failure cleared it
+
+
+def test_exchange_kernel_timing_waits_for_its_own_launch(lcr, small_ckpt):
+    """The timing graphs launch the layers' grids many times in a row at one
+    position, each launch joining into the residual stream. Each launch's
+    broadcast words carry their own tag, so its o_proj blocks wait for its own
+    attention: after the same timing graphs, the exchange model and the
+    separate-kernel model hold the same state (the next step's logits are
+    the same bits)."""
+    kw = dict(max_seq=256, prefill_via_decode=1)
+    m = lcr.Model(small_ckpt, **kw)
+    ref = lcr.Model(small_ckpt, decode_exchange=0, **kw)
+    prompt = lcr.synthetic_tokens(40, m.vocab, seed=8)
+    a = m.logits(m.prefill(prompt))
+    b = ref.logits(ref.prefill(prompt))
+    expect_bits_equal(a.view(np.uint32), b.view(np.uint32), "prompt")
+    for name in ("qkv_attention_oproj", "qkv_attention", "o_proj", "qkv_attention_oproj"):
+        for model in (m, ref):
+            ms, nbytes = model.time_decode_kernel(name, 40)
+            assert ms > 0 and nbytes > 0
+    tok = oracle.argmax(a)
+    expect_bits_equal(m.logits(m.decode(tok)).view(np.uint32), ref.logits(ref.decode(tok)).view(np.uint32),
+                      "step after timing")
+    assert m.exchange_status() == (2, 0)

@@ -39,6 +39,8 @@ typedef struct lcr_model_options {
                            decode step in one grid, exchanging the query and the new key
                            and value in-grid (default 1; used when the device holds the grid) */
   int exchange_oproj;   /* extension: the o_proj projection joins that grid too (default 1) */
+  int exchange_split;   /* extension: split attention (long contexts) runs as two such grids:
+                           q/k/v + attention, and the split merge + o_proj (default 1) */
   int exchange_spins;   /* extension: polls before an exchange wait gives up (default 1 << 20) */
   int exchange_test_unwritten; /* tests only: exchange waits read words no block writes (default 0) */
 } lcr_model_options;

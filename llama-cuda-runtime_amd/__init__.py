@@ -98,6 +98,7 @@ class ModelOptions(ctypes.Structure):
         ("prefill_via_decode", ctypes.c_int),
         ("decode_exchange", ctypes.c_int),
         ("exchange_oproj", ctypes.c_int),
+        ("exchange_split", ctypes.c_int),
         ("exchange_spins", ctypes.c_int),
         ("exchange_test_unwritten", ctypes.c_int),
     ]

@@ -40,6 +40,7 @@ extern "C" void lcr_model_default_options(lcr_model_options* o) {
   o->prefill_via_decode = 0;
   o->decode_exchange = 1;
   o->exchange_oproj = 1;
+  o->exchange_split = 1;
   o->exchange_spins = 1 << 20;
   o->exchange_test_unwritten = 0;
 }
@@ -64,6 +65,7 @@ extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* 
     opt.prefill_via_decode = o.prefill_via_decode != 0;
     opt.decode_exchange = o.decode_exchange != 0;
     opt.exchange_oproj = o.exchange_oproj != 0;
+    opt.exchange_split = o.exchange_split != 0;
     opt.exchange_spins = o.exchange_spins > 0 ? o.exchange_spins : (1 << 20);
     opt.exchange_test_unwritten = o.exchange_test_unwritten != 0;
     auto handle = std::make_unique<lcr_model>();

@@ -90,21 +90,35 @@ struct AttnShared {
 };
 
 // What a block that runs inside the q/k/v projection's grid takes from it
-// (exchange.h): its query head and the key and value of the new position as
-// 3 * head_dim exchange words (query, key, value), plus LDS for them once
-// taken.
+// (exchange.h): its queries and, when its range holds the new position
+// (take_kv), that position's key and value; plus LDS for them once taken.
+//  - consume words (one head, one split): 3 * head_dim words (query, key,
+//    value) at `words`, one reader each, cleared when read;
+//  - broadcast words (`broadcast`; any split, one head or the whole group):
+//    the queries of the block's heads at q_words (head after head), the key
+//    at k_words and the value at v_words, tagged `tag`.
 template <int kHeadDim>
 struct AttnExchange {
-  unsigned long long* words;     // [3][kHeadDim]
+  unsigned long long* words;
+  bool broadcast;
+  unsigned long long* q_words;
+  unsigned long long* k_words;
+  unsigned long long* v_words;
+  bool take_kv;
   int spins;
   int* status;
-  float* q_lds;                  // [kHeadDim] LDS
+  float* q_lds;                  // [heads][kHeadDim] LDS
   elem_t* kv_lds;                // [2][kHeadDim] LDS, 16-byte aligned
   // When set, the head's output also goes out as broadcast words, two
   // elements each (element 2i in the low half), tagged `tag`, at
   // out_words[(head * kHeadDim) / 2 + i]: for the o_proj blocks of the grid.
   unsigned long long* out_words;
   uint32_t tag;
+};
+
+// No prologue work.
+struct NoPreWait {
+  __device__ void operator()() const {}
 };
 
 // Step 3's reduce-scatter: at offset O the lane keeps the half of its N values
@@ -153,26 +167,29 @@ using attn_flag = std::integral_constant<bool, B>;
 // keys were in. Tiles whose 64 positions are all in range skip the masking
 // selects.
 //
-// kExchange (one head, one split): the block runs inside the q/k/v
-// projection's grid. Its query and the new position's key and value are not
-// in memory yet; it issues its first tiles' cache loads, then takes them from
-// exchange words (`x`), and uses the taken key and value in place of the
-// cache's for position seq_len - 1. The arithmetic is unchanged.
-template <bool kPaged, int kHeadDim, int kHeads, bool kExchange = false>
+// kExchange: the block runs inside the q/k/v projection's grid. Its queries
+// and the new position's key and value are not in memory yet. It first runs
+// `prologue` (work of its own for the grid, every thread, before its own
+// registers fill), issues its first tiles' cache loads, then takes the
+// queries and the new key and value from exchange words (`x`), and uses the
+// taken key and value in place of the cache's for position seq_len - 1. The
+// arithmetic is unchanged.
+template <bool kPaged, int kHeadDim, int kHeads, bool kExchange = false, typename Prologue = NoPreWait>
 __device__ __forceinline__ void decode_attention_block(
     AttnShared<kPaged, kHeadDim, kHeads>& sh, elem_t* __restrict__ out,
     float* __restrict__ partials, const elem_t* __restrict__ q, const KvCacheView& view,
     int kv_head, int head0, int split, int splits, int seq_len, float scale,
-    const AttnExchange<kHeadDim>* x = nullptr) {
+    const AttnExchange<kHeadDim>* x = nullptr, Prologue prologue = Prologue{}) {
   constexpr int P = kHeadDim / 8;   // chunks per position
   constexpr int Q = 64 / P;         // positions per load instruction
   constexpr int G = kHeads;
-  static_assert(!kExchange || (kHeads == 1 && P <= 8), "exchange blocks serve one head");
+  static_assert(!kExchange || P <= 8, "exchange blocks take head_dim <= 64");
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) >> 6;
   const int j = lane % P;
   const int a = lane / P;
 
+  if constexpr (kExchange) prologue();
   const int chunk = (seq_len + splits - 1) / splits;
   const int begin = split * chunk;
   const int end = min(seq_len, begin + chunk);
@@ -220,34 +237,61 @@ __device__ __forceinline__ void decode_attention_block(
   auto exchange_wait = [&]() {
     if constexpr (kExchange) {
       static_assert(kHeadDim % 64 == 0, "exchange blocks take whole waves of words");
-      constexpr int N = 3 * kHeadDim / 64;
+      // Word i of what wave 0 takes: the queries, then the key, then the value.
+      auto keep = [&](int i, float v) {
+        if (i < G * kHeadDim) {
+          x->q_lds[i] = v;
+        } else {
+          x->kv_lds[i - G * kHeadDim] = float_to_elem(v);
+        }
+      };
       if (wave == 0) {
-        float vals[N];
-        exchange_take<N>(x->words, vals, x->spins, x->status);
+        if (!x->broadcast) {
+          constexpr int N = 3 * kHeadDim / 64;
+          float vals[N];
+          exchange_take<N>(x->words, vals, x->spins, x->status);
 #pragma unroll
-        for (int k = 0; k < N; ++k) {
-          const int i = lane + 64 * k;  // word i: query, key, value in turn
-          if (i < kHeadDim) {
-            x->q_lds[i] = vals[k];
+          for (int k = 0; k < N; ++k) keep(lane + 64 * k, vals[k]);
+        } else {
+          constexpr int NQ = G * kHeadDim / 64;
+          constexpr int NKV = 2 * kHeadDim / 64;
+          auto address = [&](int k) {
+            const int i = lane + 64 * k;
+            return i < G * kHeadDim ? x->q_words + i
+                                    : (i < G * kHeadDim + kHeadDim ? x->k_words + (i - G * kHeadDim)
+                                                                   : x->v_words + (i - G * kHeadDim - kHeadDim));
+          };
+          if (x->take_kv) {
+            uint32_t bits[NQ + NKV];
+            exchange_wait_tagged_at<NQ + NKV>(address, x->tag, bits, x->spins, x->status);
+#pragma unroll
+            for (int k = 0; k < NQ + NKV; ++k) keep(lane + 64 * k, __uint_as_float(bits[k]));
           } else {
-            x->kv_lds[i - kHeadDim] = float_to_elem(vals[k]);
+            uint32_t bits[NQ];
+            exchange_wait_tagged_at<NQ>(address, x->tag, bits, x->spins, x->status);
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) keep(lane + 64 * k, __uint_as_float(bits[k]));
           }
         }
       }
       __syncthreads();
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qv[0][e] = x->q_lds[8 * j + e] * scale;
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[g][e] = x->q_lds[g * kHeadDim + 8 * j + e] * scale;
+      }
     }
   };
-  // kExchange: position seq_len - 1 (index length - 1 of the one split) comes
-  // from the exchange, not from the cache, whose copy its producer may not
-  // have written yet: the lanes holding it overwrite their chunk of the tile
-  // that contains it (the last tile of the range, the last one its wave
-  // processes, so no later load of that wave is still in flight).
+  // kExchange: position seq_len - 1 comes from the exchange, not from the
+  // cache, whose copy its producer may not have written yet. It is the last
+  // position of the range of the block that takes it (take_kv): the lanes
+  // holding it overwrite their chunk of the tile that contains it (the last
+  // tile of the range, the last one its wave processes, so no later load of
+  // that wave is still in flight).
   auto patch_new = [&](int tile, vec16 (&kr)[P], vec16 (&vr)[P]) {
     if constexpr (kExchange) {
       const int idx = length - 1;
-      if (tile != idx / kAttnTile) return;
+      if (!x->take_kv || tile != idx / kAttnTile) return;
       const int in_tile = idx % kAttnTile;
 #pragma unroll
       for (int i = 0; i < P; ++i) {
@@ -430,9 +474,12 @@ __device__ __forceinline__ void decode_attention_block(
   // per block need their registers for the heads (and head_dim 128 needs
   // them for its tile), so they keep one set and refill the keys as soon as
   // the scores are taken and the values as soon as they are used.
-  auto run_tiles = [&](int first_tile, int last_tile, int window) {
+  // `waits` (compile-time): this window is the first, whose tiles take the
+  // exchange wait (a separate instance, so later windows hold nothing for it).
+  auto run_tiles = [&](int first_tile, int last_tile, int window, auto waits) {
+    constexpr bool kWaits = decltype(waits)::value;
     if (first_tile + wave >= last_tile) {
-      if (window == 0) exchange_wait();
+      if constexpr (kWaits) exchange_wait();
       return;
     }
     if constexpr (G <= 2 && P <= 8) {
@@ -458,7 +505,7 @@ __device__ __forceinline__ void decode_attention_block(
       tile_chunks(tile, window, o);
       load_chunks(view.keys, o, ka);
       load_chunks(view.values, o, va);
-      bool first = window == 0;
+      bool first = kWaits;
       while (true) {
         const int t1 = tile + kAttnWaves;
         const bool more1 = t1 < last_tile;
@@ -493,11 +540,13 @@ __device__ __forceinline__ void decode_attention_block(
       tile_chunks(tile, window, o);
       load_chunks(view.keys, o, kr);
       load_chunks(view.values, o, vr);
+      if constexpr (kWaits) exchange_wait();
       while (true) {
         const int next = tile + kAttnWaves;
         const bool more = next < last_tile;
         const int count = tile_count(tile);
         const bool full = count == kAttnTile;
+        patch_new(tile, kr, vr);
         if (full) {
           score_tile(count, kr, attn_flag<true>{});
         } else {
@@ -524,16 +573,15 @@ __device__ __forceinline__ void decode_attention_block(
   const int tiles = (length + kAttnTile - 1) / kAttnTile;
   if constexpr (kPaged) {
     constexpr int kWindowTiles = kAttnPositionTable / kAttnTile;
-    for (int first = 0; first < tiles; first += kWindowTiles) {
-      if (first > 0) {
-        __syncthreads();  // every wave is done with the previous window's table
-        fill_table(first * kAttnTile);
-        __syncthreads();
-      }
-      run_tiles(first, min(tiles, first + kWindowTiles), first * kAttnTile);
+    if (tiles > 0) run_tiles(0, min(tiles, kWindowTiles), 0, attn_flag<kExchange>{});
+    for (int first = kWindowTiles; first < tiles; first += kWindowTiles) {
+      __syncthreads();  // every wave is done with the previous window's table
+      fill_table(first * kAttnTile);
+      __syncthreads();
+      run_tiles(first, min(tiles, first + kWindowTiles), first * kAttnTile, attn_flag<false>{});
     }
   } else {
-    run_tiles(0, tiles, 0);
+    run_tiles(0, tiles, 0, attn_flag<kExchange>{});
   }
 
   // Step 6.
@@ -614,25 +662,33 @@ constexpr int kMaxHeadDim = 128;
 constexpr int kMergeLdsFloats = kMaxSplits * (kPartialHeader + kMaxHeadDim) + kMaxSplits;
 static_assert(kMaxSplits <= 64, "the merge takes the maximum over the splits in one wave");
 
+//
+// A block of more than kMergeThreads threads may run it: the others only pass
+// the barriers and take part in the output loop. With `out_words`, the output
+// also goes out as broadcast words, two elements each, tagged `tag`, at
+// out_words[(head * head_dim) / 2 + i] (head_dim a multiple of 64).
 __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
                                                      const float* __restrict__ partials, int head,
-                                                     int splits, int head_dim, float* lds) {
+                                                     int splits, int head_dim, float* lds,
+                                                     unsigned long long* out_words = nullptr, uint32_t tag = 0) {
   const int stride = kPartialHeader + head_dim;
   const float* base = partials + static_cast<size_t>(head) * splits * stride;
   const int n = splits * stride;
   // Every load is issued before the first LDS store: a loop of load-then-
   // store would wait out one memory round trip per iteration.
   constexpr int kPer = (kMaxSplits * (kPartialHeader + kMaxHeadDim) + kMergeThreads - 1) / kMergeThreads;
-  float staged[kPer];
+  if (threadIdx.x < kMergeThreads) {
+    float staged[kPer];
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int i = static_cast<int>(threadIdx.x) + k * kMergeThreads;
-    staged[k] = i < n ? base[i] : 0.0f;
-  }
+    for (int k = 0; k < kPer; ++k) {
+      const int i = static_cast<int>(threadIdx.x) + k * kMergeThreads;
+      staged[k] = i < n ? base[i] : 0.0f;
+    }
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int i = static_cast<int>(threadIdx.x) + k * kMergeThreads;
-    if (i < n) lds[i] = staged[k];
+    for (int k = 0; k < kPer; ++k) {
+      const int i = static_cast<int>(threadIdx.x) + k * kMergeThreads;
+      if (i < n) lds[i] = staged[k];
+    }
   }
   __syncthreads();
   float* c = lds + kMaxSplits * (kPartialHeader + kMaxHeadDim);
@@ -652,7 +708,16 @@ __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
       tl = __builtin_fmaf(lds[s * stride + 1], c[s], tl);
       sum = __builtin_fmaf(c[s], lds[s * stride + kPartialHeader + d], sum);
     }
-    out[static_cast<size_t>(head) * head_dim + d] = float_to_elem(sum * (1.0f / tl));
+    const elem_t e = float_to_elem(sum * (1.0f / tl));
+    out[static_cast<size_t>(head) * head_dim + d] = e;
+    if (out_words != nullptr) {
+      // d and d + 1 are neighbouring lanes of one wave (whole waves of d).
+      const uint32_t bits = e.bits;
+      const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1));
+      if ((d & 1) == 0) {
+        exchange_put_tagged(out_words + (static_cast<size_t>(head) * head_dim + d) / 2, tag, bits | (next << 16));
+      }
+    }
   }
   __syncthreads();
 }

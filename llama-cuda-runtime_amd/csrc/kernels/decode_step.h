@@ -66,11 +66,15 @@ struct DecodeStepArgs {
   int compute_units;         // of the device: sizes the output head's grid
   // In-grid exchange (exchange.h): when set and splits == 1, the q/k/v
   // projection and the attention run as one grid (with exchange_oproj, the
-  // o_proj projection too). Words (X = num_heads * head_dim): [0, 3X) the
-  // query, key and value hand-over, [num_heads][3][head_dim]; [3X, 3.5X) the
-  // attention output, two elements per word; [3.5X, 7X) never written.
+  // o_proj projection too); with exchange_split and splits > 1, the q/k/v
+  // projection and the split attention run as one grid, and (with
+  // exchange_oproj) the split merge and o_proj as another. Words: see
+  // exchange_*_word() below; as many again after the written ones are never
+  // written (tests of the give-up path read there).
   unsigned long long* exchange;
   bool exchange_oproj;
+  bool exchange_split;
+  int exchange_slots;        // blocks of the split grid the device holds at once
   int* exchange_status;      // [1] raised by a wait that gave up
   int exchange_spins;        // polls before a wait gives up
   int exchange_read_offset;  // added to every word the grid reads (0; 3.5X in tests of the give-up path)
@@ -83,9 +87,27 @@ bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads,
 // and all its blocks fit on the device at once.
 bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, int hidden, bool paged,
                           int compute_units, bool with_oproj);
+// Blocks of the split exchange grid the device holds at once, 0 if none.
+int decode_split_exchange_slots(int num_heads, int num_kv_heads, int head_dim, bool paged, int compute_units);
+
+// Exchange word regions (X = num_heads * head_dim):
+//  [0, 3X)     the query, key and value hand-over of one-split grids,
+//              [num_heads][3][head_dim], read once and cleared;
+//  [3X, 3.5X)  the attention output, two elements per word, tagged;
+//  [3.5X, ...) the q/k/v projection's output in row order, tagged (at most
+//              3X words: num_kv_heads <= num_heads).
+__host__ __device__ inline size_t exchange_attn_out_word(int num_heads, int head_dim) {
+  return 3 * static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim);
+}
+__host__ __device__ inline size_t exchange_qkv_word(int num_heads, int head_dim) {
+  return 7 * static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim) / 2;
+}
+inline size_t exchange_written_words(int num_heads, int head_dim) {
+  return 13 * static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim) / 2;
+}
 // Exchange words of the step (see DecodeStepArgs::exchange).
 inline size_t decode_exchange_words(int num_heads, int head_dim) {
-  return 7 * static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim);
+  return 2 * exchange_written_words(num_heads, head_dim);
 }
 // Launches of one graph that exchange words through the same buffer
 // (enqueue_decode_layer's tag_slot is below this).

@@ -110,17 +110,17 @@ __device__ __forceinline__ void exchange_put_tagged(unsigned long long* word, ui
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One wave waits for N words per lane (word lane + 64 k of `words`) to carry
-// `tag`, two polls in flight as in exchange_take, at most `spins` polls;
-// returns the payloads.
-template <int N>
-__device__ __forceinline__ void exchange_wait_tagged(unsigned long long* words, uint32_t tag, uint32_t (&out)[N],
-                                                     int spins, int* status) {
+// One wave waits for N words per lane to carry `tag`, two polls in flight as
+// in exchange_take, at most `spins` polls; returns the payloads. Word k of a
+// lane is at address(k) (by default word lane + 64 k of `words`).
+template <int N, typename Address>
+__device__ __forceinline__ void exchange_wait_tagged_at(Address address, uint32_t tag, uint32_t (&out)[N],
+                                                        int spins, int* status) {
   const int lane = static_cast<int>(threadIdx.x & 63u);
   unsigned long long a[N], b[N];
   auto poll = [&](unsigned long long (&w)[N]) {
 #pragma unroll
-    for (int k = 0; k < N; ++k) w[k] = exchange_peek(words + lane + 64 * k);
+    for (int k = 0; k < N; ++k) w[k] = exchange_peek(address(k));
   };
   auto all_current = [&](const unsigned long long (&w)[N]) {
     bool ok = true;
@@ -147,6 +147,13 @@ __device__ __forceinline__ void exchange_wait_tagged(unsigned long long* words, 
   }
 #pragma unroll
   for (int k = 0; k < N; ++k) out[k] = static_cast<uint32_t>(a[k]);
+}
+
+template <int N>
+__device__ __forceinline__ void exchange_wait_tagged(unsigned long long* words, uint32_t tag, uint32_t (&out)[N],
+                                                     int spins, int* status) {
+  const int lane = static_cast<int>(threadIdx.x & 63u);
+  exchange_wait_tagged_at<N>([&](int k) { return words + lane + 64 * k; }, tag, out, spins, status);
 }
 
 }  // namespace lcr

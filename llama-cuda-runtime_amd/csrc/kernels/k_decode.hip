@@ -142,18 +142,26 @@ struct QkvShared {
 // head: the first WAVES / 2 waves take the first rows of the pairs, the others
 // the second ones. With kPublish the rotated query and key values and the
 // value rows also go out as exchange words (exchange.h) for the attention
-// blocks of the same grid, 3 * HD words per query head h: its query at
-// x[3 h HD + i], and the key and value of its kv head at x[3 h HD + HD + i]
-// and x[3 h HD + 2 HD + i] (a kv head's once for each of its G query heads).
+// blocks of the same grid:
+//  - kPublishConsume: 3 * HD consume words per query head h: its query at
+//    x[3 h HD + i], and the key and value of its kv head at x[3 h HD + HD + i]
+//    and x[3 h HD + 2 HD + i] (a kv head's once for each of its G query heads);
+//  - kPublishBroadcast: broadcast words tagged `tag`, in the projection's row
+//    order (queries, keys, values, head after head) from
+//    exchange_qkv_word().
 //
 // At layer 0 block 0 also seeds the residual sum with the embedding row,
 // unless `seed` is false (the exchange grid with o_proj blocks, which read
 // the embedding row themselves: a seed written from one XCD's L2 and joins
 // written from others could be written back in either order).
-template <int NCH, int HD, bool kPaged, int WAVES, int RW, int G, bool kPublish>
+constexpr int kPublishNone = 0;
+constexpr int kPublishConsume = 1;
+constexpr int kPublishBroadcast = 2;
+
+template <int NCH, int HD, bool kPaged, int WAVES, int RW, int G, int kPublish>
 __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDevicePtrs& w,
                                           const KvCacheView& view, int layer, int block,
-                                          QkvShared<NCH, WAVES / 2 * RW>& sh, bool seed = true) {
+                                          QkvShared<NCH, WAVES / 2 * RW>& sh, bool seed = true, uint32_t tag = 0) {
   constexpr int H = NCH * 512;
   constexpr int HALF = HD / 2;
   constexpr int PAIRS = WAVES / 2 * RW;  // rotation pairs per block
@@ -208,6 +216,21 @@ __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDe
     const float lo = sh.rowv[k];
     const float hi = sh.rowv[PAIRS + k];
     unsigned long long* xw = a.exchange;
+    if constexpr (kPublish == kPublishBroadcast) {
+      // Published first, in row order: the rotated or copied values below,
+      // as floats of their element values.
+      unsigned long long* dst = xw + exchange_qkv_word(a.num_heads, HD) + static_cast<size_t>(head) * HD;
+      float lo_out = lo, hi_out = hi;
+      if (head < a.num_heads + a.num_kv_heads) {
+        lo_out = elem_to_float(float_to_elem(lo * rot.x - hi * rot.y));
+        hi_out = elem_to_float(float_to_elem(hi * rot.x + lo * rot.y));
+      } else {
+        lo_out = elem_to_float(float_to_elem(lo));
+        hi_out = elem_to_float(float_to_elem(hi));
+      }
+      exchange_put_tagged(dst + i, tag, __float_as_uint(lo_out));
+      exchange_put_tagged(dst + i + HALF, tag, __float_as_uint(hi_out));
+    }
     if (head < a.num_heads + a.num_kv_heads) {
       const float ra = lo * rot.x - hi * rot.y;
       const float rb = hi * rot.x + lo * rot.y;
@@ -216,7 +239,7 @@ __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDe
       if (head < a.num_heads) {
         a.q[head * HD + i] = ea;
         a.q[head * HD + i + HALF] = eb;
-        if constexpr (kPublish) {
+        if constexpr (kPublish == kPublishConsume) {
           unsigned long long* dst = xw + static_cast<size_t>(3 * head) * HD;
           exchange_put(dst + i, elem_to_float(ea));
           exchange_put(dst + i + HALF, elem_to_float(eb));
@@ -226,7 +249,7 @@ __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDe
         const size_t off = view.offset<kPaged>(kvh, pos);
         view.keys[off + i] = ea;
         view.keys[off + i + HALF] = eb;
-        if constexpr (kPublish) {
+        if constexpr (kPublish == kPublishConsume) {
 #pragma unroll
           for (int g = 0; g < G; ++g) {
             unsigned long long* dst = xw + static_cast<size_t>(3 * (kvh * G + g) + 1) * HD;
@@ -242,7 +265,7 @@ __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDe
       const elem_t eb = float_to_elem(hi);
       view.values[off + i] = ea;
       view.values[off + i + HALF] = eb;
-      if constexpr (kPublish) {
+      if constexpr (kPublish == kPublishConsume) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           unsigned long long* dst = xw + static_cast<size_t>(3 * (kvh * G + g) + 2) * HD;
@@ -258,7 +281,7 @@ template <int NCH, int HD, bool kPaged>
 __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(DecodeStepArgs a, LayerDevicePtrs w,
                                                             KvCacheView view, int layer) {
   __shared__ QkvShared<NCH, kWaves / 2 * kQkvRowsPerWave> sh;
-  qkv_block<NCH, HD, kPaged, kWaves, kQkvRowsPerWave, 1, false>(a, w, view, layer, blockIdx.x, sh);
+  qkv_block<NCH, HD, kPaged, kWaves, kQkvRowsPerWave, 1, kPublishNone>(a, w, view, layer, blockIdx.x, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -405,7 +428,7 @@ __global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepA
   __shared__ ExchangeStepShared<NCH, HD, kPaged> sh;
   const int b = static_cast<int>(blockIdx.x);
   if (b < qkv_blocks) {
-    qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, true>(a, w, view, layer, b, sh.qkv, !kOProj);
+    qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, kPublishConsume>(a, w, view, layer, b, sh.qkv, !kOProj);
     return;
   }
   const size_t broadcast = 3 * static_cast<size_t>(a.num_heads) * HD;  // first broadcast word
@@ -427,6 +450,8 @@ __global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepA
   const int head = kv_head * G + g;
   AttnExchange<HD> x;
   x.words = a.exchange + a.exchange_read_offset + static_cast<size_t>(3 * head) * HD;
+  x.broadcast = false;
+  x.take_kv = true;
   x.spins = a.exchange_spins;
   x.status = a.exchange_status;
   x.q_lds = sh.at.q;
@@ -436,6 +461,89 @@ __global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepA
   const int seq_len = *a.position + 1;
   decode_attention_block<kPaged, HD, 1, true>(sh.at.attn, a.attn, a.partials, nullptr, view, kv_head, head,
                                               0, 1, seq_len, scale, &x);
+}
+
+// q/k/v projection and split attention in one grid (splits > 1). Every block
+// is an attention block, numbered as attention_step_kernel numbers them; the
+// first qkv_blocks of them also compute 16 q/k/v rows (kAttnWaves waves of
+// kQkvRowsPerWave rows), after issuing their first cache tiles and before
+// they wait, and publish them as broadcast words for every attention block.
+// All blocks fit on the device at once (the host checks), and each does its
+// own q/k/v rows before it waits, so every wait is eventually served. The
+// split partials go to memory for the merge, as attention_step_kernel's do.
+template <int NCH, int HD, bool kPaged, int G, int kHeads>
+__global__ __launch_bounds__(kAttnThreads) void split_exchange_kernel(DecodeStepArgs a, LayerDevicePtrs w,
+                                                                      KvCacheView view, int layer, int qkv_blocks,
+                                                                      float scale, int tag_slot) {
+  __shared__ AttnShared<kPaged, HD, kHeads> ash;
+  __shared__ QkvShared<NCH, kAttnWaves / 2 * kQkvRowsPerWave> qsh;
+  __shared__ float q_lds[kHeads * HD];
+  __shared__ __attribute__((aligned(16))) elem_t kv_lds[2 * HD];
+  constexpr int kBlocksPerGroup = G / kHeads;
+  const int b = static_cast<int>(blockIdx.x);
+  const uint32_t tag = (*a.epoch) * static_cast<uint32_t>(kExchangeTagSlots) + static_cast<uint32_t>(tag_slot) + 1u;
+  auto project = [&]() {
+    if (b < qkv_blocks) {
+      qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, kPublishBroadcast>(a, w, view, layer, b, qsh, true,
+                                                                                     tag);
+    }
+  };
+  const int seq_len = *a.position + 1;
+  const int splits = min(a.splits, seq_len);
+  int unit, g = 0;
+  if (kBlocksPerGroup > 1) {
+    attention_block_coords(b, a.num_kv_heads * a.splits, kBlocksPerGroup, &unit, &g);
+  } else {
+    unit = b;
+  }
+  const int kv_head = unit / a.splits;
+  const int split = unit % a.splits;
+  if (split >= splits) {
+    // No range at this position (a graph captured for more splits): only the
+    // projection rows, if the block has any.
+    project();
+    return;
+  }
+  const int head0 = kv_head * G + g * kHeads;
+  unsigned long long* words = a.exchange + a.exchange_read_offset + exchange_qkv_word(a.num_heads, HD);
+  AttnExchange<HD> x;
+  x.words = nullptr;
+  x.broadcast = true;
+  x.q_words = words + static_cast<size_t>(head0) * HD;
+  x.k_words = words + static_cast<size_t>(a.num_heads + kv_head) * HD;
+  x.v_words = words + static_cast<size_t>(a.num_heads + a.num_kv_heads + kv_head) * HD;
+  // The split whose range holds the new position (splits past the end of the
+  // sequence have empty ranges, so it need not be the last one).
+  const int chunk = (seq_len + splits - 1) / splits;
+  x.take_kv = split == (seq_len - 1) / chunk;
+  x.spins = a.exchange_spins;
+  x.status = a.exchange_status;
+  x.q_lds = q_lds;
+  x.kv_lds = kv_lds;
+  x.out_words = nullptr;
+  x.tag = tag;
+  decode_attention_block<kPaged, HD, kHeads, true>(ash, a.attn, a.partials, nullptr, view, kv_head, head0, split,
+                                                   splits, seq_len, scale, &x, project);
+}
+
+// The split merge and o_proj in one grid: blocks 0 .. num_heads - 1 merge one
+// query head's split partials (from memory, written by the previous kernel),
+// as attention_merge_step_kernel does, and publish the output as broadcast
+// words; the rest are the exchange grid's o_proj blocks.
+template <int NCH, int HD>
+__global__ __launch_bounds__(kAttnThreads) void merge_oproj_kernel(DecodeStepArgs a, LayerDevicePtrs w,
+                                                                   int tag_slot) {
+  __shared__ float lds[kMergeLdsFloats];
+  __shared__ __attribute__((aligned(16))) elem_t xs[NCH * 512];
+  const int b = static_cast<int>(blockIdx.x);
+  const uint32_t tag = (*a.epoch) * static_cast<uint32_t>(kExchangeTagSlots) + static_cast<uint32_t>(tag_slot) + 1u;
+  const size_t attn_words = exchange_attn_out_word(a.num_heads, HD);
+  if (b >= a.num_heads) {
+    oproj_block<NCH>(a, w.o, a.exchange + a.exchange_read_offset + attn_words, tag, b - a.num_heads, xs, false);
+    return;
+  }
+  const int splits = min(a.splits, *a.position + 1);
+  merge_split_partials(a.attn, a.partials, b, splits, HD, lds, a.exchange + attn_words, tag);
 }
 
 // Split merge (splits > 1 only), one kMergeThreads-thread block per query head.
@@ -640,6 +748,32 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
     HIP_CHECK_LAUNCH();
     mask &= ~(kDecodeQkv | kDecodeAttention);
   }
+  if (a.exchange != nullptr && a.exchange_split && a.splits > 1 && (mask & kDecodeQkv) && (mask & kDecodeAttention)) {
+    constexpr int kGroupHeads = G <= kLongContextHeads ? G : (G % kLongContextHeads == 0 ? kLongContextHeads : 1);
+    const bool grouped = a.splits >= kGroupedMinSplits && kGroupHeads > 1;
+    const int units = a.num_kv_heads * a.splits * (grouped ? G / kGroupHeads : G);
+    const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
+    if (units >= qkv_blocks && units <= a.exchange_slots) {
+      const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
+      if (grouped) {
+        split_exchange_kernel<NCH, HD, kPaged, G, kGroupHeads>
+            <<<units, kAttnThreads, 0, s>>>(a, w, view, layer, qkv_blocks, scale, tag_slot);
+      } else {
+        split_exchange_kernel<NCH, HD, kPaged, G, 1><<<units, kAttnThreads, 0, s>>>(a, w, view, layer, qkv_blocks,
+                                                                                   scale, tag_slot);
+      }
+      HIP_CHECK_LAUNCH();
+      if (a.exchange_oproj && (mask & kDecodeOProj)) {
+        merge_oproj_kernel<NCH, HD><<<a.num_heads + a.hidden / (kAttnWaves * kOProjRowsPerWave), kAttnThreads, 0, s>>>(
+            a, w, tag_slot);
+        mask &= ~kDecodeOProj;
+      } else {
+        attention_merge_step_kernel<<<a.num_heads, kMergeThreads, 0, s>>>(a, HD);
+      }
+      HIP_CHECK_LAUNCH();
+      mask &= ~(kDecodeQkv | kDecodeAttention);
+    }
+  }
   if (mask & kDecodeQkv) {
     qkv_rope_kernel<NCH, HD, kPaged><<<qkv_rows / (kWaves * kQkvRowsPerWave), kThreads, 0, s>>>(a, w, view, layer);
     HIP_CHECK_LAUNCH();
@@ -723,6 +857,44 @@ bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, int hid
   if (!with_oproj) return slots >= qkv_blocks + num_heads;
   const int waiting = num_heads + hidden / (kAttnWaves * kOProjRowsPerWave);
   return slots >= qkv_blocks + num_heads && slots > waiting;
+}
+
+// Blocks of the split exchange grid the device holds at once (the fewest over
+// its variants for this geometry), or 0 when it has none.
+int decode_split_exchange_slots(int num_heads, int num_kv_heads, int head_dim, bool paged, int compute_units) {
+  if (head_dim != 64 || num_kv_heads <= 0 || num_heads * head_dim != 2048) return 0;
+  const int g = num_heads / num_kv_heads;
+  const int qkv_rows = (num_heads + 2 * num_kv_heads) * head_dim;
+  if (qkv_rows % (kAttnWaves * kQkvRowsPerWave) != 0) return 0;
+  int fewest = 1 << 30;
+  auto consider = [&](const void* fn) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kAttnThreads, 0) != hipSuccess) per_cu = 0;
+    fewest = std::min(fewest, per_cu * compute_units);
+  };
+#define LCR_SPLIT_FNS(G_)                                                                                      \
+  case G_: {                                                                                                   \
+    constexpr int kGH = G_ <= kLongContextHeads ? G_ : (G_ % kLongContextHeads == 0 ? kLongContextHeads : 1); \
+    if (paged) {                                                                                               \
+      consider(reinterpret_cast<const void*>(&split_exchange_kernel<4, 64, true, G_, 1>));                    \
+      consider(reinterpret_cast<const void*>(&split_exchange_kernel<4, 64, true, G_, kGH>));                  \
+    } else {                                                                                                   \
+      consider(reinterpret_cast<const void*>(&split_exchange_kernel<4, 64, false, G_, 1>));                   \
+      consider(reinterpret_cast<const void*>(&split_exchange_kernel<4, 64, false, G_, kGH>));                 \
+    }                                                                                                          \
+    consider(reinterpret_cast<const void*>(&merge_oproj_kernel<4, 64>));                                       \
+    break;                                                                                                     \
+  }
+  switch (g) {
+    LCR_SPLIT_FNS(1)
+    LCR_SPLIT_FNS(2)
+    LCR_SPLIT_FNS(4)
+    LCR_SPLIT_FNS(8)
+    default:
+      return 0;
+  }
+#undef LCR_SPLIT_FNS
+  return fewest == (1 << 30) ? 0 : fewest;
 }
 
 // One block per compute unit, each taking the same number of row groups

@@ -58,6 +58,10 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
     exchange_enabled_ = fused_ && options_.decode_exchange &&
                         decode_exchange_fits(config_.num_heads, config_.num_kv_heads, config_.head_dim,
                                              config_.hidden_size, paged, multiprocessors_, false);
+    exchange_split_slots_ = fused_ && options_.decode_exchange && options_.exchange_split
+                                ? decode_split_exchange_slots(config_.num_heads, config_.num_kv_heads,
+                                                              config_.head_dim, paged, multiprocessors_)
+                                : 0;
     exchange_oproj_ = exchange_enabled_ && options_.exchange_oproj &&
                       decode_exchange_fits(config_.num_heads, config_.num_kv_heads, config_.head_dim,
                                            config_.hidden_size, paged, multiprocessors_, true);
@@ -368,8 +372,10 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.paged = options_.kv_layout == KvLayout::kPaged;
   a.splits = splits;
   a.compute_units = multiprocessors_;
-  a.exchange = exchange_enabled_ ? exchange_words_ : nullptr;
+  a.exchange = (exchange_enabled_ || exchange_split_slots_ > 0) ? exchange_words_ : nullptr;
   a.exchange_oproj = exchange_oproj_;
+  a.exchange_split = exchange_split_slots_ > 0;
+  a.exchange_slots = exchange_split_slots_;
   a.exchange_status = exchange_status_;
   a.exchange_spins = std::max(1, options_.exchange_spins);
   a.exchange_read_offset = options_.exchange_test_unwritten

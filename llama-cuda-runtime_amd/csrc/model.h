@@ -69,6 +69,7 @@ class Model {
     // exchange words (kernels/exchange.h), when the device holds the grid.
     bool decode_exchange = true;
     bool exchange_oproj = true;           // and the o_proj projection in the same grid
+    bool exchange_split = true;           // split attention: q/k/v + attention, and merge + o_proj, as grids
     int exchange_spins = 1 << 20;         // polls before an exchange wait gives up
     bool exchange_test_unwritten = false; // tests: waits read words no block writes
   };
@@ -155,6 +156,7 @@ class Model {
   void clear_exchange();
   // Whether o_proj runs in the exchange grid too.
   bool exchange_oproj() const { return exchange_oproj_; }
+  bool exchange_split() const { return exchange_split_slots_ > 0; }
 
  private:
   void load_weights(const SafetensorsArchive& archive);
@@ -213,6 +215,7 @@ class Model {
   int* exchange_status_ = nullptr;
   bool exchange_enabled_ = false;
   bool exchange_oproj_ = false;
+  int exchange_split_slots_ = 0;  // 0: split attention keeps separate kernels
   uint32_t* epoch_ = nullptr;     // [1] decode steps completed (exchange tags)
   int32_t* pinned_state_ = nullptr;  // host {token, position}
 

@@ -156,3 +156,44 @@ def test_exchange_kernel_timing_waits_for_its_own_launch(lcr, small_ckpt):
     expect_bits_equal(m.logits(m.decode(tok)).view(np.uint32), ref.logits(ref.decode(tok)).view(np.uint32),
                       "step after timing")
     assert m.exchange_status() == (2, 0)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("splits", [8, 32])
+def test_split_exchange_grids_match_oracle(lcr, small_ckpt, paged, splits):
+    """Split attention as two grids: q/k/v + attention (every block an
+    attention block, the first 192 computing q/k/v rows first and publishing
+    broadcast words), then the split merge + o_proj. 8 splits run per-head
+    blocks (256 of them) and 32 splits whole-group blocks (256): the logits
+    equal the oracle's with the same split count and the separate kernels',
+    bit for bit, including steps whose position leaves later splits empty."""
+    kw = dict(max_seq=512, paged=int(paged), prefill_via_decode=1, attention_splits=splits)
+    m = lcr.Model(small_ckpt, **kw)
+    ref = lcr.Model(small_ckpt, exchange_split=0, **kw)
+    o = oracle.OracleModel(small_ckpt, max_seq=512, paged=paged, multiprocessors=m.stats().multiprocessors,
+                           attention_splits=splits)
+    for prompt_len in (5, 300):
+        for model in (m, ref):
+            model.reset()
+        o.reset()
+        prompt = lcr.synthetic_tokens(prompt_len, m.vocab, seed=prompt_len + splits)
+        got = greedy_logits(m, prompt, 3)
+        sep = greedy_logits(ref, prompt, 3)
+        lo = [o.prefill(prompt, use_decode_path=True)]
+        for _ in range(3):
+            lo.append(o.decode(oracle.argmax(lo[-1])))
+        for s, (g, t, e) in enumerate(zip(got, sep, lo)):
+            expect_bits_equal(t.view(np.uint32), e.view(np.uint32), f"{prompt_len}: step {s}: separate vs oracle")
+            expect_bits_equal(g.view(np.uint32), e.view(np.uint32), f"{prompt_len}: step {s}: grids vs oracle")
+    assert m.exchange_status()[1] == 0
+
+
+def test_split_exchange_wait_gives_up(lcr, small_ckpt):
+    """The split grids' waits pointed at words no block writes give up and
+    raise the status; every kernel still exits."""
+    m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=1, attention_splits=8, exchange_spins=4,
+                  exchange_test_unwritten=1)
+    m.prefill(lcr.synthetic_tokens(5, m.vocab, seed=4))
+    assert m.exchange_status()[1] == 1
+    m.exchange_clear()
+    assert m.exchange_status()[1] == 0

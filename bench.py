@@ -209,6 +209,7 @@ def long_context(lcr, model_dir: Path, config: dict, ctx: int, steps: int = 64) 
     m.set_position(ctx)
     _, ms = m.generate_greedy(1, steps)
     att_ms, att_bytes = m.time_decode_kernel("attention", 16)
+    grid_ms, grid_bytes = m.time_decode_kernel("qkv_attention_oproj", 16)
     st = m.stats()
     splits = m.decode_splits(ctx + steps // 2)
     m.close()
@@ -221,6 +222,11 @@ def long_context(lcr, model_dir: Path, config: dict, ctx: int, steps: int = 64) 
         "attention_us_per_layer": att_ms * 1000.0,
         "attention_bytes_per_layer": att_bytes,
         "attention_gbs": att_bytes / (att_ms / 1000.0) / 1e9,
+        # What the step runs for q/k/v, attention, merge and o_proj: the two
+        # exchange grids (or the separate kernels where the device lacks them).
+        "qkv_attention_oproj_us_per_layer": grid_ms * 1000.0,
+        "qkv_attention_oproj_bytes_per_layer": grid_bytes,
+        "qkv_attention_oproj_gbs": grid_bytes / (grid_ms / 1000.0) / 1e9,
     }
 
 

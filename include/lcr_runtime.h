@@ -27,6 +27,13 @@ int lcr_memcpy_dtod(void* dst, const void* src, size_t bytes);
 int lcr_device_memset(void* ptr, int value, size_t bytes);
 int lcr_device_synchronize(void);
 
+/* extension (measurement): reads `bytes` of device memory at `buf` (16-byte aligned, a multiple of
+ * 16 KiB) with the streaming 16-byte loads the decode kernels use, in `blocks` workgroups of 256
+ * threads, reps + 1 times on the default stream; *best_ms is the fastest of the last `reps`
+ * launches (hipEvents). bytes / *best_ms is the read rate the device sustains for this load form:
+ * the measured ceiling beside the published HBM peak. */
+int lcr_stream_read(const void* buf, size_t bytes, int blocks, int reps, float* best_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -211,6 +211,7 @@ SIGNATURES = {
     "lcr_memcpy_htod": (_I, [_P, _P, _SZ]),
     "lcr_memcpy_dtoh": (_I, [_P, _P, _SZ]),
     "lcr_memcpy_dtod": (_I, [_P, _P, _SZ]),
+    "lcr_stream_read": (_I, [_P, _SZ, _I, _I, ctypes.POINTER(ctypes.c_float)]),
     "lcr_device_memset": (_I, [_P, _I, _SZ]),
     "lcr_device_synchronize": (_I, []),
 }
@@ -449,6 +450,18 @@ def device_copy(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
     if nbytes > min(dst.nbytes, src.nbytes):
         raise LcrError(f"copy of {nbytes} bytes exceeds a buffer ({dst.nbytes}, {src.nbytes})")
     check(dst.lib, dst.lib.lcr_memcpy_dtod(dst.ptr, src.ptr, nbytes), "memcpy_dtod")
+
+
+def stream_read_gbs(nbytes: int = 1 << 30, blocks: int = 8192, reps: int = 10, variant: str = "bf16") -> float:
+    """Read rate (GB/s) of the library's streaming 16-byte loads over a fresh
+    device buffer of nbytes (lcr_stream_read: the fastest of `reps` launches)."""
+    buf = DeviceBuffer(nbytes, variant=variant)
+    try:
+        ms = ctypes.c_float()
+        check(buf.lib, buf.lib.lcr_stream_read(buf.ptr, nbytes, blocks, reps, ctypes.byref(ms)), "stream_read")
+        return nbytes / (ms.value * 1e-3) / 1e9
+    finally:
+        buf.free()
 
 
 class Model:

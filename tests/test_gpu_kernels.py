@@ -747,3 +747,21 @@ def test_argument_errors(gpu, lcr):
     assert lib.lcr_gemm_residual_rmsnorm_ws(None, None, None, None, None, None, 0, 2048, 2048, 1e-5, None, 0,
                                             NULL) == 0
     assert lib.lcr_rope_table(None, None, 0, 64, NULL) == 0
+
+
+def test_stream_read_probe(lcr):
+    """lcr_stream_read (the measured read ceiling of the bench line): a rate
+    in a plausible range for 1 GiB past the memory-side cache, and argument
+    checks that fail with a message rather than launching."""
+    gbs = lcr.stream_read_gbs(1 << 30, blocks=4096, reps=3)
+    assert 1000.0 < gbs < 12000.0, gbs
+    lib = lcr.load_library("bf16")
+    ms = ctypes.c_float()
+    buf = lcr.DeviceBuffer(1 << 20)
+    assert lib.lcr_stream_read(buf.ptr, (1 << 20) - 16, 64, 1, ctypes.byref(ms)) == -1
+    assert b"whole units" in lib.lcr_last_error_message()
+    assert lib.lcr_stream_read(buf.ptr + 8, 1 << 14, 64, 1, ctypes.byref(ms)) == -1
+    assert b"aligned" in lib.lcr_last_error_message()
+    assert lib.lcr_stream_read(buf.ptr, 1 << 20, 0, 1, ctypes.byref(ms)) == -1
+    assert lib.lcr_stream_read(buf.ptr, 1 << 20, 64, 1, ctypes.byref(ms)) == 0 and ms.value > 0
+    buf.free()

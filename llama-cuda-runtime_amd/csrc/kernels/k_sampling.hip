@@ -275,7 +275,8 @@ __device__ __forceinline__ void bitonic_keep(float& v, int& i, float pv, int pi,
 // values); the total from the partial sums in the 1024-thread tree of
 // block_sum_1024; the first kMaxCandidates candidates gathered from the
 // blocks' lists in block order; the sort with one element per thread
-// (exchanges between lanes of a wave by shuffles, between waves through LDS);
+// (exchanges between lanes of a wave by shuffles, between waves through LDS;
+// for top_k <= 64 only the best 64 are put in order);
 // the walk with every exponential computed beforehand, one per thread.
 // With `step` set (a device-resident generation loop), the uniform is
 // step.uniforms[*step.counter], and the id also becomes the next step's input
@@ -341,23 +342,57 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
     idx = cand_indices[at];
   }
 
-  // 5. Bitonic sort into (value desc, index asc), one element per thread.
-  for (int span = 2; span <= kMaxCandidates; span <<= 1) {
-    for (int step = span >> 1; step > 0; step >>= 1) {
-      float pv;
-      int pi;
-      if (step < 64) {
-        pv = __shfl_xor(v, step, 64);
-        pi = __shfl_xor(idx, step, 64);
-      } else {
-        values[t] = v;
-        indices[t] = idx;
-        __syncthreads();
-        pv = values[t ^ step];
-        pi = indices[t ^ step];
-        __syncthreads();
+  // 5. Order (value desc, index asc), one element per thread.
+  if (top_k > 0 && top_k <= 64) {
+    // The walk reads only the first top_k: the best 64 in order suffice. Each
+    // wave sorts its 64 (best at lane 0); then four levels merge the waves'
+    // lists in pairs, keeping the better 64 of each pair: for two lists in
+    // that order the better of A[l] and B[63 - l] is a bitonic sequence
+    // holding the pair's best 64, which steps 32 .. 1 of the sort put in
+    // order. The order is total (indices are distinct), so these 64 and
+    // their order are the full sort's first 64. Wave 0 ends with them.
+    for (int span = 2; span <= 64; span <<= 1) {
+      for (int step = span >> 1; step > 0; step >>= 1) {
+        bitonic_keep(v, idx, __shfl_xor(v, step, 64), __shfl_xor(idx, step, 64), lane, span, step);
       }
-      bitonic_keep(v, idx, pv, pi, t, span, step);
+    }
+    for (int lists = kSampleThreads / 64; lists > 1; lists >>= 1) {
+      values[t] = v;
+      indices[t] = idx;
+      __syncthreads();
+      if (wave < lists / 2) {
+        const int other = (wave + lists / 2) * 64 + 63 - lane;
+        const float ov = values[other];
+        const int oi = indices[other];
+        if (ranks_before(ov, oi, v, idx)) {
+          v = ov;
+          idx = oi;
+        }
+        for (int step = 32; step > 0; step >>= 1) {
+          bitonic_keep(v, idx, __shfl_xor(v, step, 64), __shfl_xor(idx, step, 64), lane, 64, step);
+        }
+      }
+      __syncthreads();
+    }
+  } else {
+    // Bitonic sort of all candidates.
+    for (int span = 2; span <= kMaxCandidates; span <<= 1) {
+      for (int step = span >> 1; step > 0; step >>= 1) {
+        float pv;
+        int pi;
+        if (step < 64) {
+          pv = __shfl_xor(v, step, 64);
+          pi = __shfl_xor(idx, step, 64);
+        } else {
+          values[t] = v;
+          indices[t] = idx;
+          __syncthreads();
+          pv = values[t ^ step];
+          pi = indices[t ^ step];
+          __syncthreads();
+        }
+        bitonic_keep(v, idx, pv, pi, t, span, step);
+      }
     }
   }
   values[t] = v;

@@ -661,7 +661,8 @@ def test_sampling_matches_oracle(gpu, orc, lcr):
         logits = (r.normal(0, 0.9 + 0.3 * (trial % 4), size=vocab)).astype(np.float32)
         if trial % 5 == 0:
             logits[r.integers(0, vocab, 8)] = logits.max()  # exact ties
-        for (T, k, pp) in [(0.8, 40, 0.95), (1.0, 0, 0.9), (0.5, 0, 1.0), (1.3, 5, 0.5), (0.0, 0, 1.0)]:
+        for (T, k, pp) in [(0.8, 40, 0.95), (1.0, 0, 0.9), (0.5, 0, 1.0), (1.3, 5, 0.5), (0.0, 0, 1.0),
+                           (0.7, 64, 1.0), (0.7, 65, 1.0)]:
             u = uniforms[(trial * 5) % 64]
             got = gpu_sample(lib, logits, T, k, pp, u)
             exp = oracle.sample(logits, T, k, pp, u)
@@ -682,7 +683,7 @@ def test_sampling_edges_match_oracle(gpu, orc, lcr):
     crowded[r.choice(128256, 5000, replace=False)] = np.float32(4.0) - r.random(5000).astype(np.float32) * 0.01
     cases.append(crowded)
     for n, logits in enumerate(cases):
-        for (T, k, pp) in [(0.8, 40, 0.95), (1.0, 0, 0.9), (1.0, 0, 1.0), (2.0, 3, 1.0)]:
+        for (T, k, pp) in [(0.8, 40, 0.95), (1.0, 0, 0.9), (1.0, 0, 1.0), (2.0, 3, 1.0), (3.0, 64, 1.0)]:
             u = uniforms[n % 32]
             got = gpu_sample(lib, logits, T, k, pp, u)
             exp = oracle.sample(logits, T, k, pp, u)

@@ -195,13 +195,15 @@ def prefill_flops(config: dict, T: int) -> float:
     return lin + attn
 
 
-def long_context(lcr, model_dir: Path, config: dict, ctx: int, steps: int = 64) -> dict:
+def long_context(lcr, model_dir: Path, config: dict, ctx: int, steps: int = 64, eager: bool = False) -> dict:
     """paged cache (16-token pages, seeded random
     page permutation) pre-filled with N(0, 1) at `ctx`, then `steps` greedy
-    decode steps on the graph; attention timed on its own as well."""
+    decode steps on the graph; attention timed on its own as well. With
+    `eager` the steps' kernels are launched directly (for profilers, which
+    do not trace graph replays here) and nothing is graph-timed."""
     import numpy as np
     layers = config["num_hidden_layers"]
-    m = lcr.Model(model_dir, max_seq=ctx + steps + 1, paged=1, page_size=16)
+    m = lcr.Model(model_dir, max_seq=ctx + steps + 1, paged=1, page_size=16, use_graph=0 if eager else 1)
     geo = m.kv_geometry()
     m.fill_kv_normal(20260904 + ctx, 1.0)
     tables = np.random.default_rng(ctx).permutation(layers * geo["max_pages"]).astype(np.int32)
@@ -210,6 +212,10 @@ def long_context(lcr, model_dir: Path, config: dict, ctx: int, steps: int = 64) 
     m.generate_greedy(1, 4)  # captures the graph for this split count
     m.set_position(ctx)
     _, ms = m.generate_greedy(1, steps)
+    if eager:
+        st = m.stats()
+        m.close()
+        return {"context": ctx, "decode_steps": steps, "launch": "eager", "ms_per_token": ms / steps}
     att_ms, att_bytes = m.time_decode_kernel("attention", 16)
     grid_ms, grid_bytes = m.time_decode_kernel("qkv_attention_oproj", 16)
     st = m.stats()
@@ -453,8 +459,8 @@ def main() -> int:
                     help="only the prefill and the timed graph-replayed decode steps, for a kernel trace "
                          "in which every decode kernel is an in-step dispatch")
     ap.add_argument("--eager", action="store_true",
-                    help="with --decode-only: enqueue each step's kernels directly instead of replaying the "
-                         "captured graph (the kernels and their order are the same)")
+                    help="with --decode-only or --long-context: enqueue each step's kernels directly instead of "
+                         "replaying the captured graph (the kernels and their order are the same)")
     ap.add_argument("--no-exchange", action="store_true",
                     help="run the decode step's q/k/v projection and attention as two kernels instead of "
                          "the exchange grid (for comparison)")
@@ -496,7 +502,8 @@ def main() -> int:
         print(json.dumps({"prefill_config4": prefill_run(lcr, model_dir, config, args.prefill)}))
         return 0
     if args.long_context > 0:
-        print(json.dumps({"long_context": long_context(lcr, model_dir, config, args.long_context)}))
+        print(json.dumps({"long_context": long_context(lcr, model_dir, config, args.long_context,
+                                                       eager=args.eager)}))
         return 0
     t0 = time.perf_counter()
     model = lcr.Model(model_dir, max_seq=args.max_seq, use_graph=0 if args.eager else 1,

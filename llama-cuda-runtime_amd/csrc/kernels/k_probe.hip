@@ -49,11 +49,19 @@ extern "C" int lcr_stream_read(const void* buf, size_t bytes, int blocks, int re
   CAPI_CHECK(reinterpret_cast<uintptr_t>(buf) % 16 == 0, "stream_read needs a 16-byte aligned buffer");
   CAPI_CHECK(blocks > 0 && reps > 0, "stream_read needs positive blocks and repetitions");
   return capi::guarded([&]() -> int {
-    uint32_t* sink = nullptr;
-    HIP_CHECK(hipMalloc(&sink, sizeof(uint32_t)));
-    hipEvent_t start = nullptr, stop = nullptr;
-    HIP_CHECK(hipEventCreate(&start));
-    HIP_CHECK(hipEventCreate(&stop));
+    // Released on every path out, including a failed HIP call (which throws).
+    struct Resources {
+      uint32_t* sink = nullptr;
+      hipEvent_t start = nullptr, stop = nullptr;
+      ~Resources() {
+        if (start != nullptr) (void)hipEventDestroy(start);
+        if (stop != nullptr) (void)hipEventDestroy(stop);
+        if (sink != nullptr) (void)hipFree(sink);
+      }
+    } res;
+    HIP_CHECK(hipMalloc(&res.sink, sizeof(uint32_t)));
+    HIP_CHECK(hipEventCreate(&res.start));
+    HIP_CHECK(hipEventCreate(&res.stop));
     const size_t units = bytes / kProbeUnit;
     const auto* p = static_cast<const vec16*>(buf);
     // A lane whose fold happens to equal this value stores 4 bytes to the
@@ -61,18 +69,15 @@ extern "C" int lcr_stream_read(const void* buf, size_t bytes, int blocks, int re
     const uint32_t never = 0x9e3779b9u;
     float best = 0.0f;
     for (int r = 0; r < reps + 1; ++r) {
-      HIP_CHECK(hipEventRecord(start, nullptr));
-      stream_read_kernel<<<blocks, kProbeThreads>>>(p, units, never, sink);
+      HIP_CHECK(hipEventRecord(res.start, nullptr));
+      stream_read_kernel<<<blocks, kProbeThreads>>>(p, units, never, res.sink);
       HIP_CHECK_LAUNCH();
-      HIP_CHECK(hipEventRecord(stop, nullptr));
-      HIP_CHECK(hipEventSynchronize(stop));
+      HIP_CHECK(hipEventRecord(res.stop, nullptr));
+      HIP_CHECK(hipEventSynchronize(res.stop));
       float ms = 0.0f;
-      HIP_CHECK(hipEventElapsedTime(&ms, start, stop));
+      HIP_CHECK(hipEventElapsedTime(&ms, res.start, res.stop));
       if (r > 0 && (best == 0.0f || ms < best)) best = ms;  // the first launch warms up
     }
-    (void)hipEventDestroy(start);
-    (void)hipEventDestroy(stop);
-    (void)hipFree(sink);
     *best_ms = best;
     return LCR_OK;
   });

@@ -1,6 +1,7 @@
-// The fused decode step: five kernels per layer plus the output head, every
-// one reading the position and token id from device memory so the whole step
-// can be captured once in a hipGraph and replayed.
+// The fused decode step: five kernels per layer (three where the device runs
+// q/k/v, attention and o_proj as one exchange grid, exchange.h) plus the
+// output head, every one reading the position and token id from device memory
+// so the whole step can be captured once in a hipGraph and replayed.
 //
 // The arithmetic is exactly that of the reference's unfused sequence
 // (src/model.cu:370-484): every bf16 rounding point of the reference is kept

@@ -4,7 +4,8 @@
 //
 // Decode is a weight stream: 2.47 GB of bf16 weights per token for
 // Llama-3.2-1B, each used for one multiply-add. The decode step therefore runs
-// as fused kernels (five per layer, see kernels/decode_step.h) captured once in
+// as fused kernels (three per layer with the exchange grid, see
+// kernels/decode_step.h) captured once in
 // a hipGraph per attention split count and replayed, with the token id and
 // position living in device memory so nothing has to be re-captured per token.
 // Prefill (more than one token) is compute bound and runs the projections as

@@ -130,3 +130,19 @@ def test_gemm_split_plans(lcr):
         splits, rem = divmod(b, T * N * 4)
         assert rem == 0 and splits in (2, 4, 8, 16), (T, N, K, b)
         assert K // splits >= 256
+
+
+@pytest.mark.parametrize("variant", ["bf16", "fp16"])
+def test_choose_attention_splits_export(lcr, variant):
+    """lcr_choose_attention_splits is host arithmetic (no device call): it
+    equals the hand-worked answers of src/kernels/attention.cu:419-431 and the
+    oracle over a grid."""
+    from test_oracle import SPLIT_KNOWN_ANSWERS
+    lib = lcr.load_library(variant)
+    for args, want in SPLIT_KNOWN_ANSWERS:
+        assert lib.lcr_choose_attention_splits(*args) == want, args
+    L = oracle.load()
+    for kv in (1, 2, 4, 8):
+        for cus in (1, 32, 256, 304):
+            for n in (1, 255, 256, 4096, 8192, 32768, 200000):
+                assert lib.lcr_choose_attention_splits(kv, n, cus) == L.orc_choose_attention_splits(kv, n, cus)

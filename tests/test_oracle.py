@@ -646,3 +646,83 @@ def test_sample_full_vocabulary_matches_float64_walk():
             assert oracle.sample(logits, T, k, p, float(u)) == want, (trial, sigma, k, u)
             checked += 1
     assert cases >= 12 and checked >= 80, (cases, checked)
+
+
+# ---------------------------------------------------------------------------
+# layout helpers: head merge, paged gather, split count
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tokens,heads,hd", [(5, 3, 64), (1, 32, 64), (7, 4, 24), (0, 4, 64)])
+def test_merge_heads_is_a_transpose(L, tokens, heads, hd):
+    """src/kernels/elementwise.cu:124-143: heads[h][t][:] -> out[t][h*hd:]. The
+    closed form is a numpy axis swap; tokens != heads catches a swapped pair of
+    strides, random bits catch a dropped or repeated element."""
+    r = rng(tokens * 100 + heads)
+    x = r.integers(0, 1 << 16, (heads, tokens, hd), dtype=np.uint16)
+    out = np.full(tokens * heads * hd + 8, 0xABCD, dtype=np.uint16)
+    L.orc_merge_heads(out.ctypes.data, x.ctypes.data, tokens, heads, hd)
+    assert np.array_equal(out[:tokens * heads * hd], np.transpose(x, (1, 0, 2)).ravel())
+    assert np.all(out[tokens * heads * hd:] == 0xABCD)  # nothing past the end is written
+
+
+@pytest.mark.parametrize("positions", [1, 15, 16, 77, 96])
+def test_gather_kv_reads_through_the_page_table(L, positions):
+    """src/kernels/attention.cu:302-316: out[h][p] = pool[table[p / 16]][h][p % 16]
+    for a pool laid out [page][kv head][16 slots][hd] (src/kv_cache.cu:112-124).
+    The expected rows come from numpy fancy indexing over that 4-d shape, not
+    from kv_offset; the page table is a permutation with spare pages so that
+    reading page p instead of table[p] fails."""
+    kv, hd, ps = 8, 64, 16
+    pages = 9
+    r = rng(positions)
+    pool_k = r.integers(0, 1 << 16, (pages, kv, ps, hd), dtype=np.uint16)
+    pool_v = r.integers(0, 1 << 16, (pages, kv, ps, hd), dtype=np.uint16)
+    table = r.permutation(pages).astype(np.int32)
+    view = oracle_view(pool_k, pool_v, table, ps, kv * ps * hd, ps * hd, kv, hd)
+    out_k = np.zeros((kv, positions, hd), dtype=np.uint16)
+    out_v = np.zeros((kv, positions, hd), dtype=np.uint16)
+    L.orc_gather_kv(out_k.ctypes.data, out_v.ctypes.data, ctypes.byref(view), positions)
+    pos = np.arange(positions)
+    want_k = pool_k[table[pos // ps], :, pos % ps, :].transpose(1, 0, 2)
+    want_v = pool_v[table[pos // ps], :, pos % ps, :].transpose(1, 0, 2)
+    assert np.array_equal(out_k, want_k)
+    assert np.array_equal(out_v, want_v)
+
+
+SPLIT_KNOWN_ANSWERS = [
+    # (kv heads, positions, CUs) -> splits, worked by hand from
+    # src/kernels/attention.cu:419-431: ceil(2*CUs / kv), capped by
+    # max(1, positions / 256) and by 64, never below 1.
+    ((8, 200, 256), 1),      # 200 / 256 = 0 useful splits -> 1
+    ((8, 2048, 256), 8),     # 64 wanted, 8 useful
+    ((8, 32768, 256), 64),   # 64 wanted, 128 useful
+    ((8, 32768, 20), 5),     # ceil(40 / 8) = 5
+    ((8, 8192, 256), 32),    # 64 wanted, 32 useful
+    ((1, 100000, 256), 64),  # 512 wanted, capped at 64
+    ((3, 4096, 10), 7),      # ceil(20 / 3) = 7, 16 useful
+    ((8, 255, 1), 1),
+    ((8, 512, 1), 1),        # ceil(2 / 8) = 1
+    ((2, 1024, 4), 4),       # ceil(8 / 2) = 4, 4 useful
+    ((2, 1023, 4), 3),       # 3 useful
+]
+
+
+@pytest.mark.parametrize("args,want", SPLIT_KNOWN_ANSWERS)
+def test_choose_attention_splits_known_answers(L, args, want):
+    assert L.orc_choose_attention_splits(*args) == want
+
+
+def test_choose_attention_splits_invariants(L):
+    """Over a grid: 1 <= splits <= 64; every split keeps >= 256 positions once
+    the context has 256; more CUs or more positions never lower the count."""
+    for kv in (1, 2, 4, 8, 16):
+        for cus in (1, 20, 80, 256, 304):
+            prev = 0
+            for n in (1, 100, 255, 256, 511, 512, 2048, 8191, 8192, 32768, 131072):
+                s = L.orc_choose_attention_splits(kv, n, cus)
+                assert 1 <= s <= 64
+                if n >= 256:
+                    assert n // s >= 256
+                assert s >= prev
+                prev = s
+                assert L.orc_choose_attention_splits(kv, n, cus + 1) >= s

@@ -65,7 +65,8 @@ struct DecodeStepArgs {
   bool paged;
   int splits;
   int compute_units;         // of the device: sizes the output head's grid
-  // In-grid exchange (exchange.h): when set and splits == 1, the q/k/v
+  // In-grid exchange (exchange.h), over the words at `exchange` (null: no
+  // exchange grid runs). With exchange_single and splits == 1, the q/k/v
   // projection and the attention run as one grid (with exchange_oproj, the
   // o_proj projection too); with exchange_split and splits > 1, the q/k/v
   // projection and the split attention run as one grid, and (with
@@ -73,10 +74,11 @@ struct DecodeStepArgs {
   // exchange_*_word() below; as many again after the written ones are never
   // written (tests of the give-up path read there).
   unsigned long long* exchange;
+  bool exchange_single;
   bool exchange_oproj;
   bool exchange_split;
   int exchange_slots;        // blocks of the split grid the device holds at once
-  int* exchange_status;      // [1] raised by a wait that gave up
+  int* exchange_status;      // [1] raised by a wait that gave up (host-coherent memory)
   int exchange_spins;        // polls before a wait gives up
   int exchange_read_offset;  // added to every word the grid reads (0; 3.5X in tests of the give-up path)
   uint32_t* epoch;           // [1] steps completed; advanced by the step's last kernel

@@ -733,7 +733,8 @@ template <int NCH, int NCH_F, int HD, bool kPaged, int G>
 void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, const KvCacheView& view,
                          int layer, hipStream_t s, unsigned mask, int tag_slot) {
   const int qkv_rows = (a.num_heads + 2 * a.num_kv_heads) * HD;
-  if (a.exchange != nullptr && a.splits == 1 && (mask & kDecodeQkv) && (mask & kDecodeAttention)) {
+  if (a.exchange != nullptr && a.exchange_single && a.splits == 1 && (mask & kDecodeQkv) &&
+      (mask & kDecodeAttention)) {
     const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
     const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
     if (a.exchange_oproj && (mask & kDecodeOProj)) {
@@ -912,7 +913,10 @@ void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
                           const KvCacheView& view, int layer, hipStream_t s, unsigned mask, int tag_slot) {
   const int g = a.num_heads / a.num_kv_heads;
   if (tag_slot < 0) tag_slot = layer;
-  LCR_CHECK(tag_slot < kExchangeTagSlots, "exchange tag slot " << tag_slot << " out of range");
+  // Only the exchange grids tag words with the slot.
+  if (a.exchange != nullptr && (mask & kDecodeQkv) && (mask & kDecodeAttention)) {
+    LCR_CHECK(tag_slot < kExchangeTagSlots, "exchange tag slot " << tag_slot << " out of range");
+  }
 #define LCR_LAYER_CASE(G_)                                                                \
   case G_:                                                                                \
     if (a.paged) {                                                                        \

@@ -43,11 +43,16 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
   HIP_CHECK(hipMemcpy(inv_freq_, inv_freq.data(), inv_freq.size() * sizeof(float),
                       hipMemcpyHostToDevice));
 
-  allocate_arena();
   HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&pinned_state_), 2 * sizeof(int32_t),
                           hipHostMallocDefault));
   pinned_state_[0] = 0;
   pinned_state_[1] = 0;
+  // Before the arena: allocating it clears the exchange state, status included.
+  HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&exchange_status_host_), sizeof(int),
+                          hipHostMallocCoherent | hipHostMallocMapped));
+  *exchange_status_host_ = 0;
+  HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&exchange_status_), exchange_status_host_, 0));
+  allocate_arena();
 
   fused_ = options_.fused_decode &&
            decode_step_supported(config_.hidden_size, config_.intermediate_size,
@@ -82,11 +87,13 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
 }
 
 Model::~Model() {
-  for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
-  for (auto& kv : sampled_graphs_) (void)hipGraphExecDestroy(kv.second);
-  graphs_.clear();
   if (stream_ != nullptr) (void)hipStreamSynchronize(stream_);
+  for (auto& kv : graphs_) destroy_captured(kv.second);
+  for (auto& kv : sampled_graphs_) destroy_captured(kv.second);
+  graphs_.clear();
+  sampled_graphs_.clear();
   if (pinned_state_ != nullptr) (void)hipHostFree(pinned_state_);
+  if (exchange_status_host_ != nullptr) (void)hipHostFree(exchange_status_host_);
   if (stream_ != nullptr) (void)hipStreamDestroy(stream_);
   (void)hipFree(weight_block_);
   (void)hipFree(inv_freq_);
@@ -217,7 +224,6 @@ void Model::allocate_arena() {
       static_cast<size_t>(options_.max_seq) * sizeof(float),          // uniforms_
       sizeof(int32_t),                                                // draw_counter_
       decode_exchange_words(config_.num_heads, config_.head_dim) * sizeof(unsigned long long),  // exchange_words_
-      sizeof(int),                                                    // exchange_status_
       sizeof(uint32_t),                                               // epoch_
   };
   size_t total = 0;
@@ -244,7 +250,6 @@ void Model::allocate_arena() {
   uniforms_ = arena_.alloc<float>(static_cast<size_t>(options_.max_seq));
   draw_counter_ = arena_.alloc<int32_t>(1);
   exchange_words_ = arena_.alloc<unsigned long long>(decode_exchange_words(config_.num_heads, config_.head_dim));
-  exchange_status_ = arena_.alloc<int>(1);
   epoch_ = arena_.alloc<uint32_t>(1);
   HIP_CHECK(hipMemset(epoch_, 0, sizeof(uint32_t)));
   clear_exchange();
@@ -372,7 +377,8 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.paged = options_.kv_layout == KvLayout::kPaged;
   a.splits = splits;
   a.compute_units = multiprocessors_;
-  a.exchange = (exchange_enabled_ || exchange_split_slots_ > 0) ? exchange_words_ : nullptr;
+  a.exchange = exchange_in_use() ? exchange_words_ : nullptr;
+  a.exchange_single = exchange_enabled_;
   a.exchange_oproj = exchange_oproj_;
   a.exchange_split = exchange_split_slots_ > 0;
   a.exchange_slots = exchange_split_slots_;
@@ -386,10 +392,14 @@ DecodeStepArgs Model::step_args(int splits) const {
 }
 
 int Model::exchange_status() const {
-  int status = 0;
   HIP_CHECK(hipStreamSynchronize(stream_));
-  HIP_CHECK(hipMemcpy(&status, exchange_status_, sizeof(int), hipMemcpyDeviceToHost));
-  return status;
+  return __atomic_load_n(exchange_status_host_, __ATOMIC_ACQUIRE);
+}
+
+void Model::check_exchange() {
+  if (!exchange_in_use() || __atomic_load_n(exchange_status_host_, __ATOMIC_ACQUIRE) == 0) return;
+  clear_exchange();
+  LCR_FAIL("a decode step's in-grid exchange wait gave up; its results are not valid");
 }
 
 void Model::advance_epoch() {
@@ -404,8 +414,36 @@ void Model::clear_exchange() {
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipMemset(exchange_words_, 0,
                       decode_exchange_words(config_.num_heads, config_.head_dim) * sizeof(unsigned long long)));
-  HIP_CHECK(hipMemset(exchange_status_, 0, sizeof(int)));
   HIP_CHECK(hipDeviceSynchronize());
+  __atomic_store_n(exchange_status_host_, 0, __ATOMIC_RELEASE);
+}
+
+void Model::destroy_captured(CapturedStep& c) {
+  if (c.exec != nullptr) (void)hipGraphExecDestroy(c.exec);
+  if (c.graph != nullptr) (void)hipGraphDestroy(c.graph);
+  c.exec = nullptr;
+  c.graph = nullptr;
+}
+
+template <typename Enqueue>
+Model::CapturedStep Model::capture_step(Enqueue enqueue) {
+  CapturedStep c;
+  HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+  try {
+    enqueue();
+  } catch (...) {
+    hipGraph_t discard = nullptr;
+    (void)hipStreamEndCapture(stream_, &discard);
+    if (discard != nullptr) (void)hipGraphDestroy(discard);
+    throw;
+  }
+  HIP_CHECK(hipStreamEndCapture(stream_, &c.graph));
+  const hipError_t status = hipGraphInstantiate(&c.exec, c.graph, nullptr, nullptr, 0);
+  if (status != hipSuccess) {
+    destroy_captured(c);
+    HIP_CHECK(status);
+  }
+  return c;
 }
 
 void Model::launch_fused_step(int seq_len) {
@@ -425,25 +463,8 @@ void Model::launch_fused_step(int seq_len) {
     return;
   }
   auto it = graphs_.find(splits);
-  if (it == graphs_.end()) {
-    hipGraph_t graph = nullptr;
-    HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-    try {
-      enqueue();
-    } catch (...) {
-      hipGraph_t discard = nullptr;
-      (void)hipStreamEndCapture(stream_, &discard);
-      if (discard != nullptr) (void)hipGraphDestroy(discard);
-      throw;
-    }
-    HIP_CHECK(hipStreamEndCapture(stream_, &graph));
-    hipGraphExec_t exec = nullptr;
-    const hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    HIP_CHECK(status);
-    it = graphs_.emplace(splits, exec).first;
-  }
-  HIP_CHECK(hipGraphLaunch(it->second, stream_));
+  if (it == graphs_.end()) it = graphs_.emplace(splits, capture_step(enqueue)).first;
+  HIP_CHECK(hipGraphLaunch(it->second.exec, stream_));
 }
 
 const float* Model::decode(int token) {
@@ -468,12 +489,13 @@ const float* Model::decode(int token) {
   timer.stop(stream_);
   HIP_CHECK(hipStreamSynchronize(stream_));
   stats_.last_decode_ms = timer.elapsed_ms();
+  check_exchange();
   if (profiler_.enabled()) profiler_.collect();
   return logits_;
 }
 
 void Model::clear_sampled_graphs() {
-  for (auto& kv : sampled_graphs_) (void)hipGraphExecDestroy(kv.second);
+  for (auto& kv : sampled_graphs_) destroy_captured(kv.second);
   sampled_graphs_.clear();
 }
 
@@ -498,25 +520,8 @@ void Model::launch_sampled_step(int seq_len) {
     return;
   }
   auto it = sampled_graphs_.find(splits);
-  if (it == sampled_graphs_.end()) {
-    hipGraph_t graph = nullptr;
-    HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-    try {
-      enqueue();
-    } catch (...) {
-      hipGraph_t discard = nullptr;
-      (void)hipStreamEndCapture(stream_, &discard);
-      if (discard != nullptr) (void)hipGraphDestroy(discard);
-      throw;
-    }
-    HIP_CHECK(hipStreamEndCapture(stream_, &graph));
-    hipGraphExec_t exec = nullptr;
-    const hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    HIP_CHECK(status);
-    it = sampled_graphs_.emplace(splits, exec).first;
-  }
-  HIP_CHECK(hipGraphLaunch(it->second, stream_));
+  if (it == sampled_graphs_.end()) it = sampled_graphs_.emplace(splits, capture_step(enqueue)).first;
+  HIP_CHECK(hipGraphLaunch(it->second.exec, stream_));
 }
 
 std::vector<int> Model::generate_sampled(int first_token, int steps, float temperature, int top_k,
@@ -569,10 +574,7 @@ std::vector<int> Model::generate_sampled(int first_token, int steps, float tempe
   position_ = start + steps;
   std::vector<int32_t> ids(static_cast<size_t>(steps));
   HIP_CHECK(hipMemcpy(ids.data(), history_ + start + 1, ids.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
-  if (exchange_enabled_ && exchange_status() != 0) {
-    clear_exchange();
-    LCR_FAIL("a decode step's in-grid exchange wait gave up; its results are not valid");
-  }
+  check_exchange();
   for (int s = 0; s < steps; ++s) {
     LCR_CHECK(ids[static_cast<size_t>(s)] >= 0 && ids[static_cast<size_t>(s)] < config_.vocab_size,
               "sampling produced token id " << ids[static_cast<size_t>(s)] << ", outside the vocabulary");
@@ -618,10 +620,7 @@ std::vector<int> Model::generate_greedy(int first_token, int steps, double* elap
   std::vector<int32_t> ids(static_cast<size_t>(steps));
   HIP_CHECK(hipMemcpy(ids.data(), history_ + start + 1, static_cast<size_t>(steps) * sizeof(int32_t),
                       hipMemcpyDeviceToHost));
-  if (exchange_enabled_ && exchange_status() != 0) {
-    clear_exchange();
-    LCR_FAIL("a decode step's in-grid exchange wait gave up; its results are not valid");
-  }
+  check_exchange();
   for (int s = 0; s < steps; ++s) out[static_cast<size_t>(s)] = ids[static_cast<size_t>(s)];
   return out;
 }
@@ -673,6 +672,11 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
     LCR_FAIL("unknown decode kernel \"" << kernel << "\"");
   }
   if (bytes_per_launch) *bytes_per_launch = bytes;
+  // Each launch of an exchange grid tags its broadcast words with its own
+  // slot of the epoch, so one timing graph holds at most that many.
+  const bool exchange_grid = exchange_in_use() && (mask & kDecodeQkv) && (mask & kDecodeAttention);
+  LCR_CHECK(!exchange_grid || launches <= kExchangeTagSlots,
+            "timing an exchange grid takes at most " << kExchangeTagSlots << " launches, got " << launches);
   pinned_state_[1] = position_ - 1;  // the step that produced the current cache length
   HIP_CHECK(hipMemcpyAsync(position_dev_, &pinned_state_[1], sizeof(int32_t), hipMemcpyHostToDevice,
                            stream_));
@@ -696,37 +700,34 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
       }
     }
   };
-  hipGraph_t graph = nullptr;
-  HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+  CapturedStep timing = capture_step(enqueue);
+  hipEvent_t start = nullptr, stop = nullptr;
+  float ms = 0.0f;
   try {
-    enqueue();
+    HIP_CHECK(hipEventCreate(&start));
+    HIP_CHECK(hipEventCreate(&stop));
+    HIP_CHECK(hipGraphLaunch(timing.exec, stream_));  // warm-up replay
+    // A new epoch for the timed replay, so no exchange word of the warm-up
+    // replay passes for one of its own, and another after it, so none of the
+    // timed replay's words passes for one of the next decode step (whose
+    // launches use the same slots, one per layer).
+    advance_epoch();
+    HIP_CHECK(hipEventRecord(start, stream_));
+    HIP_CHECK(hipGraphLaunch(timing.exec, stream_));
+    HIP_CHECK(hipEventRecord(stop, stream_));
+    HIP_CHECK(hipEventSynchronize(stop));
+    HIP_CHECK(hipEventElapsedTime(&ms, start, stop));
+    advance_epoch();
+    check_exchange();
   } catch (...) {
-    hipGraph_t discard = nullptr;
-    (void)hipStreamEndCapture(stream_, &discard);
-    if (discard != nullptr) (void)hipGraphDestroy(discard);
+    if (start != nullptr) (void)hipEventDestroy(start);
+    if (stop != nullptr) (void)hipEventDestroy(stop);
+    destroy_captured(timing);
     throw;
   }
-  HIP_CHECK(hipStreamEndCapture(stream_, &graph));
-  hipGraphExec_t exec = nullptr;
-  const hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  (void)hipGraphDestroy(graph);
-  HIP_CHECK(status);
-  hipEvent_t start = nullptr, stop = nullptr;
-  HIP_CHECK(hipEventCreate(&start));
-  HIP_CHECK(hipEventCreate(&stop));
-  HIP_CHECK(hipGraphLaunch(exec, stream_));  // warm-up replay
-  // A new epoch for the timed replay, so no exchange word of the warm-up
-  // replay passes for one of its own.
-  advance_epoch();
-  HIP_CHECK(hipEventRecord(start, stream_));
-  HIP_CHECK(hipGraphLaunch(exec, stream_));
-  HIP_CHECK(hipEventRecord(stop, stream_));
-  HIP_CHECK(hipEventSynchronize(stop));
-  float ms = 0.0f;
-  HIP_CHECK(hipEventElapsedTime(&ms, start, stop));
   (void)hipEventDestroy(start);
   (void)hipEventDestroy(stop);
-  (void)hipGraphExecDestroy(exec);
+  destroy_captured(timing);
   return static_cast<double>(ms) / launches;
 }
 

@@ -151,7 +151,8 @@ class Model {
   // Whether the decode step runs q/k/v and attention as one exchange grid.
   bool decode_exchange() const { return exchange_enabled_; }
   // Non-zero when an exchange wait of a past step gave up (its results are
-  // then not to be trusted); reading it synchronizes the stream.
+  // then not to be trusted); reading it synchronizes the stream. decode(),
+  // prefill() and the generate_* loops check it themselves and throw.
   int exchange_status() const;
   // Clears the exchange words and the status (after a wait gave up).
   void clear_exchange();
@@ -213,17 +214,36 @@ class Model {
   unsigned long long* argmax_partials_ = nullptr;
   int32_t* history_ = nullptr;    // [max_seq + 1]
   unsigned long long* exchange_words_ = nullptr;  // decode_exchange_words(...)
-  int* exchange_status_ = nullptr;
+  // Raised by an exchange wait that gave up. Host-coherent pinned memory the
+  // kernels write directly, so the host reads it after the synchronization
+  // every step ends with, at no cost to the device.
+  int* exchange_status_ = nullptr;       // device address of exchange_status_host_
+  int* exchange_status_host_ = nullptr;
+  // Whether any exchange grid can run (its waits then need checking).
+  bool exchange_in_use() const { return exchange_enabled_ || exchange_split_slots_ > 0; }
+  // After a synchronization: throws lcr::Error, clearing the words and the
+  // status, when a wait of the steps since the last check gave up.
+  void check_exchange();
   bool exchange_enabled_ = false;
   bool exchange_oproj_ = false;
   int exchange_split_slots_ = 0;  // 0: split attention keeps separate kernels
   uint32_t* epoch_ = nullptr;     // [1] decode steps completed (exchange tags)
   int32_t* pinned_state_ = nullptr;  // host {token, position}
 
-  std::map<int, hipGraphExec_t> graphs_;  // by split count
+  // A captured graph and its executable, destroyed together: the graph is
+  // kept for as long as the executable made from it.
+  struct CapturedStep {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+  };
+  static void destroy_captured(CapturedStep& c);
+  // Captures what `enqueue` launches on the stream and instantiates it.
+  template <typename Enqueue>
+  CapturedStep capture_step(Enqueue enqueue);
+  std::map<int, CapturedStep> graphs_;  // by split count
   // Sampled steps' graphs, by split count, for the parameters in
   // sampled_params_ (other parameters capture them again).
-  std::map<int, hipGraphExec_t> sampled_graphs_;
+  std::map<int, CapturedStep> sampled_graphs_;
   struct SampledParams {
     float temperature = 0.0f;
     int top_k = 0;

@@ -12,9 +12,10 @@ and the o_proj blocks the attention output from tagged broadcast words.
     q/k/v rows than one grid of one block per compute unit holds, and keep
     the two-kernel step);
   - a wait that finds no writer gives up after its poll limit, raises the
-    status (generate_greedy then fails with a message), and leaves no wave
-    spinning: the failure is forced from the host by pointing the waits at
-    words no block writes, so every kernel still exits normally.
+    status (decode(), prefill() and generate_greedy then fail with a message,
+    as the reference's decode returns valid logits or throws), and leaves no
+    wave spinning: the failure is forced from the host by pointing the waits
+    at words no block writes, so every kernel still exits normally.
 """
 
 import numpy as np
@@ -88,7 +89,17 @@ def test_exchange_group_sizes(lcr, tmp_path_factory, kv_heads, paged):
     # block plus one block per query head must fit (groups of 4 and 8 do on
     # 256 compute units; groups of 1 and 2 keep the two-kernel step).
     blocks = (32 + 2 * kv_heads) * 64 // 16 + 32
-    assert m.exchange_status() == (2 if blocks <= m.stats().multiprocessors else 0, 0)
+    fits = blocks <= m.stats().multiprocessors
+    assert m.exchange_status() == (2 if fits else 0, 0)
+    if not fits:
+        # The one-split grid must not run where it does not fit: with its waits
+        # pointed at words no block writes, a step that ran it would fail.
+        probe = lcr.Model(ckpt, max_seq=64, paged=int(paged), prefill_via_decode=1, exchange_spins=4,
+                          exchange_test_unwritten=1)
+        probe.prefill(lcr.synthetic_tokens(3, m.vocab, seed=1))
+        probe.decode(1)
+        assert probe.exchange_status() == (0, 0)
+        probe.close()
     o = oracle.OracleModel(ckpt, max_seq=256, paged=paged, multiprocessors=m.stats().multiprocessors)
     prompt = lcr.synthetic_tokens(70, m.vocab, seed=kv_heads)
     got = greedy_logits(m, prompt, 3)
@@ -115,23 +126,51 @@ def test_exchange_generate_greedy_matches_oracle(lcr, small_ckpt):
     assert m.exchange_status() == (2, 0)
 
 
+@pytest.mark.parametrize("graph", [1, 0])
 @pytest.mark.parametrize("oproj", [1, 0])
-def test_exchange_wait_gives_up(lcr, small_ckpt, oproj):
+def test_exchange_wait_gives_up(lcr, small_ckpt, oproj, graph):
     """Waits pointed at words no block writes: each gives up after four polls
-    and raises the status; the steps still finish (their logits are not
-    valid), generate_greedy reports the failure, and clearing resets the
-    status."""
-    m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=1, exchange_spins=4, exchange_test_unwritten=1,
-                  exchange_oproj=oproj)
+    and raises the status; the steps still finish, and every entry point that
+    returns their results fails instead: decode(), prefill() through the
+    decode step (a prompt under 64 tokens, and prefill_via_decode) and
+    generate_greedy. Each failure clears the words and the status."""
     grid = 2 if oproj else 1
-    prompt = lcr.synthetic_tokens(5, m.vocab, seed=3)
-    m.prefill(prompt)
-    assert m.exchange_status() == (grid, 1)
-    m.exchange_clear()
-    assert m.exchange_status() == (grid, 0)
-    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
-        m.generate_greedy(1, 4)
-    assert m.exchange_status() == (grid, 0)  # the failure cleared it
+    for via_decode in (1, 0):
+        m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=via_decode, exchange_spins=4,
+                      exchange_test_unwritten=1, exchange_oproj=oproj, use_graph=graph)
+        prompt = lcr.synthetic_tokens(5, m.vocab, seed=3)
+        with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+            m.prefill(prompt)
+        assert m.exchange_status() == (grid, 0)  # the failure cleared it
+        with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+            m.decode(1)
+        assert m.exchange_status() == (grid, 0)
+        with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+            m.generate_greedy(1, 4)
+        assert m.exchange_status() == (grid, 0)
+        m.close()
+
+
+def test_exchange_decode_after_short_timing_graph(lcr, small_ckpt):
+    """A timing graph with no more launches than the model has layers, then a
+    new prompt: the next steps' o_proj blocks must wait for their own
+    attention output, not take the timed replay's words (which carry the
+    same slots), so the logits equal the oracle's."""
+    m = lcr.Model(small_ckpt, max_seq=256, prefill_via_decode=1)
+    o = oracle.OracleModel(small_ckpt, max_seq=256, multiprocessors=m.stats().multiprocessors)
+    m.prefill(lcr.synthetic_tokens(30, m.vocab, seed=12))
+    for name in ("qkv_attention_oproj", "qkv_attention"):
+        for launches in (1, 2):
+            m.time_decode_kernel(name, launches)
+    m.reset()
+    prompt = lcr.synthetic_tokens(7, m.vocab, seed=13)
+    got = greedy_logits(m, prompt, 3)
+    want = [o.prefill(prompt, use_decode_path=True)]
+    for _ in range(3):
+        want.append(o.decode(oracle.argmax(want[-1])))
+    for s, (g, e) in enumerate(zip(got, want)):
+        expect_bits_equal(g.view(np.uint32), e.view(np.uint32), f"step {s} after a short timing graph")
+    assert m.exchange_status() == (2, 0)
 
 
 def test_exchange_kernel_timing_waits_for_its_own_launch(lcr, small_ckpt):
@@ -190,10 +229,23 @@ def test_split_exchange_grids_match_oracle(lcr, small_ckpt, paged, splits):
 
 def test_split_exchange_wait_gives_up(lcr, small_ckpt):
     """The split grids' waits pointed at words no block writes give up and
-    raise the status; every kernel still exits."""
+    raise the status; every kernel still exits, and decode() fails. With at
+    most 8 forced splits a step at position p runs min(8, p + 1) splits; the
+    split grids need a block per (query head, split), at least one per
+    16-row q/k/v block (192 for this geometry), so they run from 6 splits on;
+    fewer splits run the separate kernels, which wait on nothing; position 0
+    runs the one-split grid."""
     m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=1, attention_splits=8, exchange_spins=4,
                   exchange_test_unwritten=1)
-    m.prefill(lcr.synthetic_tokens(5, m.vocab, seed=4))
-    assert m.exchange_status()[1] == 1
-    m.exchange_clear()
+    heads, qkv_blocks = 32, (32 + 2 * 8) * 64 // 16
+    first_split_grid = next(p for p in range(1, 8) if heads * m.decode_splits(p + 1) >= qkv_blocks)
+    assert first_split_grid == 5
+    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+        m.prefill([3])
+    assert m.exchange_status()[1] == 0
+    while m.position < first_split_grid:
+        m.decode(2)
+    assert m.exchange_status()[1] == 0
+    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+        m.decode(2)
     assert m.exchange_status()[1] == 0

@@ -6,7 +6,7 @@ Two variants, as the reference's LCR_DTYPE switch gives two builds
   liblcr_amd_fp16.so  fp16 elements (-DLCR_ELEM_FP16)
 
 The command-line programs of csrc/tools/ (llama-run, lcr-validate,
-lcr-inspect, lcr-tokenize) are linked against those libraries into bin/.
+lcr-inspect) are linked against those libraries into bin/.
 
 Every source is compiled with hipcc for gfx950 only, with -ffp-contract=off so
 that only the explicit fma calls in the kernels are fused (the kernels'
@@ -109,7 +109,6 @@ TOOLS = {
     "llama-run-fp16": ("run_main.cpp", "fp16"),
     "lcr-validate": ("validate_main.cpp", "bf16"),
     "lcr-inspect": ("inspect_main.cpp", "bf16"),
-    "lcr-tokenize": ("tokenize_main.cpp", "bf16"),
 }
 
 

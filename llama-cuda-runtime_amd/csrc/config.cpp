@@ -1,8 +1,17 @@
+// config.json is read against a schema: a table row per key this runtime
+// understands, naming the ModelConfig member it fills, whether the key must be
+// there, and which values are refused. The reader walks the tables once;
+// derived defaults (kv heads, head_dim) and the cross-field rules of
+// validate() run after. The keys, their meanings and the refusal messages
+// follow the reference (src/config.cpp:36-221; its tests match the message
+// substrings), the structure is this file's own.
 #include "config.h"
 
 #include <algorithm>
 #include <cmath>
 #include <fstream>
+#include <functional>
+#include <iterator>
 #include <sstream>
 
 #include "json.h"
@@ -10,210 +19,332 @@
 namespace lcr {
 namespace {
 
-std::string path_join(const std::string& dir, const std::string& name) {
+using json::Value;
+
+// ---------------------------------------------------------------------------
+// Schema tables
+// ---------------------------------------------------------------------------
+
+// An integer key. Required keys must be numbers; optional ones are taken when
+// they are numbers and otherwise leave the member at its sentinel (0) for the
+// derived-default pass.
+struct IntKey {
+  const char* key;
+  int ModelConfig::*member;
+  bool required;
+};
+
+constexpr IntKey kIntKeys[] = {
+    {"hidden_size", &ModelConfig::hidden_size, true},
+    {"intermediate_size", &ModelConfig::intermediate_size, true},
+    {"num_hidden_layers", &ModelConfig::num_layers, true},
+    {"num_attention_heads", &ModelConfig::num_heads, true},
+    {"vocab_size", &ModelConfig::vocab_size, true},
+    {"max_position_embeddings", &ModelConfig::max_position_embeddings, true},
+    {"num_key_value_heads", &ModelConfig::num_kv_heads, false},  // absent: multi-head attention
+    {"head_dim", &ModelConfig::head_dim, false},                  // absent: hidden / heads
+};
+
+// Optional real and boolean keys over the member's default.
+struct RealKey {
+  const char* key;
+  float ModelConfig::*member;
+};
+constexpr RealKey kRealKeys[] = {
+    {"rms_norm_eps", &ModelConfig::rms_norm_eps},
+    {"rope_theta", &ModelConfig::rope_theta},
+};
+
+struct FlagKey {
+  const char* key;
+  bool ModelConfig::*member;
+};
+constexpr FlagKey kFlagKeys[] = {
+    {"tie_word_embeddings", &ModelConfig::tie_word_embeddings},
+};
+
+// String keys whose only accepted value is `accepted` (when present). The
+// message is completed with the value found and a closing quote.
+struct OnlyValue {
+  const char* key;
+  const char* accepted;
+  const char* refusal;
+};
+constexpr OnlyValue kOnlyValues[] = {
+    {"model_type", "llama",
+     "this runtime only implements the Llama architecture, config.json says model_type=\""},
+    {"hidden_act", "silu", "only the SiLU/SwiGLU MLP is implemented, config.json says \""},
+};
+
+// Boolean features this runtime does not implement: refused when true.
+struct Unsupported {
+  const char* key;
+  const char* refusal;
+};
+constexpr Unsupported kUnsupported[] = {
+    {"attention_bias", "attention projections with bias are not implemented"},
+    {"mlp_bias", "MLP projections with bias are not implemented"},
+};
+
+// The llama3 rope_scaling block's numbers, over RopeScaling's defaults.
+struct RopeRealKey {
+  const char* key;
+  float RopeScaling::*member;
+};
+constexpr RopeRealKey kRopeRealKeys[] = {
+    {"factor", &RopeScaling::factor},
+    {"low_freq_factor", &RopeScaling::low_freq_factor},
+    {"high_freq_factor", &RopeScaling::high_freq_factor},
+};
+
+// ---------------------------------------------------------------------------
+// Readers
+// ---------------------------------------------------------------------------
+
+const Value* number_at(const Value& obj, const char* key) {
+  const Value* v = obj.find(key);
+  return (v != nullptr && v->is_number()) ? v : nullptr;
+}
+
+// Token ids: one integer (older checkpoints) or a list of them (Llama 3.x
+// stops on several). Anything else contributes nothing.
+std::vector<int> token_list(const Value* node) {
+  std::vector<int> ids;
+  if (node == nullptr) return ids;
+  if (node->is_integer()) {
+    ids.push_back(node->as_int());
+  } else if (node->is_array()) {
+    for (const Value& item : node->items()) {
+      if (item.is_integer()) ids.push_back(item.as_int());
+    }
+  }
+  return ids;
+}
+
+// The scaling scheme a rope_scaling block names ("rope_type" in current
+// checkpoints, "type" in older ones); "default" when it names none.
+std::string rope_scheme(const Value& block) {
+  for (const char* key : {"rope_type", "type"}) {
+    const Value* v = block.find(key);
+    if (v != nullptr && v->is_string()) return v->as_string();
+  }
+  return "default";
+}
+
+void read_rope_scaling(const Value& block, RopeScaling* out) {
+  const std::string scheme = rope_scheme(block);
+  if (scheme == "default" || scheme == "none") return;
+  LCR_CHECK(scheme == "llama3",
+            "only llama3 RoPE scaling is implemented, config.json says \"" << scheme << "\"");
+  out->enabled = true;
+  for (const RopeRealKey& k : kRopeRealKeys) {
+    if (const Value* v = number_at(block, k.key)) out->*k.member = v->as_float();
+  }
+  if (const Value* v = number_at(block, "original_max_position_embeddings")) {
+    out->original_max_position_embeddings = v->as_int();
+  }
+}
+
+std::string file_in(const std::string& dir, const char* name) {
   if (dir.empty()) return name;
-  return dir.back() == '/' ? dir + name : dir + "/" + name;
+  return dir + (dir.back() == '/' ? "" : "/") + name;
 }
 
-// eos_token_id is an integer in older checkpoints and a list in Llama 3.x.
-void append_eos(const json::Value& node, std::vector<int>* out) {
-  if (node.is_integer()) {
-    out->push_back(node.as_int());
-    return;
-  }
-  if (!node.is_array()) return;
-  for (const json::Value& item : node.items()) {
-    if (item.is_integer()) out->push_back(item.as_int());
-  }
-}
-
-bool read_file(const std::string& path, std::string* text) {
+// The whole file, or false when it cannot be opened.
+bool slurp(const std::string& path, std::string* text) {
   std::ifstream in(path, std::ios::binary);
-  if (!in.good()) return false;
-  std::ostringstream buffer;
-  buffer << in.rdbuf();
-  *text = buffer.str();
+  if (!in) return false;
+  text->assign(std::istreambuf_iterator<char>(in), std::istreambuf_iterator<char>());
   return true;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-field rules, checked in order; the first that fails is reported.
+// ---------------------------------------------------------------------------
+
+struct Rule {
+  std::function<bool(const ModelConfig&)> holds;
+  std::function<std::string(const ModelConfig&)> message;
+};
+
+std::string text(const char* s) { return s; }
+
+const std::vector<Rule>& rules() {
+  static const std::vector<Rule> table = {
+      {[](const ModelConfig& c) { return c.hidden_size > 0 && c.intermediate_size > 0 && c.num_layers > 0; },
+       [](const ModelConfig&) { return text("config.json needs positive hidden_size, intermediate_size and "
+                                            "num_hidden_layers"); }},
+      {[](const ModelConfig& c) { return c.num_heads > 0 && c.num_kv_heads > 0; },
+       [](const ModelConfig& c) {
+         std::ostringstream m;
+         m << "config.json needs positive head counts, got " << c.num_heads << " query and " << c.num_kv_heads
+           << " key/value heads";
+         return m.str();
+       }},
+      {[](const ModelConfig& c) { return c.num_heads % c.num_kv_heads == 0; },
+       [](const ModelConfig& c) {
+         std::ostringstream m;
+         m << "num_attention_heads (" << c.num_heads << ") must be a multiple of num_key_value_heads ("
+           << c.num_kv_heads << ")";
+         return m.str();
+       }},
+      {[](const ModelConfig& c) { return c.head_dim > 0 && c.head_dim % 2 == 0; },
+       [](const ModelConfig& c) {
+         return "RoPE rotates pairs, so head_dim must be positive and even; got " + std::to_string(c.head_dim);
+       }},
+      {[](const ModelConfig& c) { return c.vocab_size > 0; },
+       [](const ModelConfig&) { return text("vocab_size must be positive"); }},
+      {[](const ModelConfig& c) { return c.rms_norm_eps > 0.0f; },
+       [](const ModelConfig&) { return text("rms_norm_eps must be positive"); }},
+      {[](const ModelConfig& c) { return c.rope_theta > 1.0f; },
+       [](const ModelConfig&) { return text("rope_theta must be greater than 1"); }},
+      {[](const ModelConfig& c) { return !c.rope_scaling.enabled || c.rope_scaling.factor > 0.0f; },
+       [](const ModelConfig&) { return text("the llama3 RoPE factor must be positive"); }},
+      {[](const ModelConfig& c) {
+         return !c.rope_scaling.enabled || c.rope_scaling.high_freq_factor > c.rope_scaling.low_freq_factor;
+       },
+       [](const ModelConfig&) { return text("llama3 RoPE needs high_freq_factor > low_freq_factor"); }},
+      {[](const ModelConfig& c) {
+         return !c.rope_scaling.enabled || c.rope_scaling.original_max_position_embeddings > 0;
+       },
+       [](const ModelConfig&) { return text("llama3 RoPE needs a positive original_max_position_embeddings"); }},
+  };
+  return table;
 }
 
 }  // namespace
 
 bool ModelConfig::is_eos(int token_id) const {
-  return std::find(eos_token_ids.begin(), eos_token_ids.end(), token_id) !=
-         eos_token_ids.end();
+  return std::count(eos_token_ids.begin(), eos_token_ids.end(), token_id) > 0;
 }
 
-// Field semantics follow the reference's src/config.cpp:40-132.
-ModelConfig ModelConfig::from_json_string(const std::string& text) {
-  json::Value doc;
-  std::string parse_error;
-  LCR_CHECK(json::parse(text, &doc, &parse_error),
-            "config.json is not valid JSON (" << parse_error << ")");
+ModelConfig ModelConfig::from_json_string(const std::string& document) {
+  Value doc;
+  std::string why;
+  LCR_CHECK(json::parse(document, &doc, &why), "config.json is not valid JSON (" << why << ")");
   LCR_CHECK(doc.is_object(), "config.json is not a JSON object");
 
-  if (const json::Value* type = doc.find("model_type"); type && type->is_string()) {
-    LCR_CHECK(type->as_string() == "llama",
-              "this runtime only implements the Llama architecture, config.json "
-              "says model_type=\"" << type->as_string() << "\"");
+  for (const OnlyValue& k : kOnlyValues) {
+    const Value* v = doc.find(k.key);
+    if (v != nullptr && v->is_string()) {
+      LCR_CHECK(v->as_string() == k.accepted, k.refusal << v->as_string() << "\"");
+    }
   }
-
-  auto required = [&doc](const char* key) {
-    const json::Value* v = doc.find(key);
-    LCR_CHECK(v != nullptr && v->is_number(),
-              "config.json is missing the integer field \"" << key << "\"");
-    return v->as_int();
-  };
+  for (const Unsupported& k : kUnsupported) {
+    const Value* v = doc.find(k.key);
+    LCR_CHECK(v == nullptr || !v->is_bool() || !v->as_bool(), k.refusal);
+  }
 
   ModelConfig c;
-  c.hidden_size = required("hidden_size");
-  c.intermediate_size = required("intermediate_size");
-  c.num_layers = required("num_hidden_layers");
-  c.num_heads = required("num_attention_heads");
-  c.vocab_size = required("vocab_size");
-  c.max_position_embeddings = required("max_position_embeddings");
+  for (const IntKey& k : kIntKeys) {
+    const Value* v = number_at(doc, k.key);
+    LCR_CHECK(v != nullptr || !k.required, "config.json is missing the integer field \"" << k.key << "\"");
+    if (v != nullptr) c.*k.member = v->as_int();
+  }
+  for (const RealKey& k : kRealKeys) {
+    if (const Value* v = number_at(doc, k.key)) c.*k.member = v->as_float();
+  }
+  for (const FlagKey& k : kFlagKeys) {
+    const Value* v = doc.find(k.key);
+    if (v != nullptr && v->is_bool()) c.*k.member = v->as_bool();
+  }
+  // Derived defaults for the optional geometry keys.
+  if (c.num_kv_heads == 0) c.num_kv_heads = c.num_heads;
+  if (c.head_dim == 0 && c.num_heads > 0) c.head_dim = c.hidden_size / c.num_heads;
 
-  const json::Value* kv = doc.find("num_key_value_heads");
-  c.num_kv_heads = (kv != nullptr && kv->is_number()) ? kv->as_int() : c.num_heads;
-  const json::Value* hd = doc.find("head_dim");
-  c.head_dim = (hd != nullptr && hd->is_number())
-                   ? hd->as_int()
-                   : (c.num_heads > 0 ? c.hidden_size / c.num_heads : 0);
-
-  if (const json::Value* v = doc.find("rms_norm_eps"); v && v->is_number()) {
-    c.rms_norm_eps = v->as_float();
+  if (const Value* block = doc.find("rope_scaling"); block != nullptr && block->is_object()) {
+    read_rope_scaling(*block, &c.rope_scaling);
   }
-  if (const json::Value* v = doc.find("rope_theta"); v && v->is_number()) {
-    c.rope_theta = v->as_float();
-  }
-  if (const json::Value* v = doc.find("tie_word_embeddings"); v && v->is_bool()) {
-    c.tie_word_embeddings = v->as_bool();
-  }
-  if (const json::Value* v = doc.find("attention_bias"); v && v->is_bool()) {
-    LCR_CHECK(!v->as_bool(), "attention projections with bias are not implemented");
-  }
-  if (const json::Value* v = doc.find("mlp_bias"); v && v->is_bool()) {
-    LCR_CHECK(!v->as_bool(), "MLP projections with bias are not implemented");
-  }
-  if (const json::Value* v = doc.find("hidden_act"); v && v->is_string()) {
-    LCR_CHECK(v->as_string() == "silu",
-              "only the SiLU/SwiGLU MLP is implemented, config.json says \""
-                  << v->as_string() << "\"");
-  }
-
-  if (const json::Value* rs = doc.find("rope_scaling"); rs && rs->is_object()) {
-    std::string type = "default";
-    if (const json::Value* t = rs->find("rope_type"); t && t->is_string()) {
-      type = t->as_string();
-    } else if (const json::Value* t2 = rs->find("type"); t2 && t2->is_string()) {
-      type = t2->as_string();
-    }
-    if (type != "default" && type != "none") {
-      LCR_CHECK(type == "llama3", "only llama3 RoPE scaling is implemented, "
-                                  "config.json says \"" << type << "\"");
-      c.rope_scaling.enabled = true;
-      if (const json::Value* f = rs->find("factor"); f && f->is_number()) {
-        c.rope_scaling.factor = f->as_float();
-      }
-      if (const json::Value* f = rs->find("low_freq_factor"); f && f->is_number()) {
-        c.rope_scaling.low_freq_factor = f->as_float();
-      }
-      if (const json::Value* f = rs->find("high_freq_factor"); f && f->is_number()) {
-        c.rope_scaling.high_freq_factor = f->as_float();
-      }
-      if (const json::Value* f = rs->find("original_max_position_embeddings");
-          f && f->is_number()) {
-        c.rope_scaling.original_max_position_embeddings = f->as_int();
-      }
-    }
-  }
-
-  if (const json::Value* b = doc.find("bos_token_id"); b && b->is_integer()) {
-    c.bos_token_id = b->as_int();
-  }
-  if (const json::Value* e = doc.find("eos_token_id")) append_eos(*e, &c.eos_token_ids);
+  if (const Value* v = doc.find("bos_token_id"); v != nullptr && v->is_integer()) c.bos_token_id = v->as_int();
+  c.eos_token_ids = token_list(doc.find("eos_token_id"));
 
   c.validate();
   return c;
 }
 
 ModelConfig ModelConfig::load(const std::string& model_dir) {
-  const std::string config_path = path_join(model_dir, "config.json");
-  std::string text;
-  LCR_CHECK(read_file(config_path, &text), "cannot read " << config_path);
-  ModelConfig c = from_json_string(text);
+  const std::string path = file_in(model_dir, "config.json");
+  std::string document;
+  LCR_CHECK(slurp(path, &document), "cannot read " << path);
+  ModelConfig c = from_json_string(document);
 
-  // generation_config.json, when present, is the authority on stop tokens.
-  std::string gen_text;
-  if (read_file(path_join(model_dir, "generation_config.json"), &gen_text)) {
-    json::Value gen;
-    if (json::parse(gen_text, &gen, nullptr) && gen.is_object()) {
-      std::vector<int> eos;
-      if (const json::Value* e = gen.find("eos_token_id")) append_eos(*e, &eos);
-      if (!eos.empty()) c.eos_token_ids = eos;
-      if (const json::Value* b = gen.find("bos_token_id"); b && b->is_integer()) {
-        c.bos_token_id = b->as_int();
-      }
-    }
+  // Stop and start tokens: generation_config.json overrides config.json when
+  // it has them (the copy in config.json is often stale). A generation config
+  // that does not parse is ignored, as it is optional.
+  std::string gen_document;
+  Value gen;
+  if (slurp(file_in(model_dir, "generation_config.json"), &gen_document) &&
+      json::parse(gen_document, &gen, nullptr) && gen.is_object()) {
+    const std::vector<int> eos = token_list(gen.find("eos_token_id"));
+    if (!eos.empty()) c.eos_token_ids = eos;
+    if (const Value* v = gen.find("bos_token_id"); v != nullptr && v->is_integer()) c.bos_token_id = v->as_int();
   }
   return c;
 }
 
 void ModelConfig::validate() const {
-  LCR_CHECK(hidden_size > 0 && intermediate_size > 0 && num_layers > 0,
-            "config.json has a non-positive hidden_size, intermediate_size, or "
-            "num_hidden_layers");
-  LCR_CHECK(num_heads > 0 && num_kv_heads > 0,
-            "config.json has a non-positive head count");
-  LCR_CHECK(num_heads % num_kv_heads == 0,
-            "num_attention_heads (" << num_heads << ") must be a multiple of "
-            "num_key_value_heads (" << num_kv_heads << ")");
-  LCR_CHECK(head_dim > 0 && head_dim % 2 == 0,
-            "head_dim must be positive and even for RoPE, got " << head_dim);
-  LCR_CHECK(vocab_size > 0, "vocab_size must be positive");
-  LCR_CHECK(rms_norm_eps > 0.0f, "rms_norm_eps must be positive");
-  LCR_CHECK(rope_theta > 1.0f, "rope_theta must be greater than one");
-  if (rope_scaling.enabled) {
-    LCR_CHECK(rope_scaling.factor > 0.0f, "RoPE scaling factor must be positive");
-    LCR_CHECK(rope_scaling.high_freq_factor > rope_scaling.low_freq_factor,
-              "RoPE high_freq_factor must exceed low_freq_factor");
-    LCR_CHECK(rope_scaling.original_max_position_embeddings > 0,
-              "RoPE original_max_position_embeddings must be positive");
+  for (const Rule& r : rules()) {
+    if (!r.holds(*this)) throw Error(r.message(*this));
   }
 }
 
 std::string ModelConfig::summary() const {
-  std::ostringstream oss;
-  oss << "layers=" << num_layers << " hidden=" << hidden_size
-      << " ffn=" << intermediate_size << " heads=" << num_heads << "/" << num_kv_heads
-      << " head_dim=" << head_dim << " vocab=" << vocab_size
-      << " rope_theta=" << rope_theta
-      << (rope_scaling.enabled ? " rope_scaling=llama3" : "")
-      << (tie_word_embeddings ? " tied_embeddings" : "");
-  return oss.str();
+  std::ostringstream s;
+  s << num_layers << " layers, hidden " << hidden_size << ", ffn " << intermediate_size << ", " << num_heads
+    << " q heads / " << num_kv_heads << " kv heads x " << head_dim << ", vocab " << vocab_size << ", rope theta "
+    << rope_theta;
+  if (rope_scaling.enabled) s << " (llama3 x" << rope_scaling.factor << ")";
+  s << (tie_word_embeddings ? ", tied head" : ", separate head");
+  return s.str();
 }
 
-// Tensor names and order: the reference's src/config.cpp:197-221.
+// The checkpoint's tensor names and shapes (the format, the reference's
+// src/config.cpp:197-221): the embedding, then per layer the nine tensors of
+// kLayerTensors in reading order, then the final norm.
+namespace {
+
+// A per-layer tensor: its name after "model.layers.<i>.", and its [rows, cols]
+// (cols 0: a vector of `rows`) as functions of the geometry.
+struct LayerTensor {
+  const char* suffix;
+  int64_t (*rows)(const ModelConfig&);
+  int64_t (*cols)(const ModelConfig&);
+};
+
+int64_t hidden_of(const ModelConfig& c) { return c.hidden_size; }
+int64_t ffn_of(const ModelConfig& c) { return c.intermediate_size; }
+int64_t q_of(const ModelConfig& c) { return c.q_dim(); }
+int64_t kv_of(const ModelConfig& c) { return c.kv_dim(); }
+int64_t vector_of(const ModelConfig&) { return 0; }
+
+constexpr LayerTensor kLayerTensors[] = {
+    {"input_layernorm.weight", hidden_of, vector_of},
+    {"self_attn.q_proj.weight", q_of, hidden_of},
+    {"self_attn.k_proj.weight", kv_of, hidden_of},
+    {"self_attn.v_proj.weight", kv_of, hidden_of},
+    {"self_attn.o_proj.weight", hidden_of, q_of},
+    {"post_attention_layernorm.weight", hidden_of, vector_of},
+    {"mlp.gate_proj.weight", ffn_of, hidden_of},
+    {"mlp.up_proj.weight", ffn_of, hidden_of},
+    {"mlp.down_proj.weight", hidden_of, ffn_of},
+};
+
+}  // namespace
+
 std::vector<WeightSpec> required_weights(const ModelConfig& c) {
-  const int64_t hidden = c.hidden_size;
-  const int64_t ffn = c.intermediate_size;
-  const int64_t q = c.q_dim();
-  const int64_t kv = c.kv_dim();
-  std::vector<WeightSpec> out;
-  out.push_back({"model.embed_tokens.weight", {c.vocab_size, hidden}});
+  std::vector<WeightSpec> specs;
+  specs.reserve(2 + std::size(kLayerTensors) * static_cast<size_t>(std::max(0, c.num_layers)));
+  specs.push_back({"model.embed_tokens.weight", {c.vocab_size, c.hidden_size}});
   for (int layer = 0; layer < c.num_layers; ++layer) {
-    const std::string p = "model.layers." + std::to_string(layer) + ".";
-    out.push_back({p + "input_layernorm.weight", {hidden}});
-    out.push_back({p + "self_attn.q_proj.weight", {q, hidden}});
-    out.push_back({p + "self_attn.k_proj.weight", {kv, hidden}});
-    out.push_back({p + "self_attn.v_proj.weight", {kv, hidden}});
-    out.push_back({p + "self_attn.o_proj.weight", {hidden, q}});
-    out.push_back({p + "post_attention_layernorm.weight", {hidden}});
-    out.push_back({p + "mlp.gate_proj.weight", {ffn, hidden}});
-    out.push_back({p + "mlp.up_proj.weight", {ffn, hidden}});
-    out.push_back({p + "mlp.down_proj.weight", {hidden, ffn}});
+    const std::string prefix = "model.layers." + std::to_string(layer) + ".";
+    for (const LayerTensor& t : kLayerTensors) {
+      WeightSpec spec{prefix + t.suffix, {t.rows(c)}};
+      if (const int64_t cols = t.cols(c); cols > 0) spec.shape.push_back(cols);
+      specs.push_back(std::move(spec));
+    }
   }
-  out.push_back({"model.norm.weight", {hidden}});
-  return out;
+  specs.push_back({"model.norm.weight", {c.hidden_size}});
+  return specs;
 }
 
 size_t weight_bytes_per_token(const ModelConfig& config, size_t elem_size) {
@@ -226,7 +357,7 @@ size_t weight_bytes_per_token(const ModelConfig& config, size_t elem_size) {
   return elements * elem_size;
 }
 
-// The llama3 band rule of the reference's src/config.cpp:223-259: a pair whose
+// The llama3 band rule (the reference's src/config.cpp:223-259): a pair whose
 // wavelength is shorter than original_context/high_freq_factor keeps its
 // frequency, one longer than original_context/low_freq_factor is divided by
 // the factor, and one in between is a linear blend of the two weighted by

@@ -1,3 +1,13 @@
+// safetensors reading and writing.
+//
+// Reading is two steps. locate_shards() turns a checkpoint directory into the
+// list of files to map: model.safetensors alone, or the distinct shard names of
+// model.safetensors.index.json's weight_map in first-mention order. Each file
+// is then mapped whole and its header is read into TensorViews pointing into
+// the mapping; every view is checked against the file (span inside the data
+// buffer, span equal to shape x dtype size) before anything can upload it.
+// The format rules and the refusal messages follow the reference's loader
+// (src/safetensors.cpp:217-322; its tests match the message substrings).
 #include "safetensors.h"
 
 #include <fcntl.h>
@@ -10,49 +20,106 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
-#include <set>
+#include <iterator>
 #include <sstream>
+#include <utility>
 
 #include "json.h"
 
 namespace lcr {
 namespace {
 
-// Larger headers than this are a corrupt or hostile file, not a checkpoint.
-constexpr uint64_t kHeaderLimit = 32ull << 20;
+static_assert(__BYTE_ORDER__ == __ORDER_LITTLE_ENDIAN__,
+              "the header length is read as a native little-endian integer");
 
-uint64_t load_le64(const uint8_t* p) {
-  uint64_t v = 0;
-  for (int i = 7; i >= 0; --i) v = (v << 8) | p[i];
-  return v;
+// The format's own bound on the header (100 MB); a larger length is a
+// corrupt file, not a checkpoint.
+constexpr uint64_t kMaxHeaderBytes = 100'000'000;
+constexpr size_t kLengthPrefix = 8;
+
+std::string in_dir(const std::string& dir, const std::string& name) {
+  if (dir.empty()) return name;
+  return dir + (dir.back() == '/' ? "" : "/") + name;
 }
 
-bool is_regular_file(const std::string& path) {
-  struct stat st;
+bool regular_file(const std::string& path) {
+  struct stat st {};
   return ::stat(path.c_str(), &st) == 0 && S_ISREG(st.st_mode);
 }
 
-std::string path_join(const std::string& dir, const std::string& name) {
-  if (dir.empty()) return name;
-  return dir.back() == '/' ? dir + name : dir + "/" + name;
+std::string bracketed(const std::vector<int64_t>& dims) {
+  std::string out = "[";
+  for (size_t i = 0; i < dims.size(); ++i) {
+    if (i > 0) out += ", ";
+    out += std::to_string(dims[i]);
+  }
+  return out + "]";
 }
 
-std::string shape_text(const std::vector<int64_t>& shape) {
-  std::ostringstream oss;
-  oss << "[";
-  for (size_t i = 0; i < shape.size(); ++i) oss << (i ? ", " : "") << shape[i];
-  oss << "]";
-  return oss.str();
+// The files a checkpoint directory's tensors live in.
+std::vector<std::string> locate_shards(const std::string& dir) {
+  const std::string single = in_dir(dir, "model.safetensors");
+  if (regular_file(single)) return {single};
+  const std::string index_path = in_dir(dir, "model.safetensors.index.json");
+  LCR_CHECK(regular_file(index_path), "no model.safetensors or model.safetensors.index.json in " << dir);
+
+  std::ifstream in(index_path, std::ios::binary);
+  const std::string text((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
+  LCR_CHECK(in.good() || in.eof(), "cannot read " << index_path);
+  json::Value index;
+  LCR_CHECK(json::parse(text, &index, nullptr), index_path << " is not valid JSON");
+  const json::Value* weight_map = index.is_object() ? index.find("weight_map") : nullptr;
+  LCR_CHECK(weight_map != nullptr && weight_map->is_object(), index_path << " has no weight_map object");
+
+  std::vector<std::string> shards;
+  for (const auto& [tensor, file] : weight_map->members()) {
+    LCR_CHECK(file.is_string(), "weight_map entry for \"" << tensor << "\" is not a filename");
+    const std::string path = in_dir(dir, file.as_string());
+    if (std::find(shards.begin(), shards.end(), path) == shards.end()) shards.push_back(path);
+  }
+  return shards;
 }
 
-bool int_list(const json::Value& v, std::vector<int64_t>* out) {
-  if (!v.is_array()) return false;
+// A non-negative integer list (shape or offsets); false if anything else.
+bool read_extents(const json::Value* v, std::vector<int64_t>* out) {
+  if (v == nullptr || !v->is_array()) return false;
   out->clear();
-  for (const json::Value& item : v.items()) {
-    if (!item.is_integer()) return false;
+  for (const json::Value& item : v->items()) {
+    if (!item.is_integer() || item.as_int64() < 0) return false;
     out->push_back(item.as_int64());
   }
   return true;
+}
+
+// One header entry, checked against the data buffer [payload, payload + size).
+TensorView describe(const std::string& file, const std::string& name, const json::Value& entry,
+                    const uint8_t* payload, size_t payload_size) {
+  LCR_CHECK(entry.is_object(), "tensor \"" << name << "\" in " << file << " is not described by an object");
+  const json::Value* dtype = entry.find("dtype");
+  const json::Value* shape = entry.find("shape");
+  const json::Value* offsets = entry.find("data_offsets");
+  LCR_CHECK(dtype != nullptr && shape != nullptr && offsets != nullptr,
+            "tensor \"" << name << "\" in " << file << " is missing dtype, shape, or data_offsets");
+  LCR_CHECK(dtype->is_string(), "tensor \"" << name << "\" in " << file << " has a non-string dtype");
+
+  TensorView t;
+  t.name = name;
+  t.dtype = dtype_from_string(dtype->as_string());
+  LCR_CHECK(read_extents(shape, &t.shape), "tensor \"" << name << "\" in " << file << " has a malformed shape");
+  std::vector<int64_t> span;
+  LCR_CHECK(read_extents(offsets, &span) && span.size() == 2 && span[0] <= span[1],
+            "tensor \"" << name << "\" in " << file << " has malformed data_offsets");
+  const size_t first = static_cast<size_t>(span[0]);
+  const size_t last = static_cast<size_t>(span[1]);
+  LCR_CHECK(last <= payload_size, "tensor \"" << name << "\" ends at byte " << last << " of the data buffer of "
+                                              << file << ", which holds " << payload_size);
+  t.nbytes = last - first;
+  const size_t wanted = static_cast<size_t>(t.numel()) * dtype_size(t.dtype);
+  LCR_CHECK(t.nbytes == wanted, "tensor \"" << name << "\" covers " << t.nbytes << " bytes; "
+                                            << dtype_name(t.dtype) << " " << t.shape_string() << " needs "
+                                            << wanted);
+  t.data = payload + first;
+  return t;
 }
 
 }  // namespace
@@ -64,159 +131,92 @@ int64_t TensorView::numel() const {
 }
 
 int64_t TensorView::dim(int index) const {
-  LCR_CHECK(index >= 0 && index < rank(), "dim " << index << " out of range for tensor \""
-                                                  << name << "\" of rank " << rank());
+  LCR_CHECK(index >= 0 && index < rank(),
+            "tensor \"" << name << "\" has rank " << rank() << ", no dimension " << index);
   return shape[static_cast<size_t>(index)];
 }
 
-std::string TensorView::shape_string() const { return shape_text(shape); }
+std::string TensorView::shape_string() const { return bracketed(shape); }
 
 void TensorView::expect_shape(std::initializer_list<int64_t> expected) const {
   expect_shape(std::vector<int64_t>(expected));
 }
 
 void TensorView::expect_shape(const std::vector<int64_t>& expected) const {
-  LCR_CHECK(expected == shape, "tensor \"" << name << "\" has shape " << shape_string()
-                                           << ", expected " << shape_text(expected));
+  LCR_CHECK(shape == expected,
+            "tensor \"" << name << "\" is " << shape_string() << ", expected " << bracketed(expected));
 }
 
 MappedFile::MappedFile(const std::string& path) : path_(path) {
-  fd_ = ::open(path.c_str(), O_RDONLY);
-  LCR_CHECK(fd_ >= 0, "cannot open " << path << ": " << std::strerror(errno));
-  struct stat st;
-  if (::fstat(fd_, &st) != 0) {
-    const int err = errno;
-    ::close(fd_);
-    fd_ = -1;
-    LCR_FAIL("cannot stat " << path << ": " << std::strerror(err));
-  }
-  size_ = static_cast<size_t>(st.st_size);
-  if (size_ <= 8) {
-    ::close(fd_);
-    fd_ = -1;
-    LCR_FAIL(path << " is too small to be a safetensors file (" << size_ << " bytes)");
-  }
-  void* map = ::mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
-  if (map == MAP_FAILED) {
-    const int err = errno;
-    ::close(fd_);
-    fd_ = -1;
-    LCR_FAIL("cannot mmap " << path << ": " << std::strerror(err));
-  }
+  // The descriptor is closed on every way out, mapped or not.
+  struct Descriptor {
+    int fd;
+    ~Descriptor() {
+      if (fd >= 0) ::close(fd);
+    }
+  } file{::open(path.c_str(), O_RDONLY | O_CLOEXEC)};
+  LCR_CHECK(file.fd >= 0, "cannot open " << path << ": " << std::strerror(errno));
+  struct stat st {};
+  LCR_CHECK(::fstat(file.fd, &st) == 0, "cannot stat " << path << ": " << std::strerror(errno));
+  const size_t bytes = static_cast<size_t>(st.st_size);
+  LCR_CHECK(bytes > kLengthPrefix, path << " holds " << bytes << " bytes, too few for a safetensors file");
+  void* map = ::mmap(nullptr, bytes, PROT_READ, MAP_PRIVATE, file.fd, 0);
+  LCR_CHECK(map != MAP_FAILED, "cannot mmap " << path << ": " << std::strerror(errno));
   base_ = static_cast<uint8_t*>(map);
+  size_ = bytes;
+  // A mapping stays valid after its descriptor is closed.
 }
 
 MappedFile::~MappedFile() {
   if (base_ != nullptr) ::munmap(base_, size_);
-  if (fd_ >= 0) ::close(fd_);
 }
 
 SafetensorsArchive::SafetensorsArchive(const std::string& model_dir) : dir_(model_dir) {
-  const std::string single = path_join(dir_, "model.safetensors");
-  const std::string index = path_join(dir_, "model.safetensors.index.json");
-  if (is_regular_file(single)) {
-    open_file(single);
-  } else if (is_regular_file(index)) {
-    std::ifstream in(index, std::ios::binary);
-    LCR_CHECK(in.good(), "cannot read " << index);
-    std::ostringstream buffer;
-    buffer << in.rdbuf();
-    json::Value doc;
-    LCR_CHECK(json::parse(buffer.str(), &doc, nullptr), index << " is not valid JSON");
-    const json::Value* map = doc.find("weight_map");
-    LCR_CHECK(map != nullptr && map->is_object(), index << " has no weight_map object");
-    std::set<std::string> shards;
-    for (const auto& member : map->members()) {
-      LCR_CHECK(member.second.is_string(),
-                "weight_map entry for \"" << member.first << "\" is not a filename");
-      shards.insert(member.second.as_string());
-    }
-    for (const std::string& shard : shards) open_file(path_join(dir_, shard));
-  } else {
-    LCR_FAIL("no model.safetensors or model.safetensors.index.json in " << dir_);
-  }
+  for (const std::string& path : locate_shards(dir_)) open_file(path);
   LCR_CHECK(!tensors_.empty(), "checkpoint in " << dir_ << " has no tensors");
 }
 
 void SafetensorsArchive::open_file(const std::string& path) {
   files_.push_back(std::make_unique<MappedFile>(path));
   const MappedFile& file = *files_.back();
-  const uint8_t* base = file.data();
-  const size_t size = file.size();
 
-  const uint64_t header_len = load_le64(base);
-  LCR_CHECK(header_len > 0 && header_len <= kHeaderLimit,
-            path << " declares an implausible header length of " << header_len << " bytes");
-  LCR_CHECK(8 + header_len <= size,
-            path << " header length " << header_len << " exceeds the file size " << size);
+  uint64_t header_bytes = 0;
+  std::memcpy(&header_bytes, file.data(), kLengthPrefix);
+  LCR_CHECK(header_bytes >= 2 && header_bytes <= kMaxHeaderBytes,
+            path << " declares a header of " << header_bytes << " bytes, which no checkpoint has");
+  LCR_CHECK(header_bytes <= file.size() - kLengthPrefix,
+            path << " header length " << header_bytes << " exceeds the file size " << file.size());
 
+  const char* header_text = reinterpret_cast<const char*>(file.data() + kLengthPrefix);
   json::Value header;
-  const char* text = reinterpret_cast<const char*>(base + 8);
-  LCR_CHECK(json::parse(text, text + header_len, &header, nullptr),
+  LCR_CHECK(json::parse(header_text, header_text + header_bytes, &header, nullptr) && header.is_object(),
             path << " has a malformed JSON header");
-  LCR_CHECK(header.is_object(), path << " header is not a JSON object");
 
-  const uint8_t* payload = base + 8 + header_len;
-  const size_t payload_size = size - 8 - header_len;
-
-  for (const auto& member : header.members()) {
-    const std::string& name = member.first;
-    if (name == "__metadata__") continue;
-    const json::Value& spec = member.second;
-    LCR_CHECK(spec.is_object(),
-              "tensor \"" << name << "\" in " << path << " is not described by an object");
-    const json::Value* dtype = spec.find("dtype");
-    const json::Value* shape = spec.find("shape");
-    const json::Value* offsets = spec.find("data_offsets");
-    LCR_CHECK(dtype != nullptr && shape != nullptr && offsets != nullptr,
-              "tensor \"" << name << "\" in " << path
-                          << " is missing dtype, shape, or data_offsets");
-    LCR_CHECK(dtype->is_string(), "tensor \"" << name << "\" has a non-string dtype");
-
-    TensorView view;
-    view.name = name;
-    view.dtype = dtype_from_string(dtype->as_string());
-    LCR_CHECK(int_list(*shape, &view.shape), "tensor \"" << name << "\" has a malformed shape");
-    for (int64_t d : view.shape) {
-      LCR_CHECK(d >= 0, "tensor \"" << name << "\" has negative extent " << d);
-    }
-    std::vector<int64_t> range;
-    LCR_CHECK(int_list(*offsets, &range) && range.size() == 2,
-              "tensor \"" << name << "\" has malformed data_offsets");
-    const int64_t begin = range[0];
-    const int64_t end = range[1];
-    LCR_CHECK(begin >= 0 && end >= begin,
-              "tensor \"" << name << "\" has data_offsets [" << begin << ", " << end << "]");
-    LCR_CHECK(static_cast<size_t>(end) <= payload_size,
-              "tensor \"" << name << "\" ends at " << end << " but the data buffer of "
-                          << path << " is only " << payload_size << " bytes");
-    view.nbytes = static_cast<size_t>(end - begin);
-    const size_t expected = static_cast<size_t>(view.numel()) * dtype_size(view.dtype);
-    LCR_CHECK(view.nbytes == expected,
-              "tensor \"" << name << "\" spans " << view.nbytes << " bytes but its shape "
-                          << view.shape_string() << " of " << dtype_name(view.dtype)
-                          << " needs " << expected);
-    view.data = payload + begin;
-    const bool inserted = tensors_.emplace(name, std::move(view)).second;
-    LCR_CHECK(inserted, "tensor \"" << name << "\" appears in more than one shard");
+  const uint8_t* payload = file.data() + kLengthPrefix + header_bytes;
+  const size_t payload_size = file.size() - kLengthPrefix - header_bytes;
+  for (const auto& [name, entry] : header.members()) {
+    if (name == "__metadata__") continue;  // free-form strings, not a tensor
+    TensorView t = describe(path, name, entry, payload, payload_size);
+    LCR_CHECK(tensors_.emplace(name, std::move(t)).second,
+              "tensor \"" << name << "\" is defined twice (again in " << path << ")");
   }
 }
 
 const TensorView* SafetensorsArchive::find(const std::string& name) const {
-  auto it = tensors_.find(name);
+  const auto it = tensors_.find(name);
   return it == tensors_.end() ? nullptr : &it->second;
 }
 
 const TensorView& SafetensorsArchive::get(const std::string& name) const {
-  const TensorView* view = find(name);
-  LCR_CHECK(view != nullptr, "checkpoint has no tensor named \"" << name << "\"");
-  return *view;
+  if (const TensorView* t = find(name)) return *t;
+  LCR_FAIL("checkpoint in " << dir_ << " has no tensor named \"" << name << "\"");
 }
 
 std::vector<std::string> SafetensorsArchive::names() const {
   std::vector<std::string> out;
   out.reserve(tensors_.size());
-  for (const auto& entry : tensors_) out.push_back(entry.first);
+  std::transform(tensors_.begin(), tensors_.end(), std::back_inserter(out),
+                 [](const auto& entry) { return entry.first; });
   std::sort(out.begin(), out.end());
   return out;
 }

@@ -51,7 +51,6 @@ class MappedFile {
 
  private:
   std::string path_;
-  int fd_ = -1;
   uint8_t* base_ = nullptr;
   size_t size_ = 0;
 };

@@ -1,12 +1,14 @@
 """The command-line tools that need no GPU (built into
-llama-cuda-runtime_amd/bin/ by build.py): lcr-inspect and lcr-tokenize, and
-the Philox draw stream that llama-run samples with.
+llama-cuda-runtime_amd/bin/ by build.py): lcr-inspect, llama-run's command
+line (help and refusals, which come before any device call), and the Philox
+draw stream that llama-run samples with.
 
   - lcr-inspect on a small checkpoint: the byte accounting against the
     reference's formula (src/model.cu:86-102) written out here from the
     config, a complete checkpoint reported clean, and missing or misshapen
     tensors each reported with exit status 1;
-  - lcr-tokenize against Hugging Face tokenizers on a trained tokenizer;
+  - llama-run --help lists every flag of the reference's command line, and
+    unknown or incomplete options exit with status 2 or 1;
   - the C++ Philox stream equal to the Python one, which test_host.py pins
     to the published known-answer vectors.
 """
@@ -100,26 +102,6 @@ def test_inspect_reports_problems(tmp_path):
     assert subprocess.run([tool("lcr-inspect")], capture_output=True).returncode == 2
 
 
-def test_tokenize_tool_matches_huggingface(tmp_path):
-    pytest.importorskip("tokenizers")
-    from test_tokenizer import corpus, trained_tokenizer
-    hf = trained_tokenizer(900, True)
-    path = tmp_path / "tokenizer.json"
-    path.write_text(hf.to_str())
-    texts = corpus(41, 200) + ["<|begin_of_text|>hi<|eot_id|>", "tab\there", "x" * 40]
-    stdin = "\n".join(json.dumps(t) for t in texts) + "\n"
-    for extra, add_bos in (([], False), (["--add-bos"], True)):
-        out = subprocess.run([tool("lcr-tokenize"), str(path), *extra], input=stdin, capture_output=True, text=True)
-        assert out.returncode == 0, out.stderr
-        lines = out.stdout.strip().split("\n")
-        assert len(lines) == len(texts)
-        for text, line in zip(texts, lines):
-            want = hf.encode(text, add_special_tokens=False).ids
-            if add_bos:
-                want = [hf.token_to_id("<|begin_of_text|>")] + want
-            assert [int(x) for x in line.split()] == want, text
-
-
 def test_cpp_philox_stream_equals_python(lcr):
     lib = lcr.load_library()
     for seed in (0, 7, 20260904, 2 ** 40 + 3):
@@ -128,3 +110,23 @@ def test_cpp_philox_stream_equals_python(lcr):
         want = np.array(lcr.philox_uniforms(seed, out.size), dtype=np.float32)
         assert np.array_equal(out, want)
         assert out.min() >= 0.0 and out.max() < 1.0
+
+
+REFERENCE_FLAGS = ["--model", "--prompt", "--system", "--chat", "--bench", "--json", "--profile", "--warmup",
+                   "--quiet", "--paged", "--max-tokens", "--temperature", "--top-k", "--top-p", "--seed",
+                   "--max-seq", "--prefill-chunk", "--page-size", "--splits", "--device", "--peak-bandwidth"]
+
+
+def test_llama_run_command_line():
+    """The flags of the reference's src/main.cu:73-123, from the help text;
+    the refusals happen before anything touches a device."""
+    out = subprocess.run([tool("llama-run"), "--help"], capture_output=True, text=True)
+    assert out.returncode == 0
+    for flag in REFERENCE_FLAGS:
+        assert f"  {flag}" in out.stdout, flag
+    bad = subprocess.run([tool("llama-run"), "--model", "x", "--frobnicate"], capture_output=True, text=True)
+    assert bad.returncode == 2 and "unknown option: --frobnicate" in bad.stderr
+    missing = subprocess.run([tool("llama-run"), "--prompt", "hi"], capture_output=True, text=True)
+    assert missing.returncode == 2 and "--model is required" in missing.stderr
+    short = subprocess.run([tool("llama-run"), "--model", "x", "--max-tokens"], capture_output=True, text=True)
+    assert short.returncode == 1 and "--max-tokens needs a value" in short.stderr

@@ -43,6 +43,10 @@ typedef struct lcr_model_options {
                            q/k/v + attention, and the split merge + o_proj (default 1) */
   int exchange_spins;   /* extension: polls before an exchange wait gives up (default 1 << 20) */
   int exchange_test_unwritten; /* tests only: exchange waits read words no block writes (default 0) */
+  int layer_grid;       /* extension: with one attention split, each layer as one grid that
+                           streams the o_proj and gate/up weights while the q/k/v -> attention
+                           -> o_proj chain runs (default 0: slower than the three kernels it
+                           replaces on MI355X; used when asked and the device holds the grid) */
 } lcr_model_options;
 
 /* ForwardStats (src/model.h:46-58) plus sizes. */
@@ -59,6 +63,7 @@ typedef struct lcr_model_stats {
   int vocab_size;
   int hidden_size;
   int num_layers;
+  int layer_grid;       /* 1 when single-split decode steps run the layer grid */
 } lcr_model_stats;
 
 void lcr_model_default_options(lcr_model_options* options);

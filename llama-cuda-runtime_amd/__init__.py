@@ -101,6 +101,7 @@ class ModelOptions(ctypes.Structure):
         ("exchange_split", ctypes.c_int),
         ("exchange_spins", ctypes.c_int),
         ("exchange_test_unwritten", ctypes.c_int),
+        ("layer_grid", ctypes.c_int),
     ]
 
 
@@ -118,6 +119,7 @@ class ModelStats(ctypes.Structure):
         ("vocab_size", ctypes.c_int),
         ("hidden_size", ctypes.c_int),
         ("num_layers", ctypes.c_int),
+        ("layer_grid", ctypes.c_int),
     ]
 
 

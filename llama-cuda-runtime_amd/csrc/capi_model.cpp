@@ -43,6 +43,7 @@ extern "C" void lcr_model_default_options(lcr_model_options* o) {
   o->exchange_split = 1;
   o->exchange_spins = 1 << 20;
   o->exchange_test_unwritten = 0;
+  o->layer_grid = 0;
 }
 
 extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* options,
@@ -68,6 +69,7 @@ extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* 
     opt.exchange_split = o.exchange_split != 0;
     opt.exchange_spins = o.exchange_spins > 0 ? o.exchange_spins : (1 << 20);
     opt.exchange_test_unwritten = o.exchange_test_unwritten != 0;
+    opt.layer_grid = o.layer_grid != 0;
     auto handle = std::make_unique<lcr_model>();
     handle->impl = std::make_unique<Model>(model_dir, opt);
     *out = handle.release();
@@ -163,6 +165,7 @@ extern "C" int lcr_model_stats_get(const lcr_model* m, lcr_model_stats* out) {
   out->vocab_size = model.config().vocab_size;
   out->hidden_size = model.config().hidden_size;
   out->num_layers = model.config().num_layers;
+  out->layer_grid = model.layer_grid() ? 1 : 0;
   return LCR_OK;
 }
 

@@ -74,6 +74,7 @@ struct DecodeStepArgs {
   // exchange_*_word() below; as many again after the written ones are never
   // written (tests of the give-up path read there).
   unsigned long long* exchange;
+  bool layer_grid;           // splits == 1: the whole layer as one grid (layer_grid_kernel)
   bool exchange_single;
   bool exchange_oproj;
   bool exchange_split;
@@ -90,6 +91,10 @@ bool decode_step_supported(int hidden, int ffn, int num_heads, int num_kv_heads,
 // and all its blocks fit on the device at once.
 bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, int hidden, bool paged,
                           int compute_units, bool with_oproj);
+// True when the whole-layer grid is compiled for this geometry and all its
+// blocks fit on the device at once.
+bool decode_layer_grid_fits(int hidden, int ffn, int num_heads, int num_kv_heads, int head_dim, bool paged,
+                            int compute_units);
 // Blocks of the split exchange grid the device holds at once, 0 if none.
 int decode_split_exchange_slots(int num_heads, int num_kv_heads, int head_dim, bool paged, int compute_units);
 

@@ -20,8 +20,20 @@ constexpr int kLmHeadMaxBlocks = 1024;
 constexpr int kLmHeadRows = 2;  // rows per wave per group
 constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
 constexpr int kDownWaves = 1;   // waves (rows) per down block
-constexpr int kQkvRowsPerWave = 2;   // rows per qkv wave
-constexpr int kOProjRowsPerWave = 2; // rows per wave of the exchange grid's o_proj blocks
+constexpr int kQkvRowsPerWave = 2;   // rows per qkv wave (separate kernel and split grid)
+#ifndef LCR_EXCHANGE_QKV_ROWS
+#define LCR_EXCHANGE_QKV_ROWS 2
+#endif
+#ifndef LCR_EXCHANGE_OPROJ_ROWS
+#define LCR_EXCHANGE_OPROJ_ROWS 2
+#endif
+// Rows per wave of the one-split exchange grid's q/k/v blocks and of the
+// exchange grids' o_proj blocks. Two: the q/k/v projection is the start of
+// the grid's dependency chain and streams fastest spread over the most
+// compute units (192 blocks of 16 rows; 96 blocks of 32 rows measured
+// 9.7 -> 11.2 us for the grid).
+constexpr int kExchangeQkvRows = LCR_EXCHANGE_QKV_ROWS;
+constexpr int kOProjRowsPerWave = LCR_EXCHANGE_OPROJ_ROWS;
 constexpr int kGateUpActsPerWave = 1;  // activations (gate + up row pairs) per gate_up wave
 // Query heads per block in the long-context attention launch (with fewer
 // than G, the heads of one kv head are spread over G / kLongContextHeads
@@ -158,10 +170,13 @@ constexpr int kPublishNone = 0;
 constexpr int kPublishConsume = 1;
 constexpr int kPublishBroadcast = 2;
 
-template <int NCH, int HD, bool kPaged, int WAVES, int RW, int G, int kPublish>
+// `after_load` runs right after the block's weight loads are issued (the layer
+// grid issues the loads of its later phases there).
+template <int NCH, int HD, bool kPaged, int WAVES, int RW, int G, int kPublish, typename AfterLoad = NoPreWait>
 __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDevicePtrs& w,
                                           const KvCacheView& view, int layer, int block,
-                                          QkvShared<NCH, WAVES / 2 * RW>& sh, bool seed = true, uint32_t tag = 0) {
+                                          QkvShared<NCH, WAVES / 2 * RW>& sh, bool seed = true, uint32_t tag = 0,
+                                          AfterLoad after_load = AfterLoad{}) {
   constexpr int H = NCH * 512;
   constexpr int HALF = HD / 2;
   constexpr int PAIRS = WAVES / 2 * RW;  // rotation pairs per block
@@ -197,6 +212,7 @@ __device__ __forceinline__ void qkv_block(const DecodeStepArgs& a, const LayerDe
     for (int r = 0; r < RW; ++r) rows[r] = w.qkv + static_cast<size_t>(head * HD + r0 + r) * H;
     tile.load(rows, lane);
   }
+  after_load();
 
   norm_finish<NCH>(sh.xs, nin, a.eps, sh.scratch, (seed && layer == 0 && block == 0) ? a.resid : nullptr);
 
@@ -340,7 +356,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStep
 
 // q/k/v projection and single-split attention in one grid (exchange.h). The
 // first qkv_blocks blocks are the projection (kAttnWaves waves of
-// kQkvRowsPerWave rows, 16 rows per block) and publish what they compute; the
+// kExchangeQkvRows rows) and publish what they compute; the
 // last num_heads blocks are the attention, one query head each, numbered as
 // attention_step_kernel numbers them (qkv_blocks is a multiple of the eight
 // XCDs, so each kv head's blocks still share one XCD). An attention block
@@ -350,7 +366,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(DecodeStep
 template <int NCH, int HD, bool kPaged>
 struct ExchangeStepShared {
   union {
-    QkvShared<NCH, kAttnWaves / 2 * kQkvRowsPerWave> qkv;
+    QkvShared<NCH, kAttnWaves / 2 * kExchangeQkvRows> qkv;
     struct {
       AttnShared<kPaged, HD, 1> attn;
       float q[HD];
@@ -428,7 +444,8 @@ __global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepA
   __shared__ ExchangeStepShared<NCH, HD, kPaged> sh;
   const int b = static_cast<int>(blockIdx.x);
   if (b < qkv_blocks) {
-    qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, kPublishConsume>(a, w, view, layer, b, sh.qkv, !kOProj);
+    qkv_block<NCH, HD, kPaged, kAttnWaves, kExchangeQkvRows, G, kPublishConsume>(a, w, view, layer, b, sh.qkv,
+                                                                                 !kOProj);
     return;
   }
   const size_t broadcast = 3 * static_cast<size_t>(a.num_heads) * HD;  // first broadcast word
@@ -544,6 +561,297 @@ __global__ __launch_bounds__(kAttnThreads) void merge_oproj_kernel(DecodeStepArg
   }
   const int splits = min(a.splits, *a.position + 1);
   merge_split_partials(a.attn, a.partials, b, splits, HD, lds, a.exchange + attn_words, tag);
+}
+
+// ---------------------------------------------------------------------------
+// The layer grid: a whole layer in one grid (one split)
+// ---------------------------------------------------------------------------
+//
+// One 512-thread block per compute unit, kLayerBlocks of them, all resident
+// at once (the host checks), each taking several roles in turn:
+//   Q  blocks 0 .. qkv_blocks - 1: 16 q/k/v rows each (qkv_block), publishing
+//      the query and the new key and value to the attention blocks (consume
+//      words); 192 blocks for Llama-3.2-1B;
+//   A  the next num_heads blocks: attention for one query head (as in
+//      qkv_attention_kernel), publishing its output as tagged words;
+//   O  every block: one o_proj row per wave, joining the residual, and
+//      publishing the joined value of its row as a tagged word;
+//   G  every block: four gate/up activation pairs per wave, after the norm of
+//      the whole residual (read from the O words), publishing the SwiGLU
+//      activations as tagged words (two elements each);
+//   D  every block: one down row per wave over all activations (read from the
+//      G words), joining the residual into memory for the next layer.
+// A block issues the weight loads of O and G before it waits for anything
+// (Q blocks right after their own q/k/v loads; attention blocks, whose own
+// registers are full, after the attention), so the o_proj and gate/up
+// weights stream while the q/k/v -> attention -> o_proj chain runs; the down
+// loads are issued once G has consumed its registers. The arithmetic of every
+// row is the separate kernels' (same tiles, same orders, same rounding
+// points), so the results are theirs bit for bit.
+//
+// Word regions (exchange.h, X = num_heads * head_dim): the one-split grid's
+// consume words [0, 3X) and attention words [3X, 3.5X); then the O words
+// (hidden of them) and the G words (ffn / 2) from 3.5X.
+constexpr int kLayerBlocks = 256;
+constexpr int kLayerActsPerWave = 4;   // gate/up activation pairs per wave
+// Of those, the ones whose rows a block requests before it waits for the
+// attention output (the rest after o_proj). Every variant measured on
+// MI355X for the Llama-3.2-1B step (1 to 4 early activations, the down row
+// requested before or after the residual wait, the quiet or the direct wait)
+// took 32-35 us per layer, against 28.4 us for the exchange grid, gate_up and
+// down kernels, which is why the model leaves this grid off by default.
+constexpr int kLayerEarlyActs = 2;
+
+__host__ __device__ inline size_t layer_resid_word(int num_heads, int head_dim) {
+  return exchange_qkv_word(num_heads, head_dim);
+}
+__host__ __device__ inline size_t layer_act_word(int num_heads, int head_dim, int hidden) {
+  return exchange_qkv_word(num_heads, head_dim) + static_cast<size_t>(hidden);
+}
+
+// Every wave of the block waits for N tagged words per lane at address(k):
+// first lane 0 alone polls one of the wave's words (one small read per poll
+// instead of the wave's whole set, while the producers still stream their
+// weights), then the wave takes them all.
+template <int N, typename Address>
+__device__ __forceinline__ void wait_tagged_quietly(Address address, uint32_t tag, uint32_t (&out)[N], int spins,
+                                                    int* status) {
+  const int lane = lane_id();
+  int polls = 0;
+  while (true) {
+    uint32_t seen = 0;
+    if (lane == 0) seen = static_cast<uint32_t>(exchange_peek(address(0)) >> 32);
+    seen = __builtin_amdgcn_readfirstlane(seen);
+    if (seen == tag) break;
+    if (++polls >= spins) break;  // the full wait below gives up and reports
+  }
+  exchange_wait_tagged_at<N>(address, tag, out, spins, status);
+}
+
+template <int NCH, int NCH_F, int HD, bool kPaged, int G>
+struct LayerShared {
+  union {
+    QkvShared<NCH, kAttnWaves / 2 * kQkvRowsPerWave> qkv;
+    struct {
+      AttnShared<kPaged, HD, 1> attn;
+      float q[HD];
+      __attribute__((aligned(16))) elem_t kv[2 * HD];
+    } at;
+    struct {
+      __attribute__((aligned(16))) elem_t xs[NCH * 512];  // o_proj input, then the normed residual
+      float scratch[16];
+    } og;
+    __attribute__((aligned(16))) elem_t act[NCH_F * 512];  // down input
+  };
+  float resid[NCH * 512];  // the residual after o_proj (G's norm input, D's join)
+  // Words the block publishes (its o_proj rows' joined residual, then its
+  // activation pairs), gathered so that one wave writes them with one store
+  // instruction: every 64-byte line of words has one writer instruction, as
+  // in the other exchange grids.
+  uint32_t publish[2 * kAttnWaves];
+};
+
+// The gate and up rows of activations first .. first + R/2 - 1, as pairs.
+template <int R, int NCH>
+__device__ __forceinline__ void load_gate_up_rows(GemvTile<R, NCH>& tile, const elem_t* __restrict__ gate_up,
+                                                  int first, int ffn, int lane) {
+  constexpr int H = NCH * 512;
+  const elem_t* rows[R];
+#pragma unroll
+  for (int k = 0; k < R / 2; ++k) {
+    rows[2 * k] = gate_up + static_cast<size_t>(first + k) * H;
+    rows[2 * k + 1] = gate_up + static_cast<size_t>(ffn + first + k) * H;
+  }
+  tile.load(rows, lane);
+}
+
+template <int NCH, int NCH_F, int HD, bool kPaged, int G>
+__global__ __launch_bounds__(kAttnThreads) void layer_grid_kernel(DecodeStepArgs a, LayerDevicePtrs w,
+                                                                  KvCacheView view, int layer, int qkv_blocks,
+                                                                  float scale, int tag_slot) {
+  constexpr int H = NCH * 512;
+  constexpr int F = NCH_F * 512;
+  constexpr int A = kLayerActsPerWave;
+  constexpr int E = kLayerEarlyActs;
+  static_assert(H / kLayerBlocks == kAttnWaves, "one o_proj and one down row per wave");
+  static_assert(F / kLayerBlocks == kAttnWaves * A, "four activations per wave");
+  static_assert(E >= 0 && E <= A, "early activations are a part of the wave's");
+  __shared__ LayerShared<NCH, NCH_F, HD, kPaged, G> sh;
+  const int b = static_cast<int>(blockIdx.x);
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const uint32_t tag = (*a.epoch) * static_cast<uint32_t>(kExchangeTagSlots) + static_cast<uint32_t>(tag_slot) + 1u;
+  unsigned long long* const attn_words = a.exchange + exchange_attn_out_word(a.num_heads, HD);
+  unsigned long long* const resid_words = a.exchange + layer_resid_word(a.num_heads, HD);
+  unsigned long long* const act_words = a.exchange + layer_act_word(a.num_heads, HD, H);
+  const int rd = a.exchange_read_offset;
+
+  const int row = b * kAttnWaves + wave;  // this wave's o_proj and down row
+  const int act0 = row * A;               // its first activation
+  GemvTile<1, NCH> wo;
+  GemvTile<2 * (E > 0 ? E : 1), NCH> wg_early;
+  GemvTile<2 * (A - E > 0 ? A - E : 1), NCH> wg_late;
+  float vold = 0.0f;  // the residual entry of `row` before the o_proj join
+  // Loads return in issue order, so a wait also waits for every load issued
+  // before it: a block requests only what arrives before the words it waits
+  // for next. During the q/k/v -> attention chain: the o_proj row, and (q/k/v
+  // and idle blocks) the gate/up rows of the first E activations; after
+  // o_proj: the other gate/up rows (the attention blocks' E as well: theirs
+  // would arrive after the attention output) and the down row, which streams
+  // behind them while G waits and runs.
+  const bool attention_role = b >= qkv_blocks && b < qkv_blocks + a.num_heads;
+  auto issue_early = [&]() {
+    vold = layer == 0 ? elem_to_float(a.embedding[static_cast<size_t>(*a.token) * H + row]) : a.resid[row];
+    const elem_t* orow[1] = {w.o + static_cast<size_t>(row) * H};
+    wo.load(orow, lane);
+    if constexpr (E > 0) {
+      if (!attention_role) load_gate_up_rows(wg_early, w.gate_up, act0, F, lane);
+    }
+  };
+
+  if (b < qkv_blocks) {
+    // Q: its q/k/v rows; the residual is not seeded here (the O role reads
+    // the embedding row at layer 0 itself).
+    qkv_block<NCH, HD, kPaged, kAttnWaves, kQkvRowsPerWave, G, kPublishConsume>(a, w, view, layer, b, sh.qkv, false);
+  } else if (attention_role) {
+    // A: attention for one query head, numbered as qkv_attention_kernel
+    // numbers its attention blocks (the q/k/v blocks are a multiple of the
+    // eight XCDs).
+    int unit, g = 0;
+    if (G > 1) {
+      attention_block_coords(b - qkv_blocks, a.num_kv_heads, G, &unit, &g);
+    } else {
+      unit = b - qkv_blocks;
+    }
+    const int head = unit * G + g;
+    AttnExchange<HD> x;
+    x.words = a.exchange + rd + static_cast<size_t>(3 * head) * HD;
+    x.broadcast = false;
+    x.take_kv = true;
+    x.spins = a.exchange_spins;
+    x.status = a.exchange_status;
+    x.q_lds = sh.at.q;
+    x.kv_lds = sh.at.kv;
+    x.out_words = attn_words;
+    x.tag = tag;
+    decode_attention_block<kPaged, HD, 1, true>(sh.at.attn, a.attn, a.partials, nullptr, view, unit, head, 0, 1,
+                                                *a.position + 1, scale, &x);
+  }
+  issue_early();
+  __syncthreads();  // the Q and A roles are done with the LDS union
+
+  // O: the attention output (two elements per word) into LDS, the row's dot,
+  // the residual join, published.
+  {
+    constexpr int PER = H / 2 / kAttnThreads;
+    uint32_t payload[PER];
+    unsigned long long* mine = attn_words + rd + wave * 64 * PER;
+    wait_tagged_quietly<PER>([&](int k) { return mine + lane + 64 * k; }, tag, payload, a.exchange_spins,
+                             a.exchange_status);
+    uint32_t* xs32 = reinterpret_cast<uint32_t*>(sh.og.xs);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) xs32[wave * 64 * PER + lane + 64 * k] = payload[k];
+    __syncthreads();
+    vec16 xv[NCH];
+    load_x_lds<NCH>(xv, sh.og.xs, lane);
+    float out[1];
+    wo.dot(out, xv);
+    if (lane == 0) {
+      const float proj = elem_to_float(float_to_elem(out[0]));
+      const float xold = elem_to_float(float_to_elem(vold));
+      sh.publish[wave] = __float_as_uint(xold + proj);
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kAttnWaves) {
+      exchange_put_tagged(resid_words + b * kAttnWaves + lane, tag, sh.publish[lane]);
+    }
+  }
+  if constexpr (E > 0) {
+    if (attention_role) load_gate_up_rows(wg_early, w.gate_up, act0, F, lane);
+  }
+  if constexpr (A - E > 0) load_gate_up_rows(wg_late, w.gate_up, act0 + E, F, lane);
+  GemvTile<1, NCH_F> wd;
+  {
+    const elem_t* drow[1] = {w.down + static_cast<size_t>(row) * F};
+    wd.load(drow, lane);
+  }
+
+  // G: the norm of the whole joined residual (threads below kThreads read
+  // chunk t of it, 8 words, as norm_load would from memory), the gate/up rows,
+  // SwiGLU, the activations published two to a word.
+  {
+    NormInput<NCH> nin;
+    static_assert(NormInput<NCH>::kPer == 1, "one norm chunk per thread");
+    if (static_cast<int>(threadIdx.x) < kThreads) {
+      uint32_t bits[8];
+      unsigned long long* mine = resid_words + rd + 8 * threadIdx.x;
+      wait_tagged_quietly<8>([&](int k) { return mine + k; }, tag, bits, a.exchange_spins, a.exchange_status);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        nin.v[0][j] = __uint_as_float(bits[j]);
+        sh.resid[8 * threadIdx.x + j] = nin.v[0][j];
+      }
+      nin.w[0] = load16(w.post_norm + 8 * threadIdx.x);
+    }
+    __syncthreads();  // O's LDS reads are done before the norm overwrites it
+    norm_finish<NCH>(sh.og.xs, nin, a.eps, sh.og.scratch, nullptr);
+    vec16 xv[NCH];
+    load_x_lds<NCH>(xv, sh.og.xs, lane);
+    float out[2 * A];
+    if constexpr (E > 0) {
+      float part[2 * (E > 0 ? E : 1)];
+      wg_early.dot(part, xv);
+#pragma unroll
+      for (int k = 0; k < 2 * E; ++k) out[k] = part[k];
+    }
+    if constexpr (A - E > 0) {
+      float part[2 * (A - E > 0 ? A - E : 1)];
+      wg_late.dot(part, xv);
+#pragma unroll
+      for (int k = 0; k < 2 * (A - E); ++k) out[2 * E + k] = part[k];
+    }
+    uint32_t pairs[A / 2];
+#pragma unroll
+    for (int k = 0; k < A / 2; ++k) {
+      const float g0 = elem_to_float(float_to_elem(out[4 * k]));
+      const float u0 = elem_to_float(float_to_elem(out[4 * k + 1]));
+      const float g1 = elem_to_float(float_to_elem(out[4 * k + 2]));
+      const float u1 = elem_to_float(float_to_elem(out[4 * k + 3]));
+      pairs[k] = static_cast<uint32_t>(float_to_elem_bits(silu(g0) * u0)) |
+                 (static_cast<uint32_t>(float_to_elem_bits(silu(g1) * u1)) << 16);
+    }
+    static_assert(A / 2 * kAttnWaves <= 2 * kAttnWaves, "the block's activation words fit the staging");
+    if (lane == 0) {
+#pragma unroll
+      for (int k = 0; k < A / 2; ++k) sh.publish[wave * (A / 2) + k] = pairs[k];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < A / 2 * kAttnWaves) {
+      exchange_put_tagged(act_words + b * (A / 2) * kAttnWaves + lane, tag, sh.publish[lane]);
+    }
+  }
+
+  // D: all activations into LDS, the dot with the down row, the join.
+  {
+    constexpr int PER = F / 2 / kAttnThreads;
+    uint32_t payload[PER];
+    unsigned long long* mine = act_words + rd + PER * threadIdx.x;
+    wait_tagged_quietly<PER>([&](int k) { return mine + k; }, tag, payload, a.exchange_spins, a.exchange_status);
+    __syncthreads();  // G's LDS reads are done before the union is reused
+    uint32_t* act32 = reinterpret_cast<uint32_t*>(sh.act);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) act32[PER * threadIdx.x + k] = payload[k];
+    __syncthreads();
+    vec16 xv[NCH_F];
+    load_x_lds<NCH_F>(xv, sh.act, lane);
+    float out[1];
+    wd.dot(out, xv);
+    if (lane == 0) {
+      const float proj = elem_to_float(float_to_elem(out[0]));
+      const float xmid = elem_to_float(float_to_elem(sh.resid[row]));
+      a.resid[row] = xmid + proj;
+    }
+  }
 }
 
 // Split merge (splits > 1 only), one kMergeThreads-thread block per query head.
@@ -733,9 +1041,16 @@ template <int NCH, int NCH_F, int HD, bool kPaged, int G>
 void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, const KvCacheView& view,
                          int layer, hipStream_t s, unsigned mask, int tag_slot) {
   const int qkv_rows = (a.num_heads + 2 * a.num_kv_heads) * HD;
+  if (a.exchange != nullptr && a.layer_grid && a.splits == 1 && mask == kDecodeAll) {
+    const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
+    layer_grid_kernel<NCH, NCH_F, HD, kPaged, G><<<kLayerBlocks, kAttnThreads, 0, s>>>(
+        a, w, view, layer, qkv_rows / (kAttnWaves * kQkvRowsPerWave), scale, tag_slot);
+    HIP_CHECK_LAUNCH();
+    return;
+  }
   if (a.exchange != nullptr && a.exchange_single && a.splits == 1 && (mask & kDecodeQkv) &&
       (mask & kDecodeAttention)) {
-    const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
+    const int qkv_blocks = qkv_rows / (kAttnWaves * kExchangeQkvRows);
     const float scale = 1.0f / std::sqrt(static_cast<float>(HD));
     if (a.exchange_oproj && (mask & kDecodeOProj)) {
       const int oproj_blocks = a.hidden / (kAttnWaves * kOProjRowsPerWave);
@@ -828,8 +1143,8 @@ bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, int hid
   if (head_dim != 64 || num_kv_heads <= 0) return false;
   const int g = num_heads / num_kv_heads;
   const int qkv_rows = (num_heads + 2 * num_kv_heads) * head_dim;
-  if (qkv_rows % (kAttnWaves * kQkvRowsPerWave) != 0) return false;
-  const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
+  if (qkv_rows % (kAttnWaves * kExchangeQkvRows) != 0) return false;
+  const int qkv_blocks = qkv_rows / (kAttnWaves * kExchangeQkvRows);
   if (qkv_blocks % 8 != 0) return false;  // the attention blocks' XCD numbering
   if (with_oproj && (hidden % (kAttnWaves * kOProjRowsPerWave) != 0 || num_heads * head_dim != 2048)) return false;
   int per_cu = 0;
@@ -858,6 +1173,43 @@ bool decode_exchange_fits(int num_heads, int num_kv_heads, int head_dim, int hid
   if (!with_oproj) return slots >= qkv_blocks + num_heads;
   const int waiting = num_heads + hidden / (kAttnWaves * kOProjRowsPerWave);
   return slots >= qkv_blocks + num_heads && slots > waiting;
+}
+
+// The layer grid runs when its work divides as the kernel assumes (one o_proj
+// and one down row per wave, four activations per wave, 16 q/k/v rows per
+// block, the attention blocks after them on whole rounds of the eight XCDs)
+// and all kLayerBlocks blocks are resident at once: every block waits for
+// words of the others.
+bool decode_layer_grid_fits(int hidden, int ffn, int num_heads, int num_kv_heads, int head_dim, bool paged,
+                            int compute_units) {
+  if (hidden != 2048 || ffn != 8192 || head_dim != 64 || num_kv_heads <= 0) return false;
+  if (num_heads * head_dim != hidden || num_heads % num_kv_heads != 0) return false;
+  const int qkv_rows = (num_heads + 2 * num_kv_heads) * head_dim;
+  if (qkv_rows % (kAttnWaves * kQkvRowsPerWave) != 0) return false;
+  const int qkv_blocks = qkv_rows / (kAttnWaves * kQkvRowsPerWave);
+  if (qkv_blocks % 8 != 0 || qkv_blocks + num_heads > kLayerBlocks) return false;
+  if (exchange_attn_out_word(num_heads, head_dim) + num_heads * head_dim / 2 > layer_resid_word(num_heads, head_dim) ||
+      layer_act_word(num_heads, head_dim, hidden) + ffn / 2 > exchange_written_words(num_heads, head_dim)) {
+    return false;
+  }
+  const void* fn = nullptr;
+#define LCR_LAYER_FN(G_)                                                                              \
+  case G_:                                                                                            \
+    fn = paged ? reinterpret_cast<const void*>(&layer_grid_kernel<4, 16, 64, true, G_>)               \
+               : reinterpret_cast<const void*>(&layer_grid_kernel<4, 16, 64, false, G_>);             \
+    break;
+  switch (num_heads / num_kv_heads) {
+    LCR_LAYER_FN(1)
+    LCR_LAYER_FN(2)
+    LCR_LAYER_FN(4)
+    LCR_LAYER_FN(8)
+    default:
+      return false;
+  }
+#undef LCR_LAYER_FN
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kAttnThreads, 0) != hipSuccess) return false;
+  return static_cast<long>(per_cu) * compute_units >= kLayerBlocks;
 }
 
 // Blocks of the split exchange grid the device holds at once (the fewest over

@@ -70,6 +70,9 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
     exchange_oproj_ = exchange_enabled_ && options_.exchange_oproj &&
                       decode_exchange_fits(config_.num_heads, config_.num_kv_heads, config_.head_dim,
                                            config_.hidden_size, paged, multiprocessors_, true);
+    layer_grid_enabled_ = fused_ && options_.decode_exchange && options_.layer_grid &&
+                          decode_layer_grid_fits(config_.hidden_size, config_.intermediate_size, config_.num_heads,
+                                                 config_.num_kv_heads, config_.head_dim, paged, multiprocessors_);
   }
 
   // The table serves the fused decode step and the prefill q/k/v projection
@@ -379,6 +382,7 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.compute_units = multiprocessors_;
   a.exchange = exchange_in_use() ? exchange_words_ : nullptr;
   a.exchange_single = exchange_enabled_;
+  a.layer_grid = layer_grid_enabled_;
   a.exchange_oproj = exchange_oproj_;
   a.exchange_split = exchange_split_slots_ > 0;
   a.exchange_slots = exchange_split_slots_;
@@ -651,6 +655,12 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
     mask = kDecodeQkv | kDecodeAttention | kDecodeOProj;
     bytes = (qd + 2 * kvd) * H * e + H * e + H * 4 + (qd + 2 * kvd) * e + 2.0 * kvd * seq_len * e + qd * e +
             H * qd * e + 2 * H * 4;
+  } else if (kernel == "layer") {
+    // The whole layer: the layer grid when the step uses it, else the
+    // kernels that run in its place.
+    mask = kDecodeAll;
+    bytes = ((qd + 2 * kvd) * H + H * qd + 2 * F * H + H * F) * e + 2 * H * e + 2.0 * kvd * seq_len * e +
+            2 * H * 4;
   } else if (kernel == "attention") {
     mask = kDecodeAttention;
     bytes = 2.0 * kvd * seq_len * e + qd * e + qd * e;

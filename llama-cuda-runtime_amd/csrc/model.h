@@ -73,6 +73,12 @@ class Model {
     bool exchange_split = true;           // split attention: q/k/v + attention, and merge + o_proj, as grids
     int exchange_spins = 1 << 20;         // polls before an exchange wait gives up
     bool exchange_test_unwritten = false; // tests: waits read words no block writes
+    // With one attention split, each layer as one grid (kernels/k_decode.hip,
+    // layer_grid_kernel) when the device holds it: the o_proj and gate/up
+    // weights stream while the q/k/v -> attention -> o_proj chain runs. Off
+    // by default: measured 32.8-34.5 us per layer on MI355X against 28.4 us
+    // for the exchange grid, gate_up and down kernels it replaces.
+    bool layer_grid = false;
   };
 
   // Prompt chunks shorter than this run token by token through the decode
@@ -146,7 +152,8 @@ class Model {
   // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head",
   // "argmax" (the reduction of the head's per-block keys to the id alone),
   // "qkv_attention" or "qkv_attention_oproj" (the exchange grids, or the
-  // kernels that run in their place).
+  // kernels that run in their place), "layer" (a whole layer: the layer grid,
+  // or the kernels that run in its place).
   double time_decode_kernel(const std::string& kernel, int launches, double* bytes_per_launch);
   // Whether the decode step runs q/k/v and attention as one exchange grid.
   bool decode_exchange() const { return exchange_enabled_; }
@@ -159,6 +166,8 @@ class Model {
   // Whether o_proj runs in the exchange grid too.
   bool exchange_oproj() const { return exchange_oproj_; }
   bool exchange_split() const { return exchange_split_slots_ > 0; }
+  // Whether single-split decode steps run each layer as one grid.
+  bool layer_grid() const { return layer_grid_enabled_; }
 
  private:
   void load_weights(const SafetensorsArchive& archive);
@@ -220,7 +229,8 @@ class Model {
   int* exchange_status_ = nullptr;       // device address of exchange_status_host_
   int* exchange_status_host_ = nullptr;
   // Whether any exchange grid can run (its waits then need checking).
-  bool exchange_in_use() const { return exchange_enabled_ || exchange_split_slots_ > 0; }
+  bool exchange_in_use() const { return exchange_enabled_ || exchange_split_slots_ > 0 || layer_grid_enabled_; }
+  bool layer_grid_enabled_ = false;
   // After a synchronization: throws lcr::Error, clearing the words and the
   // status, when a wait of the steps since the last check gave up.
   void check_exchange();

@@ -1,7 +1,9 @@
 """The decode step's q/k/v projection, single-split attention and o_proj as
 one grid (kernels/exchange.h, qkv_attention_kernel): the attention blocks take
 their query and the new position's key and value from in-grid exchange words,
-and the o_proj blocks the attention output from tagged broadcast words.
+and the o_proj blocks the attention output from tagged broadcast words. The
+models here turn the whole-layer grid off (layer_grid=0), which would
+otherwise replace this grid at one split (tests/test_gpu_layer_grid.py).
 
   - the grid is used on the Llama-3.2-1B geometry, both cache layouts, with
     o_proj (grid 2) unless asked for without it (grid 1);
@@ -27,6 +29,7 @@ from helpers import expect_bits_equal
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(num_hidden_layers=2, vocab_size=4096)
+NO_LAYER_GRID = dict(layer_grid=0)
 
 
 @pytest.fixture(scope="module")
@@ -45,11 +48,11 @@ def greedy_logits(m, prompt, steps):
 
 @pytest.mark.parametrize("paged", [False, True])
 def test_exchange_grid_is_used(lcr, small_ckpt, paged):
-    m = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1)
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=256, paged=int(paged), prefill_via_decode=1)
     assert m.exchange_status() == (2, 0)
-    one = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1, exchange_oproj=0)
+    one = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=256, paged=int(paged), prefill_via_decode=1, exchange_oproj=0)
     assert one.exchange_status() == (1, 0)
-    off = lcr.Model(small_ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1, decode_exchange=0)
+    off = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=256, paged=int(paged), prefill_via_decode=1, decode_exchange=0)
     assert off.exchange_status() == (0, 0)
 
 
@@ -60,9 +63,9 @@ def test_exchange_equals_oracle_and_two_kernel_step(lcr, small_ckpt, paged, grap
     """Prompts of 1, 63, 64 and 130 tokens put the new position first in the
     cache, last in a full tile, first in a new tile and in a later wave's tile."""
     kw = dict(max_seq=256, paged=int(paged), use_graph=graph, prefill_via_decode=1)
-    m = lcr.Model(small_ckpt, **kw)
-    one = lcr.Model(small_ckpt, exchange_oproj=0, **kw)
-    ref = lcr.Model(small_ckpt, decode_exchange=0, **kw)
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, **kw)
+    one = lcr.Model(small_ckpt, **NO_LAYER_GRID, exchange_oproj=0, **kw)
+    ref = lcr.Model(small_ckpt, **NO_LAYER_GRID, decode_exchange=0, **kw)
     o = oracle.OracleModel(small_ckpt, max_seq=256, paged=paged, multiprocessors=m.stats().multiprocessors)
     prompt = lcr.synthetic_tokens(prompt_len, m.vocab, seed=prompt_len)
     got = greedy_logits(m, prompt, 3)
@@ -84,7 +87,7 @@ def test_exchange_equals_oracle_and_two_kernel_step(lcr, small_ckpt, paged, grap
 def test_exchange_group_sizes(lcr, tmp_path_factory, kv_heads, paged):
     d = tmp_path_factory.mktemp(f"exchange_group_{kv_heads}")
     ckpt = lcr.write_synthetic_checkpoint(d, lcr.llama_config(num_key_value_heads=kv_heads, **SMALL))
-    m = lcr.Model(ckpt, max_seq=256, paged=int(paged), prefill_via_decode=1)
+    m = lcr.Model(ckpt, **NO_LAYER_GRID, max_seq=256, paged=int(paged), prefill_via_decode=1)
     # The grid runs one 512-thread block per compute unit: 16 q/k/v rows per
     # block plus one block per query head must fit (groups of 4 and 8 do on
     # 256 compute units; groups of 1 and 2 keep the two-kernel step).
@@ -94,7 +97,7 @@ def test_exchange_group_sizes(lcr, tmp_path_factory, kv_heads, paged):
     if not fits:
         # The one-split grid must not run where it does not fit: with its waits
         # pointed at words no block writes, a step that ran it would fail.
-        probe = lcr.Model(ckpt, max_seq=64, paged=int(paged), prefill_via_decode=1, exchange_spins=4,
+        probe = lcr.Model(ckpt, **NO_LAYER_GRID, max_seq=64, paged=int(paged), prefill_via_decode=1, exchange_spins=4,
                           exchange_test_unwritten=1)
         probe.prefill(lcr.synthetic_tokens(3, m.vocab, seed=1))
         probe.decode(1)
@@ -111,7 +114,7 @@ def test_exchange_group_sizes(lcr, tmp_path_factory, kv_heads, paged):
 
 
 def test_exchange_generate_greedy_matches_oracle(lcr, small_ckpt):
-    m = lcr.Model(small_ckpt, max_seq=256, prefill_via_decode=1)
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=256, prefill_via_decode=1)
     o = oracle.OracleModel(small_ckpt, max_seq=256, multiprocessors=m.stats().multiprocessors)
     prompt = lcr.synthetic_tokens(20, m.vocab, seed=5)
     first = oracle.argmax(m.logits(m.prefill(prompt)))
@@ -136,7 +139,7 @@ def test_exchange_wait_gives_up(lcr, small_ckpt, oproj, graph):
     generate_greedy. Each failure clears the words and the status."""
     grid = 2 if oproj else 1
     for via_decode in (1, 0):
-        m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=via_decode, exchange_spins=4,
+        m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=128, prefill_via_decode=via_decode, exchange_spins=4,
                       exchange_test_unwritten=1, exchange_oproj=oproj, use_graph=graph)
         prompt = lcr.synthetic_tokens(5, m.vocab, seed=3)
         with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
@@ -156,7 +159,7 @@ def test_exchange_decode_after_short_timing_graph(lcr, small_ckpt):
     new prompt: the next steps' o_proj blocks must wait for their own
     attention output, not take the timed replay's words (which carry the
     same slots), so the logits equal the oracle's."""
-    m = lcr.Model(small_ckpt, max_seq=256, prefill_via_decode=1)
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=256, prefill_via_decode=1)
     o = oracle.OracleModel(small_ckpt, max_seq=256, multiprocessors=m.stats().multiprocessors)
     m.prefill(lcr.synthetic_tokens(30, m.vocab, seed=12))
     for name in ("qkv_attention_oproj", "qkv_attention"):
@@ -181,8 +184,8 @@ def test_exchange_kernel_timing_waits_for_its_own_launch(lcr, small_ckpt):
     separate-kernel model hold the same state (the next step's logits are
     the same bits)."""
     kw = dict(max_seq=256, prefill_via_decode=1)
-    m = lcr.Model(small_ckpt, **kw)
-    ref = lcr.Model(small_ckpt, decode_exchange=0, **kw)
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, **kw)
+    ref = lcr.Model(small_ckpt, **NO_LAYER_GRID, decode_exchange=0, **kw)
     prompt = lcr.synthetic_tokens(40, m.vocab, seed=8)
     a = m.logits(m.prefill(prompt))
     b = ref.logits(ref.prefill(prompt))
@@ -207,8 +210,8 @@ def test_split_exchange_grids_match_oracle(lcr, small_ckpt, paged, splits):
     equal the oracle's with the same split count and the separate kernels',
     bit for bit, including steps whose position leaves later splits empty."""
     kw = dict(max_seq=512, paged=int(paged), prefill_via_decode=1, attention_splits=splits)
-    m = lcr.Model(small_ckpt, **kw)
-    ref = lcr.Model(small_ckpt, exchange_split=0, **kw)
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, **kw)
+    ref = lcr.Model(small_ckpt, **NO_LAYER_GRID, exchange_split=0, **kw)
     o = oracle.OracleModel(small_ckpt, max_seq=512, paged=paged, multiprocessors=m.stats().multiprocessors,
                            attention_splits=splits)
     for prompt_len in (5, 300):
@@ -235,7 +238,7 @@ def test_split_exchange_wait_gives_up(lcr, small_ckpt):
     16-row q/k/v block (192 for this geometry), so they run from 6 splits on;
     fewer splits run the separate kernels, which wait on nothing; position 0
     runs the one-split grid."""
-    m = lcr.Model(small_ckpt, max_seq=128, prefill_via_decode=1, attention_splits=8, exchange_spins=4,
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=128, prefill_via_decode=1, attention_splits=8, exchange_spins=4,
                   exchange_test_unwritten=1)
     heads, qkv_blocks = 32, (32 + 2 * 8) * 64 // 16
     first_split_grid = next(p for p in range(1, 8) if heads * m.decode_splits(p + 1) >= qkv_blocks)

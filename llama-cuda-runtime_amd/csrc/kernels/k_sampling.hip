@@ -257,6 +257,21 @@ __global__ __launch_bounds__(kCompactThreads) void sample_compact_kernel(
   if (threadIdx.x == 0) cand_counts[blockIdx.x] = total;
 }
 
+// The sampled id's stores: the output, and in a device-resident generation
+// loop the next step's input, the history, the position, the draw counter
+// and the step counter.
+__device__ __forceinline__ void finish_sample(int32_t* out_id, int picked, int draw, const SampleStepState& step) {
+  *out_id = picked;
+  if (step.counter != nullptr) {
+    const int pos = *step.position;
+    *step.next_token = picked;
+    if (pos + 1 < step.history_len) step.history[pos + 1] = picked;
+    *step.position = pos + 1;
+    *step.counter = draw + 1;
+    if (step.epoch != nullptr) *step.epoch = *step.epoch + 1u;
+  }
+}
+
 // One compare-exchange step of the bitonic sort with the element of thread
 // t ^ step: thread t keeps the element that ranks first when it is the lower
 // of the pair in an ascending run (or the upper in a descending one), else
@@ -374,6 +389,36 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
       }
       __syncthreads();
     }
+    // Wave 0 holds the best 64 in order, rank r in lane r: it walks them
+    // itself, reading rank i's weight and index from lane i (the same fma
+    // chain, in the same order, as the LDS walk below).
+    if (wave == 0) {
+      const float weight = t < found ? lcr_expf(v) : 0.0f;
+      const int limit = min(found, top_k);
+      const float inv_total = 1.0f / total_sum;
+      int keep = 0;
+      float kept_mass = 0.0f;
+      for (int i = 0; i < limit; ++i) {
+        kept_mass = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), i)), inv_total,
+                                   kept_mass);
+        ++keep;
+        if (top_p < 1.0f && kept_mass >= top_p) break;
+      }
+      if (keep == 0) keep = 1;
+      const int draw = step.counter != nullptr ? min(max(*step.counter, 0), step.draws - 1) : 0;
+      const float u = step.counter != nullptr ? step.uniforms[draw] : uniform;
+      const float target = u * kept_mass;
+      int picked = __builtin_amdgcn_readlane(idx, 0);
+      float running = 0.0f;
+      for (int i = 0; i < keep; ++i) {
+        running = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), i)), inv_total,
+                                 running);
+        picked = __builtin_amdgcn_readlane(idx, i);
+        if (running >= target) break;
+      }
+      if (t == 0) finish_sample(out_id, picked, draw, step);
+    }
+    return;
   } else {
     // Bitonic sort of all candidates.
     for (int span = 2; span <= kMaxCandidates; span <<= 1) {
@@ -424,15 +469,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
       picked = indices[i];
       if (running >= target) break;
     }
-    *out_id = picked;
-    if (step.counter != nullptr) {
-      const int pos = *step.position;
-      *step.next_token = picked;
-      if (pos + 1 < step.history_len) step.history[pos + 1] = picked;
-      *step.position = pos + 1;
-      *step.counter = draw + 1;
-      if (step.epoch != nullptr) *step.epoch = *step.epoch + 1u;
-    }
+    finish_sample(out_id, picked, draw, step);
   }
 }
 

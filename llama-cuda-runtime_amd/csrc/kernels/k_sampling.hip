@@ -72,51 +72,59 @@ __device__ __forceinline__ float max_from_keys(const unsigned long long* __restr
 // of the 1024-thread order, each adding exp(scaled_i) for i = t, t + 1024,
 // ... in order, exactly as one 1024-thread block would; the thread's partial
 // sum goes to partial_sums[t] and the block's histogram of bins to
-// block_hist[b][bin] (counts, so their order of addition is free). Four lanes
-// share a thread's chain: lane s of a quad computes the exponentials of terms
-// s, s + 4, s + 8, ... and the quad's first lane adds all of them in term
-// order, each broadcast to it across the quad, so the sum is the chain's, bit
-// for bit, with a quarter of the exponentials per lane.
-constexpr int kSumBlocks = kSampleThreads / 64;
-constexpr int kSumWaves = 4;                 // per block: 64 chains, 4 lanes each
-constexpr int kSumTerms = 8;                 // terms per lane per batch (32 per chain)
+// block_hist[b][bin] (counts, so their order of addition is free). The
+// block's 16 waves share its 64 chains: wave w computes the exponentials of
+// terms w, w + 16, ..., w + 112 of a batch of 128 for every chain (lane l,
+// chain 64 b + l: each load reads 64 consecutive logits), all of its loads in
+// flight at once, and stages them in LDS by term; then wave 0's lane l adds
+// chain l's terms in term order, so the sum is the chain's, bit for bit. One
+// batch covers vocabularies up to 131072 entries.
+constexpr int kSumChains = 64;                           // chains per block
+constexpr int kSumBlocks = kSampleThreads / kSumChains;
+constexpr int kSumWaves = 16;
+constexpr int kSumTerms = 8;                             // terms per lane per batch
+constexpr int kSumBatch = kSumWaves * kSumTerms;         // terms per chain per batch
+constexpr int kSumThreads = 64 * kSumWaves;
 
-template <int S>
-__device__ __forceinline__ float quad_lane(float v) {
-  constexpr int ctrl = S | (S << 2) | (S << 4) | (S << 6);  // quad_perm [S, S, S, S]
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
-}
-
-__global__ __launch_bounds__(64 * kSumWaves) void sample_sum_kernel(float* __restrict__ partial_sums,
-                                                                    int* __restrict__ block_hist,
-                                                                    const unsigned long long* __restrict__ block_best,
-                                                                    int best_blocks, const float* __restrict__ logits,
-                                                                    int vocab, float inv_temperature) {
+__global__ __launch_bounds__(kSumThreads) void sample_sum_kernel(float* __restrict__ partial_sums,
+                                                                 int* __restrict__ block_hist,
+                                                                 const unsigned long long* __restrict__ block_best,
+                                                                 int best_blocks, const float* __restrict__ logits,
+                                                                 int vocab, float inv_temperature) {
   __shared__ int hist[kHistogramBins];
+  __shared__ float stage[kSumBatch][kSumChains];
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) >> 6;
-  const int sub = lane & 3;
-  const int chain = static_cast<int>(blockIdx.x) * 64 + wave * 16 + (lane >> 2);
+  const int chain = static_cast<int>(blockIdx.x) * kSumChains + lane;
+  // Terms of this lane's chain (none for a chain at or past the vocabulary's
+  // end); the block's first chain has the most, which bounds the loop
+  // uniformly over the block.
+  const int chain_terms = chain < vocab ? (vocab - 1 - chain) / kSampleThreads + 1 : 0;
+  const int block_chain = static_cast<int>(blockIdx.x) * kSumChains;
+  float e[kSumTerms];
+  auto load_batch = [&](int first) {
+#pragma unroll
+    for (int j = 0; j < kSumTerms; ++j) {
+      const int k = first + wave + kSumWaves * j;
+      e[j] = k < chain_terms ? logits[chain + k * kSampleThreads] : 0.0f;
+    }
+  };
+  // The first batch's logits are requested before the maximum, which they
+  // do not depend on, so the two reads overlap.
+  load_batch(0);
   const float max_logit = max_from_keys(block_best, best_blocks);
-  for (int b = threadIdx.x; b < kHistogramBins; b += 64 * kSumWaves) hist[b] = 0;
+  for (int b = threadIdx.x; b < kHistogramBins; b += kSumThreads) hist[b] = 0;
   __syncthreads();
   float local_sum = 0.0f;
   int last_bin = 0;
-  // Batch q holds terms 4 kSumTerms q .. 4 kSumTerms (q + 1) - 1 of the
-  // chain; this lane's are those congruent to `sub` mod 4.
-  for (int first = 0; chain + first * kSampleThreads < vocab; first += 4 * kSumTerms) {
-    float e[kSumTerms];
+  for (int first = 0; block_chain + first * kSampleThreads < vocab; first += kSumBatch) {
+    if (first > 0) load_batch(first);
 #pragma unroll
     for (int j = 0; j < kSumTerms; ++j) {
-      const int i = chain + (first + 4 * j + sub) * kSampleThreads;
-      e[j] = i < vocab ? logits[i] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < kSumTerms; ++j) {
-      const int i = chain + (first + 4 * j + sub) * kSampleThreads;
+      const int k = first + wave + kSumWaves * j;
       const float scaled = (e[j] - max_logit) * inv_temperature;
-      e[j] = lcr_expf(scaled);
-      if (i < vocab) {
+      stage[wave + kSumWaves * j][lane] = k < chain_terms ? lcr_expf(scaled) : 0.0f;
+      if (k < chain_terms) {
         const int bin = min(kHistogramBins - 1, static_cast<int>(-scaled * (kHistogramBins / 20.0f)));
         if (bin == kHistogramBins - 1) {
           ++last_bin;
@@ -125,26 +133,27 @@ __global__ __launch_bounds__(64 * kSumWaves) void sample_sum_kernel(float* __res
         }
       }
     }
-    // In term order: term first + 4 j + s is lane s's e[j].
+    __syncthreads();
+    if (wave == 0) {
+      // Terms past the chain's end are staged as +0, and adding +0 to a sum
+      // of exponentials (never -0) leaves its bits unchanged, so every slot
+      // is added; reads go 32 at a time ahead of their adds.
 #pragma unroll
-    for (int j = 0; j < kSumTerms; ++j) {
-      const float t0 = quad_lane<0>(e[j]);
-      const float t1 = quad_lane<1>(e[j]);
-      const float t2 = quad_lane<2>(e[j]);
-      const float t3 = quad_lane<3>(e[j]);
-      const int k = first + 4 * j;
-      if (chain + k * kSampleThreads < vocab) local_sum += t0;
-      if (chain + (k + 1) * kSampleThreads < vocab) local_sum += t1;
-      if (chain + (k + 2) * kSampleThreads < vocab) local_sum += t2;
-      if (chain + (k + 3) * kSampleThreads < vocab) local_sum += t3;
+      for (int k0 = 0; k0 < kSumBatch; k0 += 32) {
+        float t[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) t[u] = stage[k0 + u][lane];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) local_sum += t[u];
+      }
     }
+    __syncthreads();
   }
   last_bin = wave_sum_int(last_bin);
-  if (sub == 0) partial_sums[chain] = local_sum;
-  __syncthreads();
+  if (wave == 0) partial_sums[chain] = local_sum;
   if (lane == 0) atomicAdd(&hist[kHistogramBins - 1], last_bin);
   __syncthreads();
-  for (int b = threadIdx.x; b < kHistogramBins; b += 64 * kSumWaves) {
+  for (int b = threadIdx.x; b < kHistogramBins; b += kSumThreads) {
     block_hist[blockIdx.x * kHistogramBins + b] = hist[b];
   }
 }
@@ -257,19 +266,60 @@ __global__ __launch_bounds__(kCompactThreads) void sample_compact_kernel(
   if (threadIdx.x == 0) cand_counts[blockIdx.x] = total;
 }
 
+// What a sampled step reads of the device-resident generation loop's state:
+// the draw index (clamped to the draws), its uniform, the position and the
+// step counter (for a single call: draw 0, the caller's uniform).
+struct StepValues {
+  int draw;
+  float u;
+  int position;
+  uint32_t epoch;
+};
+
+__device__ __forceinline__ StepValues load_step_values(const SampleStepState& step, float uniform) {
+  StepValues sv{0, uniform, 0, 0u};
+  if (step.counter != nullptr) {
+    sv.position = *step.position;
+    if (step.epoch != nullptr) sv.epoch = *step.epoch;
+    sv.draw = min(max(*step.counter, 0), step.draws - 1);
+    sv.u = step.uniforms[sv.draw];
+  }
+  return sv;
+}
+
 // The sampled id's stores: the output, and in a device-resident generation
 // loop the next step's input, the history, the position, the draw counter
 // and the step counter.
-__device__ __forceinline__ void finish_sample(int32_t* out_id, int picked, int draw, const SampleStepState& step) {
+__device__ __forceinline__ void finish_sample(int32_t* out_id, int picked, const StepValues& sv,
+                                              const SampleStepState& step) {
   *out_id = picked;
   if (step.counter != nullptr) {
-    const int pos = *step.position;
     *step.next_token = picked;
-    if (pos + 1 < step.history_len) step.history[pos + 1] = picked;
-    *step.position = pos + 1;
-    *step.counter = draw + 1;
-    if (step.epoch != nullptr) *step.epoch = *step.epoch + 1u;
+    if (sv.position + 1 < step.history_len) step.history[sv.position + 1] = picked;
+    *step.position = sv.position + 1;
+    *step.counter = sv.draw + 1;
+    if (step.epoch != nullptr) *step.epoch = sv.epoch + 1u;
   }
+}
+
+// The value of lane (lane ^ step), step a power of two below 64 that is a
+// constant once the loops around the call are unrolled: DPP and LDS swizzles
+// for the short distances (xor_lane), which move the same bits as a general
+// shuffle without its address computation and LDS round trip.
+template <typename T>
+__device__ __forceinline__ T xor_lane_step(T v, int step) {
+  static_assert(sizeof(T) == 4, "one 32-bit lane value");
+  const float f = __builtin_bit_cast(float, v);
+  float r;
+  switch (step) {
+    case 1: r = xor_lane<1>(f); break;
+    case 2: r = xor_lane<2>(f); break;
+    case 4: r = xor_lane<4>(f); break;
+    case 8: r = xor_lane<8>(f); break;
+    case 16: r = xor_lane<16>(f); break;
+    default: r = xor_lane<32>(f); break;
+  }
+  return __builtin_bit_cast(T, r);
 }
 
 // One compare-exchange step of the bitonic sort with the element of thread
@@ -310,12 +360,17 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
   __shared__ float values[kMaxCandidates];
   __shared__ int indices[kMaxCandidates];
   __shared__ float weights[kMaxCandidates];
+  __shared__ StepValues shared_step;
   const int t = threadIdx.x;
   const int lane = lane_id();
   const int wave = t >> 6;
   static_assert(kSampleThreads == kMaxCandidates, "one candidate per thread");
 
   const float partial = partial_sums[t];
+  // The step state, read by wave 1 (idle until the sum's barriers) so that
+  // its dependent reads (the counter, then the uniform it indexes) pass
+  // under wave 0's scan; the sum's barriers publish it.
+  if (t == 64) shared_step = load_step_values(step, uniform);
 
   // Where each block's list starts in the merged order (wave 0, exclusive
   // scan over the blocks, 64 at a time).
@@ -366,9 +421,11 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
     // holding the pair's best 64, which steps 32 .. 1 of the sort put in
     // order. The order is total (indices are distinct), so these 64 and
     // their order are the full sort's first 64. Wave 0 ends with them.
+#pragma unroll
     for (int span = 2; span <= 64; span <<= 1) {
+#pragma unroll
       for (int step = span >> 1; step > 0; step >>= 1) {
-        bitonic_keep(v, idx, __shfl_xor(v, step, 64), __shfl_xor(idx, step, 64), lane, span, step);
+        bitonic_keep(v, idx, xor_lane_step(v, step), xor_lane_step(idx, step), lane, span, step);
       }
     }
     for (int lists = kSampleThreads / 64; lists > 1; lists >>= 1) {
@@ -383,40 +440,42 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
           v = ov;
           idx = oi;
         }
+#pragma unroll
         for (int step = 32; step > 0; step >>= 1) {
-          bitonic_keep(v, idx, __shfl_xor(v, step, 64), __shfl_xor(idx, step, 64), lane, 64, step);
+          bitonic_keep(v, idx, xor_lane_step(v, step), xor_lane_step(idx, step), lane, 64, step);
         }
       }
       __syncthreads();
     }
-    // Wave 0 holds the best 64 in order, rank r in lane r: it walks them
-    // itself, reading rank i's weight and index from lane i (the same fma
-    // chain, in the same order, as the LDS walk below).
+    // Wave 0 holds the best 64 in order, rank r in lane r. The walk's two
+    // loops add the same terms in the same order (fma(weight_i, 1 / total,
+    // running) from 0), so both read the prefixes of one chain: every lane
+    // runs that chain over the 64 ranks and keeps prefix r in lane r, and
+    // the cut (the first rank whose prefix reaches top_p, within top_k) and
+    // the pick (the first kept rank whose prefix reaches the target) are the
+    // lowest set bits of two ballots.
     if (wave == 0) {
       const float weight = t < found ? lcr_expf(v) : 0.0f;
       const int limit = min(found, top_k);
       const float inv_total = 1.0f / total_sum;
-      int keep = 0;
-      float kept_mass = 0.0f;
-      for (int i = 0; i < limit; ++i) {
-        kept_mass = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), i)), inv_total,
-                                   kept_mass);
-        ++keep;
-        if (top_p < 1.0f && kept_mass >= top_p) break;
+      float chain = 0.0f, prefix = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 64; ++i) {
+        chain = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), i)), inv_total,
+                               chain);
+        prefix = lane == i ? chain : prefix;
       }
-      if (keep == 0) keep = 1;
-      const int draw = step.counter != nullptr ? min(max(*step.counter, 0), step.draws - 1) : 0;
-      const float u = step.counter != nullptr ? step.uniforms[draw] : uniform;
-      const float target = u * kept_mass;
-      int picked = __builtin_amdgcn_readlane(idx, 0);
-      float running = 0.0f;
-      for (int i = 0; i < keep; ++i) {
-        running = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), i)), inv_total,
-                                 running);
-        picked = __builtin_amdgcn_readlane(idx, i);
-        if (running >= target) break;
-      }
-      if (t == 0) finish_sample(out_id, picked, draw, step);
+      const unsigned long long cross = __ballot(lane < limit && top_p < 1.0f && prefix >= top_p);
+      const int walked = cross != 0 ? __ffsll(cross) : limit;  // ranks the first loop takes
+      const float kept_mass =
+          walked > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prefix), walked - 1)) : 0.0f;
+      const int keep = max(walked, 1);
+      const StepValues sv = shared_step;
+      const float target = sv.u * kept_mass;
+      const unsigned long long hit = __ballot(lane < keep && prefix >= target);
+      const int rank = hit != 0 ? __ffsll(hit) - 1 : keep - 1;
+      const int picked = __builtin_amdgcn_readlane(idx, rank);
+      if (t == 0) finish_sample(out_id, picked, sv, step);
     }
     return;
   } else {
@@ -459,9 +518,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
       if (top_p < 1.0f && kept_mass >= top_p) break;
     }
     if (keep == 0) keep = 1;
-    const int draw = step.counter != nullptr ? min(max(*step.counter, 0), step.draws - 1) : 0;
-    const float u = step.counter != nullptr ? step.uniforms[draw] : uniform;
-    const float target = u * kept_mass;
+    const StepValues sv = shared_step;
+    const float target = sv.u * kept_mass;
     int picked = indices[0];
     float running = 0.0f;
     for (int i = 0; i < keep; ++i) {
@@ -469,7 +527,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
       picked = indices[i];
       if (running >= target) break;
     }
-    finish_sample(out_id, picked, draw, step);
+    finish_sample(out_id, picked, sv, step);
   }
 }
 
@@ -526,7 +584,7 @@ extern "C" int lcr_sample(int32_t* out_id, const float* logits, int vocab, float
   const float inv_temperature = 1.0f / temperature;
   argmax_partial_kernel<<<blocks, kArgmaxThreads, 0, s>>>(best, logits, vocab);
   CAPI_LAUNCHED();
-  sample_sum_kernel<<<kSumBlocks, 64 * kSumWaves, 0, s>>>(sums, hist, best, blocks, logits, vocab, inv_temperature);
+  sample_sum_kernel<<<kSumBlocks, kSumThreads, 0, s>>>(sums, hist, best, blocks, logits, vocab, inv_temperature);
   CAPI_LAUNCHED();
   sample_compact_kernel<<<compact_blocks, kCompactThreads, 0, s>>>(cand_values, cand_indices, counts, logits, vocab,
                                                                    inv_temperature, best, blocks, hist);
@@ -556,7 +614,7 @@ void enqueue_sample_step(const float* logits, int vocab, float temperature, int 
   float* cand_values = scratch + kScratchKeys + kScratchSums + kScratchHist + compact_blocks;
   int* cand_indices = reinterpret_cast<int*>(cand_values + static_cast<size_t>(compact_blocks) * kCompactSlice);
   const float inv_temperature = 1.0f / temperature;
-  sample_sum_kernel<<<kSumBlocks, 64 * kSumWaves, 0, s>>>(sums, hist, block_best, best_blocks, logits, vocab,
+  sample_sum_kernel<<<kSumBlocks, kSumThreads, 0, s>>>(sums, hist, block_best, best_blocks, logits, vocab,
                                                           inv_temperature);
   HIP_CHECK_LAUNCH();
   sample_compact_kernel<<<compact_blocks, kCompactThreads, 0, s>>>(cand_values, cand_indices, counts, logits, vocab,

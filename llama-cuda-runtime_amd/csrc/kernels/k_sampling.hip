@@ -52,6 +52,21 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
 }
 
 
+// Inclusive prefix sum over the 64 lanes of a wave (integers: exact in any
+// order), on DPP: within each row of 16 lanes by shifts of 1, 2, 4 and 8
+// (lanes shifted in from outside the row read 0), then the total of row 0
+// into row 1 and of row 2 into row 3 (row_bcast:15), then that of rows 0-1
+// into rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ int wave_inclusive_scan_int(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15, rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31, rows 2 and 3
+  return v;
+}
+
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -373,20 +388,29 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
   if (t == 64) shared_step = load_step_values(step, uniform);
 
   // Where each block's list starts in the merged order (wave 0, exclusive
-  // scan over the blocks, 64 at a time).
+  // scan over the blocks, 64 at a time). The counts of the first
+  // kCountChunks chunks are all requested before the first is scanned.
   if (wave == 0) {
-    int carry = 0;
-    for (int base = 0; base < compact_blocks; base += 64) {
-      const int b = base + lane;
-      const int count = b < compact_blocks ? cand_counts[b] : 0;
-      int incl = count;
+    constexpr int kCountChunks = 4;
+    int counts[kCountChunks];
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int other = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += other;
-      }
+    for (int k = 0; k < kCountChunks; ++k) {
+      const int b = 64 * k + lane;
+      counts[k] = b < compact_blocks ? cand_counts[b] : 0;
+    }
+    int carry = 0;
+    auto scan_chunk = [&](int base, int count) {
+      const int b = base + lane;
+      const int incl = wave_inclusive_scan_int(count);
       if (b < compact_blocks) block_start[b] = carry + incl - count;
-      carry += __shfl(incl, 63, 64);
+      carry += __builtin_amdgcn_readlane(incl, 63);
+    };
+#pragma unroll
+    for (int k = 0; k < kCountChunks; ++k) {
+      if (64 * k < compact_blocks) scan_chunk(64 * k, counts[k]);
+    }
+    for (int base = 64 * kCountChunks; base < compact_blocks; base += 64) {
+      scan_chunk(base, base + lane < compact_blocks ? cand_counts[base + lane] : 0);
     }
     if (lane == 0) shared_found = min(carry, kMaxCandidates);
   }
@@ -407,7 +431,10 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
         hi_b = mid - 1;
       }
     }
-    const size_t at = static_cast<size_t>(lo_b) * kCompactSlice + static_cast<size_t>(t - block_start[lo_b]);
+    // Within block lo_b's list by construction; clamped into the lists all
+    // the same, so no start table can send the read elsewhere.
+    const int in_list = min(max(t - block_start[lo_b], 0), kCompactSlice - 1);
+    const size_t at = static_cast<size_t>(lo_b) * kCompactSlice + static_cast<size_t>(in_list);
     v = cand_values[at];
     idx = cand_indices[at];
   }

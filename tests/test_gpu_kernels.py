@@ -670,14 +670,16 @@ def test_sampling_matches_oracle(gpu, orc, lcr):
 
 
 def test_sampling_edges_match_oracle(gpu, orc, lcr):
-    """Vocabularies that do not fill the sampler's per-wave ranges, and a
+    """Vocabularies that do not fill the sampler's per-wave ranges, or take
+    more than one batch of its ordered sums (over 131,072 entries) or more
+    than the compaction counts it requests at once (over 262,144), and a
     first histogram bin holding more than 1024 candidates (the cutoff is then
     one bin and the candidates are the first 1024 in index order)."""
     lib = gpu
     r = rng(91)
     uniforms = lcr.philox_uniforms(7, 32)
     cases = []
-    for vocab in (1, 63, 64, 65, 1000, 1025, 4097):
+    for vocab in (1, 63, 64, 65, 1000, 1025, 4097, 140000, 300000):
         cases.append(r.normal(0, 1.2, size=vocab).astype(np.float32))
     crowded = r.normal(-30, 1, size=128256).astype(np.float32)
     crowded[r.choice(128256, 5000, replace=False)] = np.float32(4.0) - r.random(5000).astype(np.float32) * 0.01

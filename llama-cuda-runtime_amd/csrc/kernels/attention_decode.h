@@ -108,6 +108,12 @@ struct AttnExchange {
   int spins;
   int* status;
   float* q_lds;                  // [heads][kHeadDim] LDS
+  // Take the queries before requesting the first tiles rather than after:
+  // for a block that computed q/k/v rows first, whose queries are mostly
+  // published by then. Loads complete in issue order, so a wait issued behind
+  // both of a wave's tiles holds every wave until both have landed; taken
+  // first, the wave starts on its first tile while the second is in flight.
+  bool early_wait = false;
   elem_t* kv_lds;                // [2][kHeadDim] LDS, 16-byte aligned
   // When set, the head's output also goes out as broadcast words, two
   // elements each (element 2i in the low half), tagged `tag`, at
@@ -233,7 +239,8 @@ __device__ __forceinline__ void decode_attention_block(
   }
   // kExchange: wave 0 takes the query and the new key and value from the
   // exchange words into LDS; after the barrier every lane reads its query
-  // chunk. Every wave calls this exactly once, after its first tile's loads.
+  // chunk. Every wave calls this exactly once: after its first tile's loads,
+  // or before them with x->early_wait.
   auto exchange_wait = [&]() {
     if constexpr (kExchange) {
       static_assert(kHeadDim % 64 == 0, "exchange blocks take whole waves of words");
@@ -502,10 +509,16 @@ __device__ __forceinline__ void decode_attention_block(
       vec16 ka[P], va[P], kb[P], vb[P];
       uint32_t o[P];
       int tile = first_tile + wave;
+      bool first = kWaits;
+      if constexpr (kWaits) {
+        if (x->early_wait) {
+          exchange_wait();
+          first = false;
+        }
+      }
       tile_chunks(tile, window, o);
       load_chunks(view.keys, o, ka);
       load_chunks(view.values, o, va);
-      bool first = kWaits;
       while (true) {
         const int t1 = tile + kAttnWaves;
         const bool more1 = t1 < last_tile;
@@ -537,10 +550,15 @@ __device__ __forceinline__ void decode_attention_block(
       vec16 kr[P], vr[P];
       uint32_t o[P];
       int tile = first_tile + wave;
+      if constexpr (kWaits) {
+        if (x->early_wait) exchange_wait();
+      }
       tile_chunks(tile, window, o);
       load_chunks(view.keys, o, kr);
       load_chunks(view.values, o, vr);
-      if constexpr (kWaits) exchange_wait();
+      if constexpr (kWaits) {
+        if (!x->early_wait) exchange_wait();
+      }
       while (true) {
         const int next = tile + kAttnWaves;
         const bool more = next < last_tile;

@@ -539,6 +539,8 @@ __global__ __launch_bounds__(kAttnThreads) void split_exchange_kernel(DecodeStep
   x.kv_lds = kv_lds;
   x.out_words = nullptr;
   x.tag = tag;
+  // 8192 positions: 0.697 -> 0.688 ms per token; 32768: 0.855 -> 0.835.
+  x.early_wait = b < qkv_blocks;
   decode_attention_block<kPaged, HD, kHeads, true>(ash, a.attn, a.partials, nullptr, view, kv_head, head0, split,
                                                    splits, seq_len, scale, &x, project);
 }

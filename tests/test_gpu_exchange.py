@@ -2,8 +2,9 @@
 one grid (kernels/exchange.h, qkv_attention_kernel): the attention blocks take
 their query and the new position's key and value from in-grid exchange words,
 and the o_proj blocks the attention output from tagged broadcast words. The
-models here turn the whole-layer grid off (layer_grid=0), which would
-otherwise replace this grid at one split (tests/test_gpu_layer_grid.py).
+models here pass layer_grid=0 (the default) explicitly, so that they keep
+testing this grid whatever the default of the whole-layer grid, which
+replaces it at one split when on (tests/test_gpu_layer_grid.py).
 
   - the grid is used on the Llama-3.2-1B geometry, both cache layouts, with
     o_proj (grid 2) unless asked for without it (grid 1);

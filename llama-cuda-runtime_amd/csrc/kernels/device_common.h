@@ -182,27 +182,47 @@ __host__ __device__ __forceinline__ void lcr_sincosf(float angle, float* s_out, 
   *c_out = static_cast<float>(c);
 }
 
-// The value of lane (lane ^ kMask), for a compile-time mask. Lane exchanges
-// only move bits, so which hardware path carries them cannot change a result:
-// DPP quad permutes for masks 1 and 2, a DPP row rotate by 8 for mask 8 (both
-// are plain VALU operand modifiers), the LDS swizzle's xor mode for 4 and 16,
-// and ds_bpermute for 32.
+// The 32 bits of lane (lane ^ kMask), for a compile-time mask. Lane exchanges
+// only move bits, so which hardware path carries them cannot change a result.
+// All run in the VALU, without the LDS round trip of ds_bpermute or
+// ds_swizzle (lane layouts checked on gfx950 with an in-bounds probe):
+//  - 1 and 2: DPP quad permutes;
+//  - 4: DPP row_half_mirror (lane i of each 8 reads lane 7 - i), then the
+//    quad permute [3, 2, 1, 0] (lane j reads lane 3 - j of its quad): lane i
+//    ends with lane i ^ 4;
+//  - 8: DPP row_ror:8 within each row of 16;
+//  - 16: v_permlane16_swap of the value with itself returns rows (0, 0, 2, 2)
+//    and rows (1, 1, 3, 3); a lane of row 1 or 3 takes the first, of row 0
+//    or 2 the second;
+//  - 32: v_permlane32_swap the same with halves: the upper half takes the
+//    lower half's values and the lower half the upper's.
+template <int kMask>
+__device__ __forceinline__ int xor_lane_bits(int x) {
+  static_assert(kMask == 1 || kMask == 2 || kMask == 4 || kMask == 8 || kMask == 16 || kMask == 32,
+                "a lane distance of one wave64 butterfly step");
+  if constexpr (kMask == 1) {
+    return __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
+  } else if constexpr (kMask == 2) {
+    return __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+  } else if constexpr (kMask == 4) {
+    const int mirrored = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, true);  // row_half_mirror
+    return __builtin_amdgcn_update_dpp(0, mirrored, 0x1B, 0xF, 0xF, true);          // quad_perm [3,2,1,0]
+  } else if constexpr (kMask == 8) {
+    return __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true);  // row_ror:8
+  } else if constexpr (kMask == 16) {
+    const auto rows = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(x), static_cast<unsigned>(x), false,
+                                                       false);
+    return static_cast<int>((threadIdx.x & 16u) ? rows[0] : rows[1]);
+  } else {
+    const auto halves = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(x), static_cast<unsigned>(x), false,
+                                                         false);
+    return static_cast<int>((threadIdx.x & 32u) ? halves[0] : halves[1]);
+  }
+}
+
 template <int kMask>
 __device__ __forceinline__ float xor_lane(float v) {
-  const int x = __builtin_bit_cast(int, v);
-  int r;
-  if constexpr (kMask == 1) {
-    r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
-  } else if constexpr (kMask == 2) {
-    r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
-  } else if constexpr (kMask == 8) {
-    r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true);  // row_ror:8
-  } else if constexpr (kMask == 4 || kMask == 16) {
-    r = __builtin_amdgcn_ds_swizzle(x, (kMask << 10) | 0x1F);      // xor mode
-  } else {
-    r = __shfl_xor(x, kMask, 64);
-  }
-  return __builtin_bit_cast(float, r);
+  return __builtin_bit_cast(float, xor_lane_bits<kMask>(__builtin_bit_cast(int, v)));
 }
 
 // Butterfly over the 64 lanes of a wavefront, offsets 32, 16, 8, 4, 2, 1.

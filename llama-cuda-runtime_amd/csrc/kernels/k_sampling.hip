@@ -68,9 +68,12 @@ __device__ __forceinline__ int wave_inclusive_scan_int(int v) {
 }
 
 __device__ __forceinline__ int wave_sum_int(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += xor_lane_bits<32>(v);
+  v += xor_lane_bits<16>(v);
+  v += xor_lane_bits<8>(v);
+  v += xor_lane_bits<4>(v);
+  v += xor_lane_bits<2>(v);
+  return v + xor_lane_bits<1>(v);
 }
 
 // The maximum logit from the argmax blocks' partial keys (exact in any

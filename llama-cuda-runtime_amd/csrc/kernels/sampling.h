@@ -60,14 +60,20 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
   return a > b ? a : b;
 }
 
+template <int O>
+__device__ __forceinline__ unsigned long long max_with_lane(unsigned long long v) {
+  const uint32_t lo = static_cast<uint32_t>(xor_lane_bits<O>(static_cast<int>(static_cast<uint32_t>(v))));
+  const uint32_t hi = static_cast<uint32_t>(xor_lane_bits<O>(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+  return umax64(v, (static_cast<unsigned long long>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), o, 64);
-    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), o, 64);
-    v = umax64(v, (static_cast<unsigned long long>(hi) << 32) | lo);
-  }
-  return v;
+  v = max_with_lane<32>(v);
+  v = max_with_lane<16>(v);
+  v = max_with_lane<8>(v);
+  v = max_with_lane<4>(v);
+  v = max_with_lane<2>(v);
+  return max_with_lane<1>(v);
 }
 
 // Maximum key over a block (any size that is a multiple of 64, at most 1024).

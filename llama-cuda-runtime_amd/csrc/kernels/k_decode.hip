@@ -33,6 +33,15 @@ constexpr int kQkvRowsPerWave = 2;   // rows per qkv wave (separate kernel and s
 // compute units (192 blocks of 16 rows; 96 blocks of 32 rows measured
 // 9.7 -> 11.2 us for the grid).
 constexpr int kExchangeQkvRows = LCR_EXCHANGE_QKV_ROWS;
+// Ticks of the 100 MHz realtime counter (1 us) that the one-split grid's
+// o_proj blocks wait before requesting their weight rows. The blocks that
+// are dispatched with the first wave of the grid (the grid has more blocks
+// than compute units) would otherwise stream their rows beside the q/k/v
+// rows at the head of the grid's dependency chain; their output is needed
+// only after attention, about 7 us in. Measured in one session: 0.5344 ms
+// per token without the wait, 0.5317 with it (0.5322 when only blocks that
+// can be in the first wave wait; 2 us: slower).
+constexpr unsigned kOProjStartDelay = 100;
 constexpr int kOProjRowsPerWave = LCR_EXCHANGE_OPROJ_ROWS;
 constexpr int kGateUpActsPerWave = 1;  // activations (gate + up row pairs) per gate_up wave
 // Query heads per block in the long-context attention launch (with fewer
@@ -388,7 +397,7 @@ struct ExchangeStepShared {
 template <int NCH>
 __device__ __forceinline__ void oproj_block(const DecodeStepArgs& a, const elem_t* __restrict__ W,
                                             unsigned long long* words, uint32_t tag, int ob, elem_t* xs,
-                                            bool first) {
+                                            bool first, unsigned start_delay = 0) {
   constexpr int K = NCH * 512;
   constexpr int RW = kOProjRowsPerWave;
   constexpr int PER = K / 2 / kAttnThreads;  // words per lane
@@ -396,6 +405,12 @@ __device__ __forceinline__ void oproj_block(const DecodeStepArgs& a, const elem_
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   const int row0 = (ob * kAttnWaves + wave) * RW;
+  if (start_delay > 0) {
+    // Wait start_delay ticks of the 100 MHz realtime counter before
+    // requesting the weight rows (see kOProjStartDelay).
+    const unsigned long long t0 = wall_clock64();
+    while (wall_clock64() - t0 < start_delay) __builtin_amdgcn_s_sleep(2);
+  }
   GemvTile<RW, NCH> tile;
   {
     const elem_t* rows[RW];
@@ -453,7 +468,7 @@ __global__ __launch_bounds__(kAttnThreads) void qkv_attention_kernel(DecodeStepA
   if constexpr (kOProj) {
     if (b >= qkv_blocks + a.num_heads) {
       oproj_block<NCH>(a, w.o, a.exchange + a.exchange_read_offset + broadcast, tag, b - qkv_blocks - a.num_heads,
-                       sh.ox, layer == 0);
+                       sh.ox, layer == 0, kOProjStartDelay);
       return;
     }
   }

@@ -196,6 +196,11 @@ __host__ __device__ __forceinline__ void lcr_sincosf(float angle, float* s_out, 
 //    or 2 the second;
 //  - 32: v_permlane32_swap the same with halves: the upper half takes the
 //    lower half's values and the lower half the upper's.
+// The lane's index within its wave, from the hardware (any block shape).
+__device__ __forceinline__ unsigned hw_lane() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 template <int kMask>
 __device__ __forceinline__ int xor_lane_bits(int x) {
   static_assert(kMask == 1 || kMask == 2 || kMask == 4 || kMask == 8 || kMask == 16 || kMask == 32,
@@ -212,11 +217,11 @@ __device__ __forceinline__ int xor_lane_bits(int x) {
   } else if constexpr (kMask == 16) {
     const auto rows = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(x), static_cast<unsigned>(x), false,
                                                        false);
-    return static_cast<int>((threadIdx.x & 16u) ? rows[0] : rows[1]);
+    return static_cast<int>((hw_lane() & 16u) ? rows[0] : rows[1]);
   } else {
     const auto halves = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(x), static_cast<unsigned>(x), false,
                                                          false);
-    return static_cast<int>((threadIdx.x & 32u) ? halves[0] : halves[1]);
+    return static_cast<int>((hw_lane() & 32u) ? halves[0] : halves[1]);
   }
 }
 

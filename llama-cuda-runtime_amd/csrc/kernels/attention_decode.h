@@ -82,8 +82,6 @@ struct AttnShared {
   float wave_m[kAttnWaves][kHeads];
   float wave_l[kAttnWaves][kHeads];
   float wave_acc[kAttnWaves][kHeads][kHeadDim];
-  float scale[kHeads][kAttnWaves];  // c_w of step 7
-  float merged_m[kHeads];           // M of step 7
   // Paged layout: the 16-byte-chunk index of position begin + i of the
   // block's range (chunk 0 of that position's key and value rows).
   uint32_t chunks[kPaged ? kAttnPositionTable : 1];
@@ -625,25 +623,24 @@ __device__ __forceinline__ void decode_attention_block(
   }
   __syncthreads();
 
-  // Step 7: the wave factors of every head in parallel, then every output.
-  if (static_cast<int>(threadIdx.x) < G * kAttnWaves) {
-    const int g = threadIdx.x / kAttnWaves;
-    const int w = threadIdx.x % kAttnWaves;
-    float tm = sh.wave_m[0][g];
-#pragma unroll
-    for (int v = 1; v < kAttnWaves; ++v) tm = fmaxf(tm, sh.wave_m[v][g]);
-    sh.scale[g][w] = lcr_expf(sh.wave_m[w][g] - tm);
-    if (w == 0) sh.merged_m[g] = tm;
-  }
-  __syncthreads();
+  // Step 7, inside each wave: a head's outputs are whole waves (kHeadDim is
+  // a multiple of 64), and every lane of such a wave takes the maximum of the
+  // head's wave maxima; lane w computes c_w, which the wave's lanes read by
+  // readlane. No barrier separates the factors from the outputs.
+  static_assert(kHeadDim % 64 == 0 && kAttnWaves <= 64, "a head's outputs are whole waves");
   for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kAttnThreads) {
     const int g = idx / kHeadDim;
     const int d = idx % kHeadDim;
+    float tm = sh.wave_m[0][g];
+#pragma unroll
+    for (int v = 1; v < kAttnWaves; ++v) tm = fmaxf(tm, sh.wave_m[v][g]);
+    const float c_lane = lcr_expf(sh.wave_m[lane % kAttnWaves][g] - tm);
     float tl = 0.0f, merged = 0.0f;
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) {
-      tl = __builtin_fmaf(sh.wave_l[w][g], sh.scale[g][w], tl);
-      merged = __builtin_fmaf(sh.scale[g][w], sh.wave_acc[w][g][d], merged);
+      const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c_lane), w));
+      tl = __builtin_fmaf(sh.wave_l[w][g], c, tl);
+      merged = __builtin_fmaf(c, sh.wave_acc[w][g][d], merged);
     }
     const int head = head0 + g;
     if (splits == 1) {
@@ -653,7 +650,10 @@ __device__ __forceinline__ void decode_attention_block(
         // kHeadDim is a multiple of 64, so a lane and its odd neighbour hold
         // outputs d and d + 1 of the same wave.
         const uint32_t bits = e.bits;
-        const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1));
+        // lane + 1's bits (DPP row_shl:1; the even lanes that use it read
+        // inside their row of 16)
+        const uint32_t next = static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(0, static_cast<int>(bits), 0x101, 0xF, 0xF, true));
         if (x->out_words != nullptr && (d & 1) == 0) {
           exchange_put_tagged(x->out_words + (static_cast<size_t>(head) * kHeadDim + d) / 2, x->tag,
                               bits | (next << 16));
@@ -662,7 +662,7 @@ __device__ __forceinline__ void decode_attention_block(
     } else {
       float* slot = partials + (static_cast<size_t>(head) * splits + split) * (kPartialHeader + kHeadDim);
       if (d == 0) {
-        slot[0] = sh.merged_m[g];
+        slot[0] = tm;
         slot[1] = tl;
       }
       slot[kPartialHeader + d] = merged;
@@ -731,7 +731,8 @@ __device__ __forceinline__ void merge_split_partials(elem_t* __restrict__ out,
     if (out_words != nullptr) {
       // d and d + 1 are neighbouring lanes of one wave (whole waves of d).
       const uint32_t bits = e.bits;
-      const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1));
+      const uint32_t next = static_cast<uint32_t>(
+          __builtin_amdgcn_update_dpp(0, static_cast<int>(bits), 0x101, 0xF, 0xF, true));  // lane + 1 (row_shl:1)
       if ((d & 1) == 0) {
         exchange_put_tagged(out_words + (static_cast<size_t>(head) * head_dim + d) / 2, tag, bits | (next << 16));
       }

@@ -47,6 +47,9 @@ typedef struct lcr_model_options {
                            streams the o_proj and gate/up weights while the q/k/v -> attention
                            -> o_proj chain runs (default 0: slower than the three kernels it
                            replaces on MI355X; used when asked and the device holds the grid) */
+  int exchange_head;    /* extension: the greedy step's argmax runs in the output head's grid,
+                           its blocks' maxima exchanged in-grid, instead of in a one-block
+                           kernel after it (default 1; used with the one-split exchange grid) */
 } lcr_model_options;
 
 /* ForwardStats (src/model.h:46-58) plus sizes. */
@@ -117,9 +120,10 @@ int lcr_model_generate_sampled(lcr_model* model, int32_t first_token, int steps,
 /* extension: the split count decode uses at a sequence length. */
 int lcr_model_decode_splits(const lcr_model* model, int seq_len);
 /* extension: times one fused decode kernel in isolation ("qkv", "attention",
- * "o_proj", "gate_up", "down", "lm_head", or "argmax": the reduction of the
- * head's per-block keys to the id alone) over `launches` launches on the
- * model's stream, each between its own pair of hipEvents, cycling through the
+ * "o_proj", "gate_up", "down", "lm_head", "argmax": the reduction of the
+ * head's per-block keys to the id alone in its own kernel, or "head": the
+ * output head with the argmax as the decode step runs them) over `launches`
+ * launches on the model's stream, each between its own pair of hipEvents, cycling through the
  * layers; returns the mean duration (ms) and the algorithmic bytes per launch.
  * Call after a prefill or decode. The kernels write their usual outputs (the
  * qkv kernel rewrites the cache at the last position), so the sequence is not

@@ -102,6 +102,7 @@ class ModelOptions(ctypes.Structure):
         ("exchange_spins", ctypes.c_int),
         ("exchange_test_unwritten", ctypes.c_int),
         ("layer_grid", ctypes.c_int),
+        ("exchange_head", ctypes.c_int),
     ]
 
 

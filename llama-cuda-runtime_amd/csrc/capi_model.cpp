@@ -44,6 +44,7 @@ extern "C" void lcr_model_default_options(lcr_model_options* o) {
   o->exchange_spins = 1 << 20;
   o->exchange_test_unwritten = 0;
   o->layer_grid = 0;
+  o->exchange_head = 1;
 }
 
 extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* options,
@@ -70,6 +71,7 @@ extern "C" int lcr_model_create(const char* model_dir, const lcr_model_options* 
     opt.exchange_spins = o.exchange_spins > 0 ? o.exchange_spins : (1 << 20);
     opt.exchange_test_unwritten = o.exchange_test_unwritten != 0;
     opt.layer_grid = o.layer_grid != 0;
+    opt.exchange_head = o.exchange_head != 0;
     auto handle = std::make_unique<lcr_model>();
     handle->impl = std::make_unique<Model>(model_dir, opt);
     *out = handle.release();

@@ -78,6 +78,7 @@ struct DecodeStepArgs {
   bool exchange_single;
   bool exchange_oproj;
   bool exchange_split;
+  bool exchange_head;        // the greedy step's argmax in the output head's grid
   int exchange_slots;        // blocks of the split grid the device holds at once
   int* exchange_status;      // [1] raised by a wait that gave up (host-coherent memory)
   int exchange_spins;        // polls before a wait gives up

@@ -17,6 +17,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kLmHeadMaxBlocks = 1024;
+// Output-head grids of up to this many blocks fold the argmax into block 0.
+constexpr int kLmHeadFoldMaxBlocks = 256;
 constexpr int kLmHeadRows = 2;  // rows per wave per group
 constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
 constexpr int kDownWaves = 1;   // waves (rows) per down block
@@ -963,7 +965,17 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(DecodeStepArgs a, Lay
 // 6. Output head: final norm, fp32 logits, argmax partials
 // ---------------------------------------------------------------------------
 
-template <int NCH>
+// kFold: the step's argmax runs in block 0 of this grid instead of in
+// argmax_step_kernel. Every block publishes its key as two tagged words (its
+// high and low halves, written by two lanes with one store instruction);
+// block 0's first wave waits for all of them (bounded; every block of the
+// grid is resident at once, one per compute unit, and only block 0 waits),
+// takes the maximum and does argmax_step_kernel's writes. The words are in
+// the q/k/v broadcast region, under the step's last tag slot, which no layer
+// of a step uses.
+constexpr int kHeadTagSlot = kExchangeTagSlots - 1;
+
+template <int NCH, bool kFold>
 __global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
   constexpr int H = NCH * 512;
   constexpr int GROUP_ROWS = kWaves * kLmHeadRows;
@@ -972,6 +984,8 @@ __global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
   __shared__ unsigned long long lds_best[16];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
+  uint32_t tag = 0;
+  if constexpr (kFold) tag = (*a.epoch) * static_cast<uint32_t>(kExchangeTagSlots) + kHeadTagSlot + 1u;
   const int groups = (a.vocab + GROUP_ROWS - 1) / GROUP_ROWS;
   const int stride = gridDim.x;
 
@@ -1032,6 +1046,50 @@ __global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
   }
   best = block_max_u64(best, lds_best);
   if (threadIdx.x == 0) a.argmax_partials[blockIdx.x] = best;
+  if constexpr (kFold) {
+    unsigned long long* words = a.exchange + exchange_qkv_word(a.num_heads, a.head_dim);
+    if (threadIdx.x < 2) {
+      exchange_put_tagged(words + 2 * blockIdx.x + threadIdx.x, tag,
+                          threadIdx.x == 0 ? static_cast<uint32_t>(best >> 32) : static_cast<uint32_t>(best));
+    }
+    if (blockIdx.x == 0 && wave == 0) {
+      constexpr int kPer = 2 * kLmHeadFoldMaxBlocks / 64;  // words per lane
+      const int n = 2 * static_cast<int>(gridDim.x);
+      unsigned long long* read = words + a.exchange_read_offset;
+      uint32_t bits[kPer];
+      exchange_wait_tagged_at<kPer>(
+          [&](int k) {
+            const int i = lane + 64 * k;
+            return read + (i < n ? i : 0);
+          },
+          tag, bits, a.exchange_spins, a.exchange_status);
+      // From this block's own key, so that a wait that gave up (its words then
+      // hold anything) still leaves a real key in the maximum.
+      unsigned long long key = best;
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        // Word 2b is block b's high half, 2b + 1 its low half: lane + 1's word.
+        const uint32_t low = static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(0, static_cast<int>(bits[k]), 0x101, 0xF, 0xF, true));  // row_shl:1
+        if ((lane & 1) == 0 && lane + 64 * k < n) {
+          key = umax64(key, (static_cast<unsigned long long>(bits[k]) << 32) | low);
+        }
+      }
+      key = wave_max_u64(key);
+      if (lane == 0) {
+        // The next step reads the embedding row of this id: after a wait that
+        // gave up (the step is reported as failed) the id must still be a row.
+        const int32_t id = static_cast<int32_t>(
+            min(static_cast<uint32_t>(argmax_id(key)), static_cast<uint32_t>(a.vocab - 1)));
+        const int pos = *a.position;
+        *a.sampled = id;
+        *a.next_token = id;
+        if (pos + 1 < a.history_len) a.history[pos + 1] = id;
+        *a.position = pos + 1;
+        *a.epoch = *a.epoch + 1u;
+      }
+    }
+  }
 }
 
 // The block maxima are reduced by a separate one-block kernel rather than by
@@ -1307,7 +1365,7 @@ void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
 
 void enqueue_decode_head_sampled(const DecodeStepArgs& a, const SampledHead& h, hipStream_t s) {
   const int blocks = lm_head_blocks(a.vocab, a.compute_units);
-  lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a);
+  lm_head_kernel<4, false><<<blocks, kThreads, 0, s>>>(a);
   HIP_CHECK_LAUNCH();
   SampleStepState step;
   step.uniforms = h.uniforms;
@@ -1329,7 +1387,15 @@ void enqueue_decode_argmax(const DecodeStepArgs& a, hipStream_t s) {
 
 void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t s, bool with_argmax) {
   const int blocks = lm_head_blocks(a.vocab, a.compute_units);
-  lm_head_kernel<4><<<blocks, kThreads, 0, s>>>(a);
+  // With the one-split exchange grid's words (the model's geometry and device
+  // run it), the argmax folds into the head's grid.
+  if (with_argmax && a.exchange_head && a.exchange != nullptr && a.epoch != nullptr &&
+      blocks <= kLmHeadFoldMaxBlocks && blocks <= a.compute_units) {
+    lm_head_kernel<4, true><<<blocks, kThreads, 0, s>>>(a);
+    HIP_CHECK_LAUNCH();
+    return;
+  }
+  lm_head_kernel<4, false><<<blocks, kThreads, 0, s>>>(a);
   HIP_CHECK_LAUNCH();
   if (!with_argmax) return;
   argmax_step_kernel<<<1, kThreads, 0, s>>>(a, blocks);

@@ -382,6 +382,7 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.compute_units = multiprocessors_;
   a.exchange = exchange_in_use() ? exchange_words_ : nullptr;
   a.exchange_single = exchange_enabled_;
+  a.exchange_head = exchange_enabled_ && options_.exchange_head;
   a.layer_grid = layer_grid_enabled_;
   a.exchange_oproj = exchange_oproj_;
   a.exchange_split = exchange_split_slots_ > 0;
@@ -640,6 +641,7 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
   const int seq_len = position_;  // attention reads the positions present
   unsigned mask = 0;
   bool argmax_only = false;
+  bool head_with_argmax = false;
   double bytes = 0.0;
   if (kernel == "qkv") {
     mask = kDecodeQkv;
@@ -678,6 +680,12 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
   } else if (kernel == "argmax") {
     argmax_only = true;
     bytes = 8.0 * lm_head_blocks(config_.vocab_size, multiprocessors_) + 3 * 4;
+  } else if (kernel == "head") {
+    // The output head as the step runs it: lm_head and the argmax (folded
+    // into lm_head's grid when the step exchanges words, else the one-block
+    // kernel after it).
+    head_with_argmax = true;
+    bytes = V * H * e + H * e + H * 4 + V * 4 + 8.0 * lm_head_blocks(config_.vocab_size, multiprocessors_) + 3 * 4;
   } else {
     LCR_FAIL("unknown decode kernel \"" << kernel << "\"");
   }
@@ -701,7 +709,7 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
       if (argmax_only) {
         enqueue_decode_argmax(args, stream_);
       } else if (mask == 0) {
-        enqueue_decode_head(args, stream_, false);
+        enqueue_decode_head(args, stream_, head_with_argmax);
       } else {
         const LayerWeights& lw = layers_[static_cast<size_t>(layer)];
         LayerDevicePtrs w{lw.input_norm, lw.qkv_proj, lw.o_proj, lw.post_attention_norm,

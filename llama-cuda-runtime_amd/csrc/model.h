@@ -79,6 +79,9 @@ class Model {
     // by default: measured 32.8-34.5 us per layer on MI355X against 28.4 us
     // for the exchange grid, gate_up and down kernels it replaces.
     bool layer_grid = false;
+    // The greedy step's argmax in the output head's grid (kernels/k_decode.hip,
+    // lm_head_kernel<..., true>), when the one-split exchange grid is in use.
+    bool exchange_head = true;
   };
 
   // Prompt chunks shorter than this run token by token through the decode
@@ -150,7 +153,9 @@ class Model {
   // different weights, each bracketed by its own pair of hipEvents. Returns
   // the mean launch duration in ms and the algorithmic bytes one launch moves.
   // kernel: "qkv", "attention", "o_proj", "gate_up", "down", "lm_head",
-  // "argmax" (the reduction of the head's per-block keys to the id alone),
+  // "argmax" (the reduction of the head's per-block keys to the id alone, in
+  // its own kernel), "head" (lm_head and the argmax as the step runs them:
+  // the argmax folded into lm_head's grid when the step exchanges words),
   // "qkv_attention" or "qkv_attention_oproj" (the exchange grids, or the
   // kernels that run in their place), "layer" (a whole layer: the layer grid,
   // or the kernels that run in its place).

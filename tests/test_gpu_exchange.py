@@ -114,8 +114,11 @@ def test_exchange_group_sizes(lcr, tmp_path_factory, kv_heads, paged):
         expect_bits_equal(g.view(np.uint32), e.view(np.uint32), f"group {32 // kv_heads} step {s}")
 
 
-def test_exchange_generate_greedy_matches_oracle(lcr, small_ckpt):
-    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=256, prefill_via_decode=1)
+@pytest.mark.parametrize("head", [1, 0])
+def test_exchange_generate_greedy_matches_oracle(lcr, small_ckpt, head):
+    """40 device-fed greedy steps, with the argmax folded into the output
+    head's grid (head=1, the default) and in its own kernel after it."""
+    m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=256, prefill_via_decode=1, exchange_head=head)
     o = oracle.OracleModel(small_ckpt, max_seq=256, multiprocessors=m.stats().multiprocessors)
     prompt = lcr.synthetic_tokens(20, m.vocab, seed=5)
     first = oracle.argmax(m.logits(m.prefill(prompt)))
@@ -240,7 +243,7 @@ def test_split_exchange_wait_gives_up(lcr, small_ckpt):
     fewer splits run the separate kernels, which wait on nothing; position 0
     runs the one-split grid."""
     m = lcr.Model(small_ckpt, **NO_LAYER_GRID, max_seq=128, prefill_via_decode=1, attention_splits=8, exchange_spins=4,
-                  exchange_test_unwritten=1)
+                  exchange_test_unwritten=1, exchange_head=0)
     heads, qkv_blocks = 32, (32 + 2 * 8) * 64 // 16
     first_split_grid = next(p for p in range(1, 8) if heads * m.decode_splits(p + 1) >= qkv_blocks)
     assert first_split_grid == 5
@@ -253,3 +256,34 @@ def test_split_exchange_wait_gives_up(lcr, small_ckpt):
     with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
         m.decode(2)
     assert m.exchange_status()[1] == 0
+
+
+@pytest.mark.parametrize("graph", [1, 0])
+def test_exchange_head_wait_gives_up(lcr, small_ckpt, graph):
+    """The output head's folded argmax waits for every head block's maximum.
+    At positions 1-4 with 8 forced splits the layers run the separate kernels,
+    which wait on nothing, so a step there fails only through the head's wait
+    (pointed at words no block writes): with the fold it gives up and decode()
+    and generate_greedy fail; without it the same steps succeed. A step whose
+    wait gave up still hands the next step a token id inside the vocabulary
+    (the device-fed loop reads that id's embedding row)."""
+    kw = dict(max_seq=128, prefill_via_decode=1, attention_splits=8, exchange_spins=4, exchange_test_unwritten=1,
+              use_graph=graph, **NO_LAYER_GRID)
+    plain = lcr.Model(small_ckpt, exchange_head=0, **kw)
+    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+        plain.prefill([3])  # position 0 runs the one-split grid
+    for _ in range(4):
+        plain.decode(2)
+    assert plain.exchange_status()[1] == 0
+    plain.close()
+    m = lcr.Model(small_ckpt, **kw)
+    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+        m.prefill([3])
+    assert m.position == 1
+    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+        m.decode(2)
+    assert m.exchange_status()[1] == 0
+    with pytest.raises(lcr.LcrError, match="exchange wait gave up"):
+        m.generate_greedy(2, 2)
+    assert m.exchange_status()[1] == 0
+    m.close()

@@ -230,7 +230,7 @@ def test_time_decode_kernel(lcr, small_ckpt):
     and written); an unknown kernel is an argument error."""
     m = lcr.Model(small_ckpt, max_seq=64)
     m.prefill(list(range(1, 9)))
-    for name in ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax"):
+    for name in ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax", "head"):
         ms, nbytes = m.time_decode_kernel(name, 8)
         assert ms > 0.0 and nbytes > 0.0, name
     assert m.time_decode_kernel("o_proj", 4)[1] == 2048 * 2048 * 2 + 2048 * 2 + 2 * 2048 * 4

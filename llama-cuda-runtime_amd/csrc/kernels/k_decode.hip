@@ -21,7 +21,12 @@ constexpr int kLmHeadMaxBlocks = 1024;
 constexpr int kLmHeadFoldMaxBlocks = 256;
 constexpr int kLmHeadRows = 2;  // rows per wave per group
 constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
-constexpr int kDownWaves = 1;   // waves (rows) per down block
+// Waves (rows) per down block. Measured on the whole step (255 graph-replayed
+// greedy steps, two rounds): 1 wave 0.5276 / 0.5281 ms, 2 waves 0.5244 /
+// 0.5246, 4 waves 0.5252 / 0.5254, 8 waves 0.5267, 16 waves 0.565. Staging
+// the activation in LDS once per block instead of every wave reading it from
+// the cache measured slower at 2, 4 and 8 waves (0.5294-0.5307 ms).
+constexpr int kDownWaves = 2;
 constexpr int kQkvRowsPerWave = 2;   // rows per qkv wave (separate kernel and split grid)
 #ifndef LCR_EXCHANGE_QKV_ROWS
 #define LCR_EXCHANGE_QKV_ROWS 2
@@ -46,6 +51,12 @@ constexpr int kExchangeQkvRows = LCR_EXCHANGE_QKV_ROWS;
 constexpr unsigned kOProjStartDelay = 100;
 constexpr int kOProjRowsPerWave = LCR_EXCHANGE_OPROJ_ROWS;
 constexpr int kGateUpActsPerWave = 1;  // activations (gate + up row pairs) per gate_up wave
+// Waves per gate_up block (at least kThreads / 64: the norm's threads). Each
+// block repeats the norm, so fewer, larger blocks would repeat it less; the
+// whole step measured slower with them (two rounds): 4 waves 0.5221 / 0.5226
+// ms, 8 waves 0.5265 / 0.5267, 16 waves 0.5309 / 0.5306, and two activations
+// per wave at 4 waves 0.5322 / 0.5324.
+constexpr int kGateUpWaves = 4;
 // Query heads per block in the long-context attention launch (with fewer
 // than G, the heads of one kv head are spread over G / kLongContextHeads
 // blocks on one XCD, which share its keys and values in L2). The whole group
@@ -927,14 +938,15 @@ __global__ __launch_bounds__(WAVES * 64) void proj_residual_kernel(DecodeStepArg
 // ---------------------------------------------------------------------------
 
 template <int NCH>
-__global__ __launch_bounds__(kThreads) void gate_up_kernel(DecodeStepArgs a, LayerDevicePtrs w) {
+__global__ __launch_bounds__(kGateUpWaves * 64) void gate_up_kernel(DecodeStepArgs a, LayerDevicePtrs w) {
+  static_assert(kGateUpWaves * 64 >= kThreads, "the norm takes the block's first kThreads threads");
   constexpr int H = NCH * 512;
   __shared__ __attribute__((aligned(16))) elem_t xs[H];
-  __shared__ float scratch[9];
+  __shared__ float scratch[kGateUpWaves * 2 + 1];  // one float per 32 threads
   constexpr int A = kGateUpActsPerWave;
   const int lane = lane_id();
   // First activation index of this wave.
-  const int i = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * A;
+  const int i = (blockIdx.x * kGateUpWaves + (threadIdx.x >> 6)) * A;
   NormInput<NCH> nin;
   norm_load<NCH>(nin, [&](int chunk, float* out) { load_resid_chunk(a.resid, chunk, out); },
                  w.post_norm);
@@ -1190,7 +1202,7 @@ void enqueue_layer_typed(const DecodeStepArgs& a, const LayerDevicePtrs& w, cons
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeGateUp) {
-    gate_up_kernel<NCH><<<a.ffn / (kWaves * kGateUpActsPerWave), kThreads, 0, s>>>(a, w);
+    gate_up_kernel<NCH><<<a.ffn / (kGateUpWaves * kGateUpActsPerWave), kGateUpWaves * 64, 0, s>>>(a, w);
     HIP_CHECK_LAUNCH();
   }
   if (mask & kDecodeDown) {

@@ -14,7 +14,10 @@ and a smaller vocabulary so the oracle finishes in seconds. On it:
   - activation taps: an MFMA prefill's within the reference validator's
     bounds of the oracle's, an unfused decode step's bit for bit;
   - the fused step for groups of 1, 2, 4 and 8 query heads per kv head, per
-    head and whole-group attention blocks, both cache layouts.
+    head and whole-group attention blocks, both cache layouts;
+  - two layer shapes the fused step does not cover (head_dim 128 at hidden
+    2048; a narrow hidden 512 / ffn 1536 model), through the unfused kernel
+    sequence, bit for bit.
 """
 
 import numpy as np
@@ -98,6 +101,35 @@ def test_decode_bit_exact_group_sizes(lcr, tmp_path_factory, kv_heads, splits, p
     assert m.stats().fused == 1
     prompt = lcr.synthetic_tokens(40, m.vocab, seed=kv_heads)
     run_steps(m, o, prompt, 4, check_every=1)
+
+
+# Layer shapes other than Llama-3.2-1B's. The fused decode kernels are
+# compiled for hidden 2048, ffn 8192 and head_dim 64, so these run the unfused
+# kernel sequence (the reference's run_layers order, src/model.cu:370-484).
+OTHER_GEOMETRIES = {
+    # head_dim 128 at the same width: 16 query heads over 8 kv heads
+    "hd128": dict(hidden_size=2048, intermediate_size=8192, num_attention_heads=16, num_key_value_heads=8,
+                  head_dim=128),
+    # a narrow model: hidden 512, ffn 1536, 8 query heads over 2 kv heads
+    "narrow": dict(hidden_size=512, intermediate_size=1536, num_attention_heads=8, num_key_value_heads=2,
+                   head_dim=64),
+}
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("geometry", sorted(OTHER_GEOMETRIES))
+def test_decode_bit_exact_other_geometries(lcr, tmp_path_factory, geometry, paged):
+    """Logits bit-identical to the oracle's at every step, with one and with
+    four attention splits, on layer shapes the fused step does not cover."""
+    d = tmp_path_factory.mktemp(f"geometry_{geometry}")
+    ckpt = lcr.write_synthetic_checkpoint(d, lcr.llama_config(**SMALL, **OTHER_GEOMETRIES[geometry]))
+    for splits in (0, 4):
+        m, o = make_pair(lcr, ckpt, max_seq=256, splits=splits, paged=paged, prefill_via_decode=1)
+        assert m.stats().fused == 0
+        prompt = lcr.synthetic_tokens(70, m.vocab, seed=len(geometry) + splits)
+        run_steps(m, o, prompt, 6, check_every=1)
+        m.close()
+        o.close()
 
 
 def test_paged_tables_match_oracle(lcr, small_ckpt):

@@ -262,6 +262,7 @@ void Model::allocate_arena() {
 
 void Model::reset() {
   position_ = 0;
+  step_argmax_ready_ = false;
   taps_.clear();
 }
 
@@ -302,6 +303,7 @@ const float* Model::prefill(const std::vector<int>& tokens) {
     LCR_CHECK(t >= 0 && t < config_.vocab_size,
               "token id " << t << " is outside the vocabulary of " << config_.vocab_size);
   }
+  step_argmax_ready_ = false;
   if (options_.prefill_via_decode) {
     GpuTimer timer;
     timer.start(stream_);
@@ -329,6 +331,7 @@ const float* Model::prefill(const std::vector<int>& tokens) {
     kv_cache_->reserve_length(position_ + chunk);
     launch_embedding_lookup(x_, embedding_, token_ids_, chunk, config_.hidden_size, stream_);
     run_layers(chunk, position_);
+    step_argmax_ready_ = false;  // the chunk's logits, without their argmax
     position_ += chunk;
     consumed += static_cast<size_t>(chunk);
     // The ids buffer above is pageable host memory read by the async copy.
@@ -477,10 +480,12 @@ const float* Model::decode(int token) {
             "sequence reached " << position_ << " positions, the cache limit");
   LCR_CHECK(token >= 0 && token < config_.vocab_size,
             "token id " << token << " is outside the vocabulary of " << config_.vocab_size);
+  step_argmax_ready_ = false;
+  const bool fused_step = fused_ && !capture_activations_;
   GpuTimer timer;
   timer.start(stream_);
   kv_cache_->reserve_length(position_ + 1);
-  if (fused_ && !capture_activations_) {
+  if (fused_step) {
     write_step_state(token);
     launch_fused_step(position_ + 1);
   } else {
@@ -495,6 +500,7 @@ const float* Model::decode(int token) {
   HIP_CHECK(hipStreamSynchronize(stream_));
   stats_.last_decode_ms = timer.elapsed_ms();
   check_exchange();
+  step_argmax_ready_ = fused_step;
   if (profiler_.enabled()) profiler_.collect();
   return logits_;
 }
@@ -532,6 +538,7 @@ void Model::launch_sampled_step(int seq_len) {
 std::vector<int> Model::generate_sampled(int first_token, int steps, float temperature, int top_k,
                                          float top_p, const float* uniforms, double* elapsed_ms) {
   LCR_CHECK(fused_, "device-side sampled generation needs the fused decode path");
+  step_argmax_ready_ = false;
   LCR_CHECK(steps >= 0, "steps must be non-negative");
   LCR_CHECK(temperature > 0.0f, "sampled generation needs a positive temperature (greedy: generate_greedy)");
   LCR_CHECK(top_p > 0.0f && top_p <= 1.0f, "top_p must be in (0, 1], got " << top_p);
@@ -590,6 +597,7 @@ std::vector<int> Model::generate_sampled(int first_token, int steps, float tempe
 
 std::vector<int> Model::generate_greedy(int first_token, int steps, double* elapsed_ms) {
   LCR_CHECK(fused_, "device-side greedy generation needs the fused decode path");
+  step_argmax_ready_ = false;
   LCR_CHECK(steps >= 0, "steps must be non-negative");
   LCR_CHECK(first_token >= 0 && first_token < config_.vocab_size,
             "token id " << first_token << " is outside the vocabulary of " << config_.vocab_size);
@@ -633,6 +641,7 @@ std::vector<int> Model::generate_greedy(int first_token, int steps, double* elap
 double Model::time_decode_kernel(const std::string& kernel, int launches,
                                  double* bytes_per_launch) {
   LCR_CHECK(fused_, "kernel timing needs the fused decode path");
+  step_argmax_ready_ = false;
   LCR_CHECK(launches > 0, "launches must be positive");
   LCR_CHECK(position_ > 0, "time kernels after a prefill, so the step state is valid");
   const double H = config_.hidden_size, F = config_.intermediate_size, V = config_.vocab_size;
@@ -912,8 +921,14 @@ void Model::capture(const std::string& name, const elem_t* source, int tokens, i
 
 int Model::sample(const float* device_logits, float temperature, int top_k, float top_p,
                   float uniform) {
-  launch_sample(sampled_id_, device_logits, config_.vocab_size, temperature, top_k, top_p, uniform,
-                attention_scratch_, stream_);
+  // A greedy pick of the logits the last fused decode step wrote reads the id
+  // that step's output head already computed; anything else runs the sampler.
+  const bool own_logits = device_logits == logits_;
+  if (!(temperature <= 0.0f && own_logits && step_argmax_ready_)) {
+    launch_sample(sampled_id_, device_logits, config_.vocab_size, temperature, top_k, top_p, uniform,
+                  attention_scratch_, stream_);
+    step_argmax_ready_ = temperature <= 0.0f && own_logits;
+  }
   int32_t id = 0;
   HIP_CHECK(hipMemcpyAsync(&id, sampled_id_, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
   HIP_CHECK(hipStreamSynchronize(stream_));

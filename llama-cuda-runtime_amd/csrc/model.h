@@ -278,6 +278,11 @@ class Model {
   ForwardStats stats_;
   bool input_norm_done_ = false;
   bool capture_activations_ = false;
+  // sampled_id_ holds the argmax of logits_: the last call that wrote them was
+  // a fused decode step, whose output head reduces its logits to their argmax
+  // (the greedy sample's key and tie rule). A greedy sample() of logits_ then
+  // reads that id instead of launching the reduction again.
+  bool step_argmax_ready_ = false;
   std::vector<Tap> taps_;
   Profiler profiler_;
 };

@@ -132,6 +132,35 @@ def test_decode_bit_exact_other_geometries(lcr, tmp_path_factory, geometry, page
         o.close()
 
 
+def test_greedy_sample_after_each_kind_of_call(lcr, small_ckpt):
+    """sample(logits, 0) returns the argmax of the logits (lowest index on
+    ties) whichever call wrote them: an MFMA prefill (the sampler's own
+    reduction runs), a fused decode step (whose output head already reduced
+    them), a decode step followed by a stochastic sample (which overwrote the
+    device's id), and the device-side greedy loop."""
+    m, o = make_pair(lcr, small_ckpt, prefill_via_decode=0)
+    ptr = m.prefill(lcr.synthetic_tokens(80, m.vocab, seed=21))
+    tok = m.sample(ptr, 0.0)
+    assert tok == oracle.argmax(m.logits(ptr))
+    for step in range(4):
+        ptr = m.decode(tok)
+        want = oracle.argmax(m.logits(ptr))
+        assert m.sample(ptr, 0.0) == want, f"step {step}"
+        assert m.sample(ptr, 0.0) == want, f"step {step}, again"
+        drawn = m.sample(ptr, 0.8, 40, 0.95, 0.37)
+        assert 0 <= drawn < m.vocab
+        assert m.sample(ptr, 0.0) == want, f"step {step}, after a stochastic sample"
+        tok = want
+    ids, _ = m.generate_greedy(tok, 5)
+    ptr = m.decode(int(ids[-1]))
+    assert m.sample(ptr, 0.0) == oracle.argmax(m.logits(ptr))
+    m.reset()
+    ptr = m.prefill(lcr.synthetic_tokens(70, m.vocab, seed=22))
+    assert m.sample(ptr, 0.0) == oracle.argmax(m.logits(ptr))
+    m.close()
+    o.close()
+
+
 def test_paged_tables_match_oracle(lcr, small_ckpt):
     m, o = make_pair(lcr, small_ckpt, paged=True, prefill_via_decode=1)
     prompt = lcr.synthetic_tokens(40, m.vocab)

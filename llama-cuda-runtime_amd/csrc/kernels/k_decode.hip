@@ -1095,6 +1095,7 @@ __global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
             min(static_cast<uint32_t>(argmax_id(key)), static_cast<uint32_t>(a.vocab - 1)));
         const int pos = *a.position;
         *a.sampled = id;
+        if (a.sampled_host != nullptr) __hip_atomic_store(a.sampled_host, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         *a.next_token = id;
         if (pos + 1 < a.history_len) a.history[pos + 1] = id;
         *a.position = pos + 1;
@@ -1117,6 +1118,7 @@ __global__ __launch_bounds__(kThreads) void argmax_step_kernel(DecodeStepArgs a,
     const int32_t id = argmax_id(best);
     const int pos = *a.position;
     *a.sampled = id;
+    if (a.sampled_host != nullptr) __hip_atomic_store(a.sampled_host, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     *a.next_token = id;
     if (pos + 1 < a.history_len) a.history[pos + 1] = id;
     *a.position = pos + 1;

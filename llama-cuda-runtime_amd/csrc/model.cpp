@@ -52,6 +52,10 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
                           hipHostMallocCoherent | hipHostMallocMapped));
   *exchange_status_host_ = 0;
   HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&exchange_status_), exchange_status_host_, 0));
+  HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&step_id_host_), sizeof(int32_t),
+                          hipHostMallocCoherent | hipHostMallocMapped));
+  *step_id_host_ = 0;
+  HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&step_id_), step_id_host_, 0));
   allocate_arena();
 
   fused_ = options_.fused_decode &&
@@ -97,6 +101,7 @@ Model::~Model() {
   sampled_graphs_.clear();
   if (pinned_state_ != nullptr) (void)hipHostFree(pinned_state_);
   if (exchange_status_host_ != nullptr) (void)hipHostFree(exchange_status_host_);
+  if (step_id_host_ != nullptr) (void)hipHostFree(step_id_host_);
   if (stream_ != nullptr) (void)hipStreamDestroy(stream_);
   (void)hipFree(weight_block_);
   (void)hipFree(inv_freq_);
@@ -396,6 +401,7 @@ DecodeStepArgs Model::step_args(int splits) const {
                                ? static_cast<int>(decode_exchange_words(config_.num_heads, config_.head_dim) / 2)
                                : 0;
   a.epoch = epoch_;
+  a.sampled_host = step_id_;
   return a;
 }
 
@@ -921,17 +927,24 @@ void Model::capture(const std::string& name, const elem_t* source, int tokens, i
 
 int Model::sample(const float* device_logits, float temperature, int top_k, float top_p,
                   float uniform) {
-  // A greedy pick of the logits the last fused decode step wrote reads the id
-  // that step's output head already computed; anything else runs the sampler.
+  // A greedy pick of the logits the last fused decode step wrote (decode()
+  // has synchronised with it) reads the id that step's output head already
+  // wrote to host-coherent memory; anything else runs the sampler.
   const bool own_logits = device_logits == logits_;
-  if (!(temperature <= 0.0f && own_logits && step_argmax_ready_)) {
+  int32_t id = 0;
+  if (temperature <= 0.0f && own_logits && step_argmax_ready_) {
+    id = __atomic_load_n(step_id_host_, __ATOMIC_ACQUIRE);
+  } else {
+    step_argmax_ready_ = false;
     launch_sample(sampled_id_, device_logits, config_.vocab_size, temperature, top_k, top_p, uniform,
                   attention_scratch_, stream_);
-    step_argmax_ready_ = temperature <= 0.0f && own_logits;
+    HIP_CHECK(hipMemcpyAsync(&id, sampled_id_, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
+    HIP_CHECK(hipStreamSynchronize(stream_));
+    if (temperature <= 0.0f && own_logits) {
+      __atomic_store_n(step_id_host_, id, __ATOMIC_RELEASE);
+      step_argmax_ready_ = true;
+    }
   }
-  int32_t id = 0;
-  HIP_CHECK(hipMemcpyAsync(&id, sampled_id_, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
-  HIP_CHECK(hipStreamSynchronize(stream_));
   LCR_CHECK(id >= 0 && id < config_.vocab_size,
             "sampling produced token id " << id << ", outside the vocabulary");
   return static_cast<int>(id);

@@ -233,6 +233,8 @@ class Model {
   // every step ends with, at no cost to the device.
   int* exchange_status_ = nullptr;       // device address of exchange_status_host_
   int* exchange_status_host_ = nullptr;
+  int32_t* step_id_ = nullptr;       // device address of step_id_host_
+  int32_t* step_id_host_ = nullptr;  // host-coherent: the greedy step's id, written by its output head
   // Whether any exchange grid can run (its waits then need checking).
   bool exchange_in_use() const { return exchange_enabled_ || exchange_split_slots_ > 0 || layer_grid_enabled_; }
   bool layer_grid_enabled_ = false;
@@ -278,10 +280,11 @@ class Model {
   ForwardStats stats_;
   bool input_norm_done_ = false;
   bool capture_activations_ = false;
-  // sampled_id_ holds the argmax of logits_: the last call that wrote them was
-  // a fused decode step, whose output head reduces its logits to their argmax
-  // (the greedy sample's key and tie rule). A greedy sample() of logits_ then
-  // reads that id instead of launching the reduction again.
+  // step_id_host_ (and sampled_id_) hold the argmax of logits_: the last call
+  // that wrote them was a fused decode step, whose output head reduces its
+  // logits to their argmax (the greedy sample's key and tie rule) and writes
+  // the id to host-coherent memory too, or a greedy sample() of logits_. A
+  // greedy sample() of logits_ then reads that id: no kernel, no copy.
   bool step_argmax_ready_ = false;
   std::vector<Tap> taps_;
   Profiler profiler_;

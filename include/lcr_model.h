@@ -76,7 +76,9 @@ void lcr_model_destroy(lcr_model* model);
 /* Model::prefill / decode: device logits [vocab] fp32, valid until the next call. */
 int lcr_model_prefill(lcr_model* model, const int32_t* tokens, int count, const float** logits);
 int lcr_model_decode(lcr_model* model, int32_t token, const float** logits);
-/* Model::sample: temperature <= 0 is argmax; uniform in [0, 1). */
+/* Model::sample: temperature <= 0 is argmax; uniform in [0, 1). A greedy
+ * sample of the logits the last lcr_model_decode returned reads the id the
+ * decode step already computed (same key and ties), with no GPU work. */
 int lcr_model_sample(lcr_model* model, const float* logits, float temperature, int top_k,
                      float top_p, float uniform, int32_t* out_id);
 int lcr_model_logits_to_host(lcr_model* model, const float* logits, float* out);

@@ -20,6 +20,11 @@ constexpr int kLmHeadMaxBlocks = 1024;
 // Output-head grids of up to this many blocks fold the argmax into block 0.
 constexpr int kLmHeadFoldMaxBlocks = 256;
 constexpr int kLmHeadRows = 2;  // rows per wave per group
+// Waves per output-head block (at least kThreads / 64: the norm's threads).
+// Measured on the whole step (two rounds): 4 waves 0.5245 / 0.5246 ms (lm_head
+// 76.0 / 75.9 us), 8 waves 0.5324 / 0.5326 (81.2 / 81.1 us), 16 waves 0.5301 /
+// 0.5299 (79.3 / 78.9 us).
+constexpr int kLmHeadWaves = 4;
 constexpr int kOProjWaves = 4;  // waves (rows) per o_proj block
 // Waves (rows) per down block. Measured on the whole step (255 graph-replayed
 // greedy steps, two rounds): 1 wave 0.5276 / 0.5281 ms, 2 waves 0.5244 /
@@ -988,11 +993,12 @@ __global__ __launch_bounds__(kGateUpWaves * 64) void gate_up_kernel(DecodeStepAr
 constexpr int kHeadTagSlot = kExchangeTagSlots - 1;
 
 template <int NCH, bool kFold>
-__global__ __launch_bounds__(kThreads) void lm_head_kernel(DecodeStepArgs a) {
+__global__ __launch_bounds__(kLmHeadWaves * 64) void lm_head_kernel(DecodeStepArgs a) {
+  static_assert(kLmHeadWaves * 64 >= kThreads && kLmHeadWaves <= 16, "the norm takes the first kThreads threads");
   constexpr int H = NCH * 512;
-  constexpr int GROUP_ROWS = kWaves * kLmHeadRows;
+  constexpr int GROUP_ROWS = kLmHeadWaves * kLmHeadRows;
   __shared__ __attribute__((aligned(16))) elem_t xs[H];
-  __shared__ float scratch[9];
+  __shared__ float scratch[kLmHeadWaves * 2 + 1];  // one float per 32 threads
   __shared__ unsigned long long lds_best[16];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
@@ -1344,7 +1350,7 @@ int decode_split_exchange_slots(int num_heads, int num_kv_heads, int head_dim, b
 // 85 us; 1024 blocks of 15-16 groups take 91 us, and grids that leave some
 // compute units with two blocks and others with one are slower still).
 int lm_head_blocks(int vocab, int compute_units) {
-  const int groups = (vocab + kWaves * kLmHeadRows - 1) / (kWaves * kLmHeadRows);
+  const int groups = (vocab + kLmHeadWaves * kLmHeadRows - 1) / (kLmHeadWaves * kLmHeadRows);
   const int cus = std::max(1, std::min(compute_units, kLmHeadMaxBlocks));
   const int per_block = (groups + cus - 1) / cus;
   return std::max(1, (groups + per_block - 1) / per_block);
@@ -1379,7 +1385,7 @@ void enqueue_decode_layer(const DecodeStepArgs& a, const LayerDevicePtrs& w,
 
 void enqueue_decode_head_sampled(const DecodeStepArgs& a, const SampledHead& h, hipStream_t s) {
   const int blocks = lm_head_blocks(a.vocab, a.compute_units);
-  lm_head_kernel<4, false><<<blocks, kThreads, 0, s>>>(a);
+  lm_head_kernel<4, false><<<blocks, kLmHeadWaves * 64, 0, s>>>(a);
   HIP_CHECK_LAUNCH();
   SampleStepState step;
   step.uniforms = h.uniforms;
@@ -1405,11 +1411,11 @@ void enqueue_decode_head(const DecodeStepArgs& a, hipStream_t s, bool with_argma
   // run it), the argmax folds into the head's grid.
   if (with_argmax && a.exchange_head && a.exchange != nullptr && a.epoch != nullptr &&
       blocks <= kLmHeadFoldMaxBlocks && blocks <= a.compute_units) {
-    lm_head_kernel<4, true><<<blocks, kThreads, 0, s>>>(a);
+    lm_head_kernel<4, true><<<blocks, kLmHeadWaves * 64, 0, s>>>(a);
     HIP_CHECK_LAUNCH();
     return;
   }
-  lm_head_kernel<4, false><<<blocks, kThreads, 0, s>>>(a);
+  lm_head_kernel<4, false><<<blocks, kLmHeadWaves * 64, 0, s>>>(a);
   HIP_CHECK_LAUNCH();
   if (!with_argmax) return;
   argmax_step_kernel<<<1, kThreads, 0, s>>>(a, blocks);

@@ -127,7 +127,9 @@ def cpu_baseline(model_dir: Path, prompt, first: int, kv: list, steps: int, max_
     workload: greedy decode from the GPU's cache after the prompt, starting at
     the GPU's first token, so its ids are also the parity check of the timed
     sequence. All threads on up to `steps` steps (capped at
-    CPU_BASELINE_SECONDS), then one thread on a shorter sample."""
+    CPU_BASELINE_SECONDS), then one thread on a shorter sample. The oracle's
+    own free-running continuation is compared here too; this leg is the only
+    part of the bench that runs the oracle."""
     ref, oracle = oracle_from_gpu_cache(model_dir, kv, len(prompt), max_seq)
     lib = oracle.load()
     threads = lib.orc_threads()
@@ -173,6 +175,7 @@ def cpu_baseline(model_dir: Path, prompt, first: int, kv: list, steps: int, max_
         "greedy_tokens_compared": m, "identical": diverge is None, "first_divergence": diverge,
         "sequence": "the timed run's ids (MFMA prefill, then the graph-replayed decode step) against "
                     "the CPU oracle decoding from the GPU's exported KV cache: the decode kernels' parity"}}
+    parity["free_running"] = free_running_continuation(model_dir, prompt, gpu_ids, max_seq)
     return cpu, parity
 
 
@@ -641,9 +644,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         cpu, parity = cpu_baseline(model_dir, prompt, int(first), kv, args.cpu_steps, args.max_seq,
                                    bytes_per_token, timed_ids)
-        progress("CPU baseline done")
-        parity["free_running"] = free_running_continuation(model_dir, prompt, timed_ids, args.max_seq)
-        progress("free-running continuation compared")
+        progress("CPU baseline and the oracle's continuation done")
 
     result = {
         "metric": "decode tok/s + HBM GB/s (% of peak), Llama-3.2-1B-arch bf16 batch 1",

@@ -84,7 +84,8 @@ struct DecodeStepArgs {
   int exchange_spins;        // polls before a wait gives up
   int exchange_read_offset;  // added to every word the grid reads (0; 3.5X in tests of the give-up path)
   uint32_t* epoch;           // [1] steps completed; advanced by the step's last kernel
-  int32_t* sampled_host;     // [1] host-coherent: the greedy step's id as well (null: not written)
+  int32_t* sampled_host;     // [1] host-coherent: the greedy step's id as well, when *want_host_id
+  const int32_t* want_host_id;  // [1] non-zero: write sampled_host (set by the host per call)
 };
 
 // True when the fused kernels are compiled for this geometry.

@@ -43,10 +43,11 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
   HIP_CHECK(hipMemcpy(inv_freq_, inv_freq.data(), inv_freq.size() * sizeof(float),
                       hipMemcpyHostToDevice));
 
-  HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&pinned_state_), 2 * sizeof(int32_t),
+  HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&pinned_state_), 3 * sizeof(int32_t),
                           hipHostMallocDefault));
   pinned_state_[0] = 0;
   pinned_state_[1] = 0;
+  pinned_state_[2] = 0;
   // Before the arena: allocating it clears the exchange state, status included.
   HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&exchange_status_host_), sizeof(int),
                           hipHostMallocCoherent | hipHostMallocMapped));
@@ -225,7 +226,7 @@ void Model::allocate_arena() {
       T * sizeof(int32_t),                       // token_ids_
       sizeof(int32_t),                           // sampled_id_
       H * sizeof(float),                         // resid_
-      sizeof(int32_t),                           // position_dev_
+      3 * sizeof(int32_t),                       // step_state_
       kMaxLmHeadBlocks * sizeof(unsigned long long),                  // argmax_partials_
       (static_cast<size_t>(options_.max_seq) + 1) * sizeof(int32_t),  // history_
       gemm_workspace_bytes(),                                         // gemm_workspace_
@@ -250,7 +251,8 @@ void Model::allocate_arena() {
   token_ids_ = arena_.alloc<int32_t>(T);
   sampled_id_ = arena_.alloc<int32_t>(1);
   resid_ = arena_.alloc<float>(H);
-  position_dev_ = arena_.alloc<int32_t>(1);
+  step_state_ = arena_.alloc<int32_t>(3);
+  position_dev_ = step_state_ + 1;
   argmax_partials_ = arena_.alloc<unsigned long long>(kMaxLmHeadBlocks);
   history_ = arena_.alloc<int32_t>(static_cast<size_t>(options_.max_seq) + 1);
   gemm_workspace_size_ = gemm_workspace_bytes();
@@ -262,7 +264,7 @@ void Model::allocate_arena() {
   HIP_CHECK(hipMemset(epoch_, 0, sizeof(uint32_t)));
   clear_exchange();
   HIP_CHECK(hipMemset(token_ids_, 0, T * sizeof(int32_t)));
-  HIP_CHECK(hipMemset(position_dev_, 0, sizeof(int32_t)));
+  HIP_CHECK(hipMemset(step_state_, 0, 3 * sizeof(int32_t)));
 }
 
 void Model::reset() {
@@ -349,13 +351,13 @@ const float* Model::prefill(const std::vector<int>& tokens) {
   return logits_;
 }
 
-void Model::write_step_state(int token) {
+// want_host_id: the step's output head also writes its greedy id to
+// host-coherent memory (a call that returns to the host right after the step).
+void Model::write_step_state(int token, bool want_host_id) {
   pinned_state_[0] = token;
   pinned_state_[1] = position_;
-  HIP_CHECK(hipMemcpyAsync(token_ids_, &pinned_state_[0], sizeof(int32_t),
-                           hipMemcpyHostToDevice, stream_));
-  HIP_CHECK(hipMemcpyAsync(position_dev_, &pinned_state_[1], sizeof(int32_t),
-                           hipMemcpyHostToDevice, stream_));
+  pinned_state_[2] = want_host_id ? 1 : 0;
+  HIP_CHECK(hipMemcpyAsync(step_state_, pinned_state_, 3 * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
 }
 
 DecodeStepArgs Model::step_args(int splits) const {
@@ -372,10 +374,10 @@ DecodeStepArgs Model::step_args(int splits) const {
   a.lm_head = lm_head_;
   a.inv_freq = inv_freq_;
   a.rope_table = rope_table_;
-  a.token = token_ids_;
+  a.token = step_state_;
   a.position = position_dev_;
   a.sampled = sampled_id_;
-  a.next_token = token_ids_;
+  a.next_token = step_state_;
   a.history = history_;
   a.history_len = options_.max_seq + 1;
   a.resid = resid_;
@@ -402,6 +404,7 @@ DecodeStepArgs Model::step_args(int splits) const {
                                : 0;
   a.epoch = epoch_;
   a.sampled_host = step_id_;
+  a.want_host_id = step_state_ + 2;
   return a;
 }
 
@@ -492,7 +495,7 @@ const float* Model::decode(int token) {
   timer.start(stream_);
   kv_cache_->reserve_length(position_ + 1);
   if (fused_step) {
-    write_step_state(token);
+    write_step_state(token, true);
     launch_fused_step(position_ + 1);
   } else {
     pinned_state_[0] = token;
@@ -573,12 +576,12 @@ std::vector<int> Model::generate_sampled(int first_token, int steps, float tempe
   for (int s = 0; s < steps; ++s) {
     const int splits = decode_splits(start + s + 1);
     if (options_.use_graph && sampled_graphs_.find(splits) == sampled_graphs_.end()) {
-      write_step_state(first_token);
+      write_step_state(first_token, false);
       launch_sampled_step(start + s + 1);
       HIP_CHECK(hipStreamSynchronize(stream_));
     }
   }
-  write_step_state(first_token);
+  write_step_state(first_token, false);
   HIP_CHECK(hipMemsetAsync(draw_counter_, 0, sizeof(int32_t), stream_));
   HIP_CHECK(hipStreamSynchronize(stream_));
   GpuTimer timer;
@@ -621,12 +624,12 @@ std::vector<int> Model::generate_greedy(int first_token, int steps, double* elap
   for (int s = 0; s < steps; ++s) {
     const int splits = decode_splits(start + s + 1);
     if (options_.use_graph && graphs_.find(splits) == graphs_.end()) {
-      write_step_state(first_token);
+      write_step_state(first_token, false);
       launch_fused_step(start + s + 1);  // captures, then runs once at `start`
       HIP_CHECK(hipStreamSynchronize(stream_));
     }
   }
-  write_step_state(first_token);
+  write_step_state(first_token, false);
   GpuTimer timer;
   timer.start(stream_);
   for (int s = 0; s < steps; ++s) launch_fused_step(start + s + 1);

@@ -183,7 +183,7 @@ class Model {
   void attention_decode(int layer, int position);
   void capture(const std::string& name, const elem_t* source, int tokens, int width);
   void capture_f32_residual(const std::string& name);
-  void write_step_state(int token);
+  void write_step_state(int token, bool want_host_id);
   void enqueue_fused_step();
   void launch_fused_step(int seq_len);
   DecodeStepArgs step_args(int splits) const;
@@ -224,6 +224,9 @@ class Model {
   int32_t* sampled_id_ = nullptr;
   // Fused decode state.
   float* resid_ = nullptr;        // [hidden] fp32 residual sum
+  // The fused step's state on the device, {token, position, want_host_id}:
+  // one copy per call from pinned_state_. position_dev_ points into it.
+  int32_t* step_state_ = nullptr;
   int32_t* position_dev_ = nullptr;
   unsigned long long* argmax_partials_ = nullptr;
   int32_t* history_ = nullptr;    // [max_seq + 1]
@@ -245,7 +248,7 @@ class Model {
   bool exchange_oproj_ = false;
   int exchange_split_slots_ = 0;  // 0: split attention keeps separate kernels
   uint32_t* epoch_ = nullptr;     // [1] decode steps completed (exchange tags)
-  int32_t* pinned_state_ = nullptr;  // host {token, position}
+  int32_t* pinned_state_ = nullptr;  // host {token, position, want_host_id}
 
   // A captured graph and its executable, destroyed together: the graph is
   // kept for as long as the executable made from it.

@@ -1005,7 +1005,8 @@ __global__ __launch_bounds__(kLmHeadWaves * 64) void lm_head_kernel(DecodeStepAr
   // kFold: the epoch read here tags the words and is advanced at the end
   // without a second read. (Reading the position here as well measured 10 us
   // slower per step: it moved the register allocation of the streaming loop
-  // below, which then drained its loads every iteration.)
+  // below, and the compiler then placed a wait for every load in flight
+  // inside that loop.)
   uint32_t tag = 0, epoch0 = 0;
   if constexpr (kFold) {
     epoch0 = *a.epoch;

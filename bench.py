@@ -293,7 +293,7 @@ SAMPLING_T, SAMPLING_TOP_K, SAMPLING_TOP_P = 0.8, 40, 0.95
 SAMPLING_UNIFORM_SEED = 20260904
 
 
-def sampling_run(lcr, config: dict, prompt_len: int = 512, steps: int = 256) -> dict:
+def sampling_run(lcr, config: dict, prompt_len: int = 512, steps: int = 256, eager: bool = False) -> dict:
     """the fp16 build, a paged cache of 16-token
     pages, a seeded 512-token prompt (MFMA prefill), then `steps` tokens
     sampled at temperature 0.8, top-k 40, top-p 0.95 with one Philox uniform
@@ -305,12 +305,14 @@ def sampling_run(lcr, config: dict, prompt_len: int = 512, steps: int = 256) -> 
         the prefill's logits on the host, then steps - 1 captured
         decode + sample steps), timed with hipEvents on the model's stream,
         as config 2's greedy loop is. This one is `tok_s`.
-    One untimed pass of each first."""
+    One untimed pass of each first. `eager` enqueues each step's kernels
+    instead of replaying the captured graph (for a kernel trace)."""
     cfg16 = lcr.llama_config(torch_dtype="float16")
     d = checkpoint_dir(lcr, cfg16, lcr.WEIGHT_SEED, fp16=True, variant="fp16")
     prompt = lcr.synthetic_tokens(prompt_len, config["vocab_size"], seed=lcr.PROMPT_SEED, variant="fp16")
     uniforms = lcr.philox_uniforms(SAMPLING_UNIFORM_SEED, steps)
-    m = lcr.Model(d, variant="fp16", max_seq=prompt_len + steps + 1, paged=1, page_size=16)
+    m = lcr.Model(d, variant="fp16", max_seq=prompt_len + steps + 1, paged=1, page_size=16,
+                  use_graph=0 if eager else 1)
 
     def run():
         ptr = m.prefill(prompt)
@@ -501,8 +503,8 @@ def main() -> int:
                     help="only the prefill and the timed graph-replayed decode steps, for a kernel trace "
                          "in which every decode kernel is an in-step dispatch")
     ap.add_argument("--eager", action="store_true",
-                    help="with --decode-only or --long-context: enqueue each step's kernels directly instead of "
-                         "replaying the captured graph (the kernels and their order are the same)")
+                    help="with --decode-only, --long-context or --sampling: enqueue each step's kernels directly "
+                         "instead of replaying the captured graph (the kernels and their order are the same)")
     ap.add_argument("--no-exchange", action="store_true",
                     help="run the decode step's q/k/v projection and attention as two kernels instead of "
                          "the exchange grid (for comparison)")
@@ -528,7 +530,7 @@ def main() -> int:
         if lcr.device_count("fp16") < 1:
             print("no HIP device visible", file=sys.stderr)
             return 1
-        print(json.dumps({"sampling_config5": sampling_run(lcr, config)}))
+        print(json.dumps({"sampling_config5": sampling_run(lcr, config, eager=args.eager)}))
         return 0
     if lcr.device_count() < 1:
         print("no HIP device visible", file=sys.stderr)

@@ -78,9 +78,18 @@ __device__ __forceinline__ int wave_sum_int(int v) {
 
 // The maximum logit from the argmax blocks' partial keys (exact in any
 // order): the value half of the largest key. Every lane of the wave gets it.
+// The first 256 keys are all requested before any is compared (a loop would
+// wait for each load before issuing the next); indices past the last key
+// read the last key again, which leaves the maximum unchanged and keeps the
+// loads unconditional (blocks >= 1).
 __device__ __forceinline__ float max_from_keys(const unsigned long long* __restrict__ block_best, int blocks) {
-  unsigned long long key = 0;
-  for (int b = lane_id(); b < blocks; b += 64) key = umax64(key, block_best[b]);
+  constexpr int kAtOnce = 4;
+  const int lane = lane_id();
+  unsigned long long first[kAtOnce];
+#pragma unroll
+  for (int j = 0; j < kAtOnce; ++j) first[j] = block_best[min(lane + 64 * j, blocks - 1)];
+  unsigned long long key = umax64(umax64(first[0], first[1]), umax64(first[2], first[3]));
+  for (int b = lane + 64 * kAtOnce; b < blocks; b += 64) key = umax64(key, block_best[b]);
   key = wave_max_u64(key);
   const uint32_t k = static_cast<uint32_t>(key >> 32);
   return u32_as_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);

@@ -270,6 +270,7 @@ void Model::allocate_arena() {
 void Model::reset() {
   position_ = 0;
   step_argmax_ready_ = false;
+  step_state_current_ = false;
   taps_.clear();
 }
 
@@ -311,6 +312,7 @@ const float* Model::prefill(const std::vector<int>& tokens) {
               "token id " << t << " is outside the vocabulary of " << config_.vocab_size);
   }
   step_argmax_ready_ = false;
+  step_state_current_ = false;
   if (options_.prefill_via_decode) {
     GpuTimer timer;
     timer.start(stream_);
@@ -491,11 +493,16 @@ const float* Model::decode(int token) {
             "token id " << token << " is outside the vocabulary of " << config_.vocab_size);
   step_argmax_ready_ = false;
   const bool fused_step = fused_ && !capture_activations_;
+  // The previous fused step left this token, this position and the host-id
+  // flag in the step state (the reference's greedy loop feeds the argmax
+  // back): no copy.
+  const bool state_current = fused_step && step_state_current_ && token == device_token_;
+  step_state_current_ = false;
   GpuTimer timer;
   timer.start(stream_);
   kv_cache_->reserve_length(position_ + 1);
   if (fused_step) {
-    write_step_state(token, true);
+    if (!state_current) write_step_state(token, true);
     launch_fused_step(position_ + 1);
   } else {
     pinned_state_[0] = token;
@@ -510,6 +517,10 @@ const float* Model::decode(int token) {
   stats_.last_decode_ms = timer.elapsed_ms();
   check_exchange();
   step_argmax_ready_ = fused_step;
+  if (fused_step) {
+    device_token_ = __atomic_load_n(step_id_host_, __ATOMIC_ACQUIRE);
+    step_state_current_ = true;
+  }
   if (profiler_.enabled()) profiler_.collect();
   return logits_;
 }
@@ -548,6 +559,7 @@ std::vector<int> Model::generate_sampled(int first_token, int steps, float tempe
                                          float top_p, const float* uniforms, double* elapsed_ms) {
   LCR_CHECK(fused_, "device-side sampled generation needs the fused decode path");
   step_argmax_ready_ = false;
+  step_state_current_ = false;
   LCR_CHECK(steps >= 0, "steps must be non-negative");
   LCR_CHECK(temperature > 0.0f, "sampled generation needs a positive temperature (greedy: generate_greedy)");
   LCR_CHECK(top_p > 0.0f && top_p <= 1.0f, "top_p must be in (0, 1], got " << top_p);
@@ -607,6 +619,7 @@ std::vector<int> Model::generate_sampled(int first_token, int steps, float tempe
 std::vector<int> Model::generate_greedy(int first_token, int steps, double* elapsed_ms) {
   LCR_CHECK(fused_, "device-side greedy generation needs the fused decode path");
   step_argmax_ready_ = false;
+  step_state_current_ = false;
   LCR_CHECK(steps >= 0, "steps must be non-negative");
   LCR_CHECK(first_token >= 0 && first_token < config_.vocab_size,
             "token id " << first_token << " is outside the vocabulary of " << config_.vocab_size);
@@ -651,6 +664,7 @@ double Model::time_decode_kernel(const std::string& kernel, int launches,
                                  double* bytes_per_launch) {
   LCR_CHECK(fused_, "kernel timing needs the fused decode path");
   step_argmax_ready_ = false;
+  step_state_current_ = false;
   LCR_CHECK(launches > 0, "launches must be positive");
   LCR_CHECK(position_ > 0, "time kernels after a prefill, so the step state is valid");
   const double H = config_.hidden_size, F = config_.intermediate_size, V = config_.vocab_size;
@@ -772,6 +786,7 @@ void Model::set_position(int position) {
             "position " << position << " outside [0, " << options_.max_seq << "]");
   kv_cache_->reserve_length(position);
   position_ = position;
+  step_state_current_ = false;
 }
 
 void Model::fill_kv_normal(uint64_t seed, float stddev) {

@@ -289,6 +289,13 @@ class Model {
   // the id to host-coherent memory too, or a greedy sample() of logits_. A
   // greedy sample() of logits_ then reads that id: no kernel, no copy.
   bool step_argmax_ready_ = false;
+  // step_state_ on the device holds {device_token_, position_, 1}: the last
+  // call was a fused decode(), whose step wrote its argmax as the next token
+  // and advanced the position, and nothing has moved the position since. A
+  // decode() of that token then has nothing to copy. Cleared by every call
+  // that writes the position or the step state.
+  bool step_state_current_ = false;
+  int32_t device_token_ = -1;
   std::vector<Tap> taps_;
   Profiler profiler_;
 };

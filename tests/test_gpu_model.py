@@ -132,6 +132,58 @@ def test_decode_bit_exact_other_geometries(lcr, tmp_path_factory, geometry, page
         o.close()
 
 
+def test_decode_copies_its_state_unless_the_last_step_left_it(lcr, small_ckpt):
+    """decode() leaves out its copy of {token, position} to the device when
+    the previous fused step left exactly that there: its argmax fed back, at
+    the position it advanced to. Every call in between that moves the
+    position or writes the step state (another token, set_position,
+    generate_greedy, reset and prefill) makes the next decode() copy again,
+    and a stochastic sample() changes neither. The logits stay bit-identical
+    to the oracle's through every kind of call."""
+    m, o = make_pair(lcr, small_ckpt, prefill_via_decode=1)
+    prompt = lcr.synthetic_tokens(20, m.vocab, seed=31)
+    lo = o.prefill(prompt, use_decode_path=True)
+    expect_bits_equal(m.logits(m.prefill(prompt)).view(np.uint32), lo.view(np.uint32), "prompt logits")
+
+    def step(tok, what):
+        ptr = m.decode(tok)
+        lo = o.decode(tok)
+        expect_bits_equal(m.logits(ptr).view(np.uint32), lo.view(np.uint32), what)
+        return ptr, oracle.argmax(lo)
+
+    ptr, tok = step(oracle.argmax(lo), "the prompt's argmax fed back")
+    ptr, tok = step(int(prompt[0]), "a prompt token")
+    for i in range(3):
+        ptr, tok = step(tok, f"argmax fed back {i}")
+    drawn = m.sample(ptr, 0.8, 40, 0.95, 0.42)
+    assert 0 <= drawn < m.vocab
+    ptr, tok = step(tok, "argmax fed back after a stochastic sample")
+    ptr, tok = step((tok + 7) % m.vocab, "another token")
+    ptr, tok = step(tok, "argmax fed back after another token")
+    back = m.position - 2
+    m.set_position(back)
+    o.set_position(back)
+    ptr, tok = step(tok, "the same token after set_position")
+    ptr, tok = step(tok, "argmax fed back after set_position")
+    ids, _ = m.generate_greedy(tok, 3)
+    want = []
+    for _ in range(3):
+        lo = o.decode(tok)
+        tok = oracle.argmax(lo)
+        want.append(tok)
+    assert [int(x) for x in ids] == want
+    ptr, tok = step(tok, "the last generated id after generate_greedy")
+    ptr, tok = step(tok, "argmax fed back after generate_greedy")
+    m.reset()
+    o.reset()
+    expect_bits_equal(m.logits(m.prefill(prompt[:5])).view(np.uint32),
+                      o.prefill(prompt[:5], use_decode_path=True).view(np.uint32), "prompt logits after reset")
+    ptr, tok = step(tok, "an earlier argmax after reset and prefill")
+    ptr, tok = step(tok, "argmax fed back after reset")
+    m.close()
+    o.close()
+
+
 def test_greedy_sample_after_each_kind_of_call(lcr, small_ckpt):
     """sample(logits, 0) returns the argmax of the logits (lowest index on
     ties) whichever call wrote them: an MFMA prefill (the sampler's own

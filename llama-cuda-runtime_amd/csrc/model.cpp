@@ -341,6 +341,7 @@ const float* Model::prefill(const std::vector<int>& tokens) {
     launch_embedding_lookup(x_, embedding_, token_ids_, chunk, config_.hidden_size, stream_);
     run_layers(chunk, position_);
     step_argmax_ready_ = false;  // the chunk's logits, without their argmax
+    step_state_current_ = false;
     position_ += chunk;
     consumed += static_cast<size_t>(chunk);
     // The ids buffer above is pageable host memory read by the async copy.

@@ -323,6 +323,35 @@ def test_activation_taps_match_oracle(lcr, small_ckpt):
         expect_bits_equal(taps[name].view(np.uint32), o2.tap(i, 1).view(np.uint32), f"decode tap {name}")
 
 
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("graph", [1, 0])
+def test_decode_to_the_cache_limit(lcr, small_ckpt, paged, graph):
+    """The cache's last positions: max_seq 70 (with 16-token pages the last
+    page is partly used), a 60-token prompt, then greedy steps until the
+    cache is full, every step's logits bit-identical to the oracle's; one
+    more step is an error, as is a device loop that would pass the limit.
+    A device loop that ends exactly at the limit gives the host loop's ids."""
+    max_seq = 70
+    opts = dict(paged=int(paged), page_size=16, prefill_via_decode=1, use_graph=graph)
+    m, o = make_pair(lcr, small_ckpt, max_seq=max_seq, paged=paged)
+    m.close()
+    m = lcr.Model(small_ckpt, max_seq=max_seq, **opts)
+    prompt = lcr.synthetic_tokens(60, m.vocab, seed=41)
+    ids = run_steps(m, o, prompt, max_seq - len(prompt))
+    assert m.position == max_seq
+    with pytest.raises(lcr.LcrError, match="cache limit"):
+        m.decode(1)
+    m.reset()
+    tok = m.sample(m.prefill(prompt), 0.0)
+    with pytest.raises(lcr.LcrError, match="exceeds the cache"):
+        m.generate_greedy(tok, max_seq - len(prompt) + 1)
+    got, _ = m.generate_greedy(tok, max_seq - len(prompt))
+    assert [tok] + [int(x) for x in got[:-1]] == ids
+    assert m.position == max_seq
+    m.close()
+    o.close()
+
+
 def test_model_errors(lcr, small_ckpt):
     m = lcr.Model(small_ckpt, max_seq=8)
     with pytest.raises(lcr.LcrError, match="exceeds the cache"):

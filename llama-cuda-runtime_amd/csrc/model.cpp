@@ -30,6 +30,7 @@ Model::Model(const std::string& model_dir, const Options& options) : options_(op
   max_tokens_ = std::min(options_.prefill_chunk, options_.max_seq);
 
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  decode_timer_ = std::make_unique<GpuTimer>();
 
   {
     const SafetensorsArchive archive(model_dir);
@@ -499,7 +500,7 @@ const float* Model::decode(int token) {
   // back): no copy.
   const bool state_current = fused_step && step_state_current_ && token == device_token_;
   step_state_current_ = false;
-  GpuTimer timer;
+  GpuTimer& timer = *decode_timer_;
   timer.start(stream_);
   kv_cache_->reserve_length(position_ + 1);
   if (fused_step) {

@@ -22,6 +22,7 @@
 
 #include "arena.h"
 #include "config.h"
+#include "hip_utils.h"
 #include "kv_cache.h"
 #include "kernels/decode_step.h"
 #include "profiler.h"
@@ -194,6 +195,9 @@ class Model {
   int multiprocessors_ = 0;
   bool fused_ = false;
   hipStream_t stream_ = nullptr;
+  // decode()'s timer, whose two events are created once with the model (on
+  // its device) rather than per call.
+  std::unique_ptr<GpuTimer> decode_timer_;
 
   elem_t* weight_block_ = nullptr;
   size_t weight_bytes_ = 0;

@@ -47,10 +47,6 @@ __device__ __forceinline__ float block_sum_1024(float v, float* lds32) {
   return total;
 }
 
-__device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
-  return va > vb || (va == vb && ia < ib);
-}
-
 
 // Inclusive prefix sum over the 64 lanes of a wave (integers: exact in any
 // order), on DPP: within each row of 16 lanes by shifts of 1, 2, 4 and 8
@@ -349,17 +345,39 @@ __device__ __forceinline__ T xor_lane_step(T v, int step) {
   return __builtin_bit_cast(T, r);
 }
 
-// One compare-exchange step of the bitonic sort with the element of thread
-// t ^ step: thread t keeps the element that ranks first when it is the lower
-// of the pair in an ascending run (or the upper in a descending one), else
-// the other, which is the swap of the pairwise formulation.
-__device__ __forceinline__ void bitonic_keep(float& v, int& i, float pv, int pi, int t, int span, int step) {
+// A candidate's place in the order (value desc, index asc) as one unsigned
+// 64-bit key: the argmax key of sampling.h (order-preserving value bits over
+// the complemented index), with -0 taken as +0 so that equal values tie on
+// the index alone (both weigh exp(0) = 1). The key round-trips the value and
+// the index. Empty places hold 0, below every candidate; NaN values have no
+// defined place.
+__device__ __forceinline__ unsigned long long cand_key(float v, int idx) {
+  return argmax_key(v == 0.0f ? 0.0f : v, static_cast<uint32_t>(idx));
+}
+
+__device__ __forceinline__ float key_value(unsigned long long key) {
+  const uint32_t k = static_cast<uint32_t>(key >> 32);
+  return u32_as_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ int key_index(unsigned long long key) {
+  return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key));
+}
+
+__device__ __forceinline__ unsigned long long xor_lane_key(unsigned long long key, int step) {
+  const uint32_t lo = xor_lane_step(static_cast<uint32_t>(key), step);
+  const uint32_t hi = xor_lane_step(static_cast<uint32_t>(key >> 32), step);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+// One compare-exchange step of the bitonic sort with the key of thread
+// t ^ step: thread t keeps the key that ranks first when it is the lower of
+// the pair in an ascending run (or the upper in a descending one), else the
+// other, which is the swap of the pairwise formulation.
+__device__ __forceinline__ void bitonic_keep(unsigned long long& key, unsigned long long partner, int t, int span,
+                                             int step) {
   const bool keep_first = ((t & step) == 0) == ((t & span) == 0);
-  const bool partner_first = ranks_before(pv, pi, v, i);
-  if (keep_first == partner_first) {
-    v = pv;
-    i = pi;
-  }
+  if (keep_first == (partner > key)) key = partner;
 }
 
 // Steps 1-2's totals and 4-6 after sample_compact_kernel, in one 1024-thread
@@ -387,6 +405,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
   __shared__ float values[kMaxCandidates];
   __shared__ int indices[kMaxCandidates];
   __shared__ float weights[kMaxCandidates];
+  __shared__ unsigned long long keys[kMaxCandidates];
   __shared__ StepValues shared_step;
   const int t = threadIdx.x;
   const int lane = lane_id();
@@ -451,7 +470,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
     idx = cand_indices[at];
   }
 
-  // 5. Order (value desc, index asc), one element per thread.
+  // 5. Order (value desc, index asc), one key per thread.
+  unsigned long long key = t < found ? cand_key(v, idx) : 0ull;
   if (top_k > 0 && top_k <= 64) {
     // The walk reads only the first top_k: the best 64 in order suffice. Each
     // wave sorts its 64 (best at lane 0); then four levels merge the waves'
@@ -464,24 +484,18 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
     for (int span = 2; span <= 64; span <<= 1) {
 #pragma unroll
       for (int step = span >> 1; step > 0; step >>= 1) {
-        bitonic_keep(v, idx, xor_lane_step(v, step), xor_lane_step(idx, step), lane, span, step);
+        bitonic_keep(key, xor_lane_key(key, step), lane, span, step);
       }
     }
     for (int lists = kSampleThreads / 64; lists > 1; lists >>= 1) {
-      values[t] = v;
-      indices[t] = idx;
+      keys[t] = key;
       __syncthreads();
       if (wave < lists / 2) {
-        const int other = (wave + lists / 2) * 64 + 63 - lane;
-        const float ov = values[other];
-        const int oi = indices[other];
-        if (ranks_before(ov, oi, v, idx)) {
-          v = ov;
-          idx = oi;
-        }
+        const unsigned long long other = keys[(wave + lists / 2) * 64 + 63 - lane];
+        if (other > key) key = other;
 #pragma unroll
         for (int step = 32; step > 0; step >>= 1) {
-          bitonic_keep(v, idx, xor_lane_step(v, step), xor_lane_step(idx, step), lane, 64, step);
+          bitonic_keep(key, xor_lane_key(key, step), lane, 64, step);
         }
       }
       __syncthreads();
@@ -494,7 +508,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
     // the pick (the first kept rank whose prefix reaches the target) are the
     // lowest set bits of two ballots.
     if (wave == 0) {
-      const float weight = t < found ? lcr_expf(v) : 0.0f;
+      const float weight = t < found ? lcr_expf(key_value(key)) : 0.0f;
       const int limit = min(found, top_k);
       const float inv_total = 1.0f / total_sum;
       float chain = 0.0f, prefix = 0.0f;
@@ -513,31 +527,30 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(int32_t* __restr
       const float target = sv.u * kept_mass;
       const unsigned long long hit = __ballot(lane < keep && prefix >= target);
       const int rank = hit != 0 ? __ffsll(hit) - 1 : keep - 1;
-      const int picked = __builtin_amdgcn_readlane(idx, rank);
+      const int picked = __builtin_amdgcn_readlane(key_index(key), rank);
       if (t == 0) finish_sample(out_id, picked, sv, step);
     }
     return;
-  } else {
-    // Bitonic sort of all candidates.
-    for (int span = 2; span <= kMaxCandidates; span <<= 1) {
-      for (int step = span >> 1; step > 0; step >>= 1) {
-        float pv;
-        int pi;
-        if (step < 64) {
-          pv = __shfl_xor(v, step, 64);
-          pi = __shfl_xor(idx, step, 64);
-        } else {
-          values[t] = v;
-          indices[t] = idx;
-          __syncthreads();
-          pv = values[t ^ step];
-          pi = indices[t ^ step];
-          __syncthreads();
-        }
-        bitonic_keep(v, idx, pv, pi, t, span, step);
+  }
+  // Bitonic sort of all candidates.
+  for (int span = 2; span <= kMaxCandidates; span <<= 1) {
+    for (int step = span >> 1; step > 0; step >>= 1) {
+      unsigned long long partner;
+      if (step < 64) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(key), step, 64);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(key >> 32), step, 64);
+        partner = (static_cast<unsigned long long>(hi) << 32) | lo;
+      } else {
+        keys[t] = key;
+        __syncthreads();
+        partner = keys[t ^ step];
+        __syncthreads();
       }
+      bitonic_keep(key, partner, t, span, step);
     }
   }
+  v = key_value(key);
+  idx = key_index(key);
   values[t] = v;
   indices[t] = idx;
   // The walk's terms, every one computed once (the same values the walk's

@@ -44,8 +44,11 @@ def test_fp16_paged_stochastic_sampling_matches_oracle(lcr, fp16_ckpt):
                              multiprocessors=m.stats().multiprocessors)
     ptr = m.prefill(prompt)
     want = ref.prefill(prompt, use_decode_path=True)
+    print(f"[sampling/decode path] prompt of {PROMPT} done on the oracle", flush=True)
     tokens = []
     for step in range(STEPS):
+        if step % 64 == 0:
+            print(f"[sampling/decode path] step {step} of {STEPS}", flush=True)
         got = m.logits(ptr)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"logits differ at step {step}"
         u = uniforms[step]
@@ -79,6 +82,7 @@ def test_fp16_mfma_prefill_then_sampling_matches_oracle_on_exported_cache(lcr, f
     ptr = m.prefill(prompt)
     got = m.logits(ptr)
     want = ref.prefill(prompt)
+    print(f"[sampling/mfma prefill] prompt of {PROMPT} done on the oracle", flush=True)
     dr = drift(got, want)
     assert dr["rel_rms"] <= 0.02 and dr["cosine"] >= 0.999, dr
     tok = m.sample(ptr, T, TOP_K, TOP_P, uniforms[0])
@@ -89,6 +93,8 @@ def test_fp16_mfma_prefill_then_sampling_matches_oracle_on_exported_cache(lcr, f
     ref.set_position(PROMPT)
     tokens = [tok]
     for step in range(1, STEPS):
+        if step % 64 == 0:
+            print(f"[sampling/mfma prefill] step {step} of {STEPS}", flush=True)
         ptr = m.decode(tok)
         want = ref.decode(tok)
         got = m.logits(ptr)
